@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path (one GPU), printing ONE JSON line.
+
+Headline (BASELINE.json metric, config C2): decode attention for 1 sequence / 1 token at context
+32768 (16 query heads, 2 KV heads, head_dim 256, f16 KV cache [2][32768][256], N(0,1) synthetic
+inputs), split-K over the KV length + LSE merge x sigmoid gate. A step = one decode call
+(split + combine kernels) over one KV cache; `value` = algorithmic KV bytes (67,108,864 B per
+step) / measured time, in GB/s. The inputs are resident in HBM; steps rotate over 6 distinct KV
+caches (384 MiB > the 256 MiB Infinity Cache) so every step streams from HBM.
+
+Also reported:
+  roofline      the split kernel (dominant) timed alone with HIP events on its stream:
+                algorithmic bytes / average launch time vs the 8 TB/s HBM peak; `traffic` is the
+                HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/), or null.
+  prefill       C4: 8192 new tokens after an 8192-token prefix, causal, f16 MFMA; TFLOP/s over
+                the unmasked (query, key) pairs (1.6493e12 FLOP) vs the 2516.6 TFLOP/s f16 peak.
+  cpu_baseline  the FP64 oracle (a C restatement of the reference's host scalar attention) on a
+                bounded sample of the same workload on this host's CPU, rank 0 only.
+
+Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
+per-launch cost does not throttle a ~10 us step; the kernels are the same ones the C ABI
+launches eagerly.
+
+    python bench.py [--gpus 1] [--steps 60] [--warmup 12]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+H, KV, D = 16, 2, 256
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2516.6
+METRIC = "decode-attn HBM GB/s @32k ctx; prefill-attn TFLOP/s @8k; % of roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=60)
+    ap.add_argument("--warmup", type=int, default=12)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--buffers", type=int, default=6)
+    ap.add_argument("--max-splits", type=int, default=128)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    return ap.parse_args()
+
+
+def graph_of(torch, fn, count):
+    """Record `count` calls fn(i) into a HIP graph (after one eager warm call per i)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(count):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(count):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_replays(torch, g, reps):
+    """Wall and event time of `reps` replays of g on the current stream (ms total)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
+
+def traffic_from_profiles(name):
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_decode(torch, A, args):
+    L, R = args.ctx, args.buffers
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(L)
+    q = torch.randn(H * D, generator=gen, device="cuda")
+    qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
+    caches = []
+    for _ in range(R):
+        k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+        v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+        caches.append((k, v))
+    sc = A.DecodeScratch(args.max_splits)
+    n_splits = A.attn_n_splits(L, args.max_splits)
+    core = torch.empty(H * D, device="cuda")
+    kv_bytes = 2 * KV * L * D * 2
+
+    def step(i):
+        k, v = caches[i % R]
+        A.attn_decode(q, qg, k, v, core, sc, L, L, n_splits)
+
+    def split_only(i):
+        k, v = caches[i % R]
+        A.attn_split(q, k, v, sc.part_m, sc.part_l, sc.part_o, L, L, n_splits)
+
+    def combine_only(i):
+        A.attn_combine(sc.part_m, sc.part_l, sc.part_o, qg, core, n_splits)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    reps = max(1, (args.steps + R - 1) // R)
+    steps = reps * R
+    g_step = graph_of(torch, step, R)
+    g_split = graph_of(torch, split_only, R)
+    g_comb = graph_of(torch, combine_only, R)
+    time_replays(torch, g_step, 2)  # warm the graph path
+    ms_step, wall_step = time_replays(torch, g_step, reps)
+    ms_split, _ = time_replays(torch, g_split, reps)
+    ms_comb, _ = time_replays(torch, g_comb, reps)
+    t_step = ms_step / steps
+    t_split = ms_split / steps
+    t_comb = ms_comb / steps
+    log(f"decode C2: step {t_step * 1e3:.2f} us (wall {wall_step / steps * 1e3:.2f} us), "
+        f"split {t_split * 1e3:.2f} us, combine {t_comb * 1e3:.2f} us, n_splits {n_splits}")
+    host = {
+        "q": q.cpu().numpy(), "qg": qg.cpu().numpy(),
+        "k": caches[0][0].view(torch.int16).cpu().numpy().view("uint16"),
+        "v": caches[0][1].view(torch.int16).cpu().numpy().view("uint16"),
+    }
+    return {
+        "steps": steps, "t_step_ms": t_step, "t_split_ms": t_split, "t_comb_ms": t_comb,
+        "kv_bytes": kv_bytes, "n_splits": n_splits, "host": host, "L": L,
+    }
+
+
+def bench_prefill(torch, A, args):
+    pos0, n = 8192, 8192
+    max_ctx = pos0 + n
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(max_ctx)
+    q = torch.randn(n * H * D, generator=gen, device="cuda")
+    qg = torch.randn(n * H * 2 * D, generator=gen, device="cuda")
+    k = torch.randn(KV * max_ctx * D, generator=gen, device="cuda").half()
+    v = torch.randn(KV * max_ctx * D, generator=gen, device="cuda").half()
+    core = torch.empty(n * H * D, device="cuda")
+
+    def call(_):
+        A.attn_prefill(q, qg, k, v, core, pos0, n, max_ctx)
+
+    call(0)
+    torch.cuda.synchronize()
+    g = graph_of(torch, call, 1)
+    time_replays(torch, g, 1)
+    ms, _ = time_replays(torch, g, args.prefill_steps)
+    t = ms / args.prefill_steps
+    pairs = n * pos0 + n * (n + 1) // 2
+    flop = 4.0 * H * D * pairs
+    tflops = flop / (t * 1e-3) / 1e12
+    log(f"prefill C4: {t:.3f} ms, {tflops:.1f} TFLOP/s")
+    host = None
+    if not args.no_cpu:
+        host = {
+            "q": q.cpu().numpy(), "qg": qg.cpu().numpy(),
+            "k": k.view(torch.int16).cpu().numpy().view("uint16"),
+            "v": v.view(torch.int16).cpu().numpy().view("uint16"),
+        }
+    return {"t_ms": t, "flop": flop, "tflops": tflops, "pos0": pos0, "n": n,
+            "max_ctx": max_ctx, "host": host}
+
+
+def cpu_decode_baseline(dec):
+    """FP64 oracle, single thread, on full C2 calls over the bench's first KV cache; about
+    10 s of CPU work."""
+    from oracle import oracle as O
+    h, L = dec["host"], dec["L"]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.decode_f64(h["q"], h["qg"], h["k"], h["v"], L, L, threads=1)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= 10.0 or reps >= 40:
+            break
+    return {
+        "value": dec["kv_bytes"] * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"C2 decode (ctx 32768): {reps} full FP64 oracle calls on KV cache 0, "
+                  f"{el:.1f} s, single thread",
+        "ms_per_call": el / reps * 1e3,
+    }
+
+
+def cpu_prefill_baseline(pre):
+    """FP64 oracle on a deterministic sample of C4 query rows (16 heads each), 16 threads."""
+    import numpy as np
+    from oracle import oracle as O
+    h = pre["host"]
+    rows = np.linspace(0, pre["n"] - 1, 48).astype(np.uint32)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    O.prefill_f64(h["q"], h["qg"], H * 2 * D, h["k"], h["v"], pre["pos0"], pre["max_ctx"], rows,
+                  threads=threads)
+    el = time.perf_counter() - t0
+    flop = float(sum(4.0 * H * D * (pre["pos0"] + int(t) + 1) for t in rows))
+    return {"value": flop / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"C4 prefill: {rows.size} query rows x 16 heads of the FP64 oracle, "
+                      f"{el:.1f} s on {threads} threads"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (the attention path runs on a single "
+              f"MI355X; multi-GPU sharding is a design note, not a bench line). Got --gpus "
+              f"{args.gpus}, WORLD_SIZE {world}.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from miso_amd import attention as A
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    dec = bench_decode(torch, A, args)
+    pre = None if args.no_prefill else bench_prefill(torch, A, args)
+
+    value = dec["kv_bytes"] / (dec["t_step_ms"] * 1e-3) / 1e9
+    split_gbs = dec["kv_bytes"] / (dec["t_split_ms"] * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": dec["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["t_step_ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: decode attention, 1 sequence x 1 token, ctx 32768, 16Q/2KV heads, "
+                        "head_dim 256, f16 KV [2][32768][256], split-K + LSE merge x sigmoid gate",
+            "ctx": dec["L"], "n_splits": dec["n_splits"], "kv_buffers_rotated": args.buffers,
+            "step": "split kernel + combine kernel (one decode call)",
+            "algorithmic_bytes_per_step": dec["kv_bytes"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_split_kernel<256>",
+            "achieved": round(split_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(split_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("decode_c2"),
+            "avg_launch_us": round(dec["t_split_ms"] * 1e3, 3),
+            "combine_avg_launch_us": round(dec["t_comb_ms"] * 1e3, 3),
+            "step_frac": round(value / HBM_PEAK_GBS, 4),
+        },
+    }
+    if pre is not None:
+        out["prefill"] = {
+            "workload": "C4: causal prefill, 8192 tokens after an 8192-token prefix (16384 keys), "
+                        "16Q/2KV, head_dim 256, f16 MFMA, f32 softmax/accumulate",
+            "value": round(pre["tflops"], 2), "unit": "TFLOP/s", "ms_per_call": round(pre["t_ms"], 4),
+            "algorithmic_flop": pre["flop"],
+            "roofline": {"bound": "mfma", "kernel": "attn_prefill_kernel<256>",
+                         "achieved": round(pre["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                         "traffic": traffic_from_profiles("prefill_c4")},
+        }
+    if not args.no_cpu:
+        log("cpu baseline (decode) ...")
+        out["cpu_baseline"] = cpu_decode_baseline(dec)
+        if pre is not None and pre["host"] is not None:
+            log("cpu baseline (prefill sample) ...")
+            out["prefill"]["cpu_baseline"] = cpu_prefill_baseline(pre)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * miso_attn.h -- C ABI of the MI355X (gfx950) gated GQA softmax-attention library
+ * (libmiso_attn.so).
+ *
+ * Every entry point launches the same kernels the C++ header API instantiates
+ * (miso_amd/kernels/attention_decode.hpp, attention_prefill.hpp); the C ABI is the boundary a
+ * non-C++ caller (ctypes, cgo, JNI) binds. Reference citations are relative to the reference
+ * repository (penta2himajin/miso).
+ *
+ * Conventions
+ *   - Pointers are device pointers (hipMalloc'd or equivalent), 16-byte aligned.
+ *   - f16 buffers hold IEEE binary16 bit patterns (uint16_t).
+ *   - Shapes are fixed by the model: 16 query heads, 2 KV heads, head_dim 256; the KV cache is
+ *     [2][max_ctx][256] per tensor (K and V separate).
+ *   - stream: a hipStream_t, or NULL for the null stream. Calls only enqueue; nothing
+ *     synchronises the host.
+ *   - Return value: 0 on success. A non-zero value is either a hipError_t from the launch or
+ *     MISO_ATTN_EINVAL for arguments rejected on the host before any launch; the message is then
+ *     available from miso_attn_last_error() (thread-local). The reference throws
+ *     std::runtime_error in both situations (src/hip_util.hpp:12-17, src/engine/attention.hip:
+ *     164-165, 203-204).
+ */
+#ifndef MISO_ATTN_H
+#define MISO_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MISO_ATTN_EINVAL 0x4D41 /* host-side argument validation failed */
+
+/* Message of the last failure on this thread ("" if none). */
+const char* miso_attn_last_error(void);
+
+/* Library / kernel-set version string. */
+const char* miso_attn_version(void);
+
+/* Split-count policy: replaces attn_n_splits(len, max_splits), kernels/attention_decode.hpp:92,
+ * as used by src/engine/attention.hip:185. Returns 1 <= n <= max(max_splits, 1); 1 for len 0.
+ * The MI355X policy differs from the reference's MI50 tuning (same contract). */
+uint32_t miso_attn_n_splits(uint32_t len, uint32_t max_splits);
+
+/* Prefill grid size: replaces attn_prefill_items(n), kernels/attention_prefill.hpp:54. */
+uint32_t miso_attn_prefill_items(uint32_t n);
+
+/* Decode prep: replaces attn_prep_kernel<256><<<18, 256, 0, stream>>>(AttnPrepParams{...}),
+ * src/engine/attention.hip:180-183 (kernels/attention_decode.hpp:19-83). Per-head RMSNorm of the
+ * 16 query heads (qg, gate half untouched) and 2 key heads, NEOX RoPE on dims [0, 64) at `pos`,
+ * writes q [16][256] and appends K/V at position pos of the caches. Rejects pos >= max_ctx. */
+int miso_attn_prep(const float* qg, const float* k, const float* v, const float* q_norm,
+                   const float* k_norm, const float* inv_freq, uint16_t* k_cache,
+                   uint16_t* v_cache, float* q, uint32_t pos, uint32_t max_ctx, float eps,
+                   void* stream);
+
+/* Batched prep for n tokens: replaces attn_prep_batch_kernel<256><<<n * 18, 256, 0, stream>>>,
+ * src/engine/attention.hip:218-223 (kernels/attention_prefill.hpp:20-40). Token t reads qg/k/v
+ * at t * proj_stride floats, writes q at t * 4096 floats and the cache at pos0 + t.
+ * Rejects pos0 + n > max_ctx. */
+int miso_attn_prep_batch(const float* qg, const float* k, const float* v, const float* q_norm,
+                         const float* k_norm, const float* inv_freq, uint16_t* k_cache,
+                         uint16_t* v_cache, float* q, uint32_t pos0, uint32_t max_ctx, float eps,
+                         uint32_t n, uint32_t proj_stride, void* stream);
+
+/* Split-K partials: replaces attn_split_kernel<256><<<dim3(n_splits, 2), 256, 0, stream>>>(
+ * AttnSplitParams{...}), src/engine/attention.hip:186-189 and tests/test_attn_splitk.hip:125-134
+ * (kernels/attention_decode.hpp:117-236). Writes part_m/part_l [2][n_splits][8] and part_o
+ * [2][n_splits][8][256] for keys [0, len). Rejects len == 0, len > max_ctx, n_splits == 0. */
+int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                    float* part_m, float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
+                    uint32_t n_splits, void* stream);
+
+/* LSE merge x sigmoid gate: replaces attn_combine_kernel<64, true, 4><<<64, 64, 0, stream>>>(
+ * AttnCombineParams{...}), src/engine/attention.hip:190-192 (kernels/attention_decode.hpp:
+ * 238-309). core [16][256] = merge of the partials x 1 / (1 + exp(-gate)), gate at qg[h*512 +
+ * 256 + d]. Bit-identical to the reference's frozen merge order. Rejects n_splits == 0. */
+int miso_attn_combine(const float* part_m, const float* part_l, const float* part_o,
+                      const float* qg, float* core, uint32_t n_splits, void* stream);
+
+/* The combine template variants and range form of the header API, launched as the reference's
+ * test and bench do (tests/test_attn_splitk.hip:43-45,78-91; bench/attention/bench_combine.hip:
+ * 40-46): variant 0 = attn_combine_kernel<256><<<16, 256>>>, 1 = <64><<<64, 64>>>,
+ * 2 = <64, true><<<64, 64>>>, 3 = <64, true, 4><<<64, 64>>>. With count > 0 it instead launches
+ * attn_combine_op<64, prepared, pipeline>(p, first, count) on <<<grid, 64>>> (variants 1-3;
+ * tiles are h * 4 + dim / 64, 64 tiles in all). Every variant is bit-identical. */
+int miso_attn_combine_variant(int variant, const float* part_m, const float* part_l,
+                              const float* part_o, const float* qg, float* core,
+                              uint32_t n_splits, uint32_t first, uint32_t count, uint32_t grid,
+                              void* stream);
+
+/* One decode step's attention: the split + combine pair of src/engine/attention.hip:185-192 in
+ * one call, with n_splits chosen by the caller (miso_attn_n_splits(len, capacity)). The partial
+ * buffers are caller-owned scratch of capacity >= n_splits. */
+int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
+                     const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                     float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
+                     void* stream);
+
+/* Causal prefill: replaces attn_prefill_kernel<256><<<attn_prefill_items(n), 256, 0, stream>>>(
+ * AttnPrefillParams{...}), src/engine/attention.hip:225-227 and tests/test_attn_splitk.hip:224-233
+ * (kernels/attention_prefill.hpp:42-161). Tokens pos0 .. pos0 + n - 1; q [n][16][256] (unscaled),
+ * gate at qg[t * qg_stride + h * 512 + 256 + d], keys [0, pos0 + n) already in the cache;
+ * core [n][16][256]. Rejects n == 0, pos0 + n > max_ctx, qg_stride < 8192. */
+int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
+                      const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
+                      uint32_t max_ctx, uint32_t qg_stride, void* stream);
+
+/* Ragged batched decode (no reference counterpart: the reference is batch-1,
+ * docs/decisions/ADR_002-build-scope-numerics-ops.md:14-18). batch sequences, one new token each:
+ * q [batch][16][256] (unscaled), gate [batch][16][256], core [batch][16][256] = per-sequence
+ * softmax(q K^T / 16) V x 1 / (1 + exp(-gate)). Sequence s has lens[s] keys stored contiguously
+ * as K/V [2][lens[s]][256] (f16) starting kv_offsets[s] halves into k_cache / v_cache; lens and
+ * kv_offsets are DEVICE arrays. max_len sizes the grid and the partial scratch: every sequence is
+ * split into at most miso_attn_ragged_splits(max_len) spans (a longer sequence still gets all of
+ * its keys, in longer spans). part_m/part_l need miso_attn_ragged_partials(batch, max_len) floats,
+ * part_o 256 times that. A sequence with lens[s] == 0 yields core = 0. Rejects batch == 0 and
+ * max_len == 0. */
+uint32_t miso_attn_ragged_splits(uint32_t max_len);
+uint64_t miso_attn_ragged_partials(uint32_t batch, uint32_t max_len);
+int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k_cache,
+                            const uint16_t* v_cache, const uint64_t* kv_offsets,
+                            const uint32_t* lens, uint32_t batch, uint32_t max_len, float* core,
+                            float* part_m, float* part_l, float* part_o, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MISO_ATTN_H */

@@ -1,0 +1,210 @@
+"""Host-side operators over torch device tensors, calling the C ABI of libmiso_attn.so.
+
+The names and argument meanings mirror the reference's kernel launch sites (kernels/
+attention_decode.hpp, kernels/attention_prefill.hpp as launched by src/engine/attention.hip and
+tests/test_attn_splitk.hip): the caller owns every buffer, including the split partials, and
+calls only enqueue work on the given stream (default: torch's current stream). Failures raise
+RuntimeError, as the reference throws std::runtime_error.
+
+torch is used for device memory and streams only; all arithmetic runs in the HIP kernels.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+Q_HEADS, KV_HEADS, DIM, GROUP = 16, 2, 256, 8
+QG_STRIDE = Q_HEADS * 2 * DIM  # 8192: [16][512] (q half, gate half) per token
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: int) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name} has {t.numel()} elements, needs >= {numel}")
+
+
+def _cache_dtype(t: torch.Tensor) -> torch.dtype:
+    return torch.float16 if t.dtype == torch.float16 else torch.int16
+
+
+def attn_n_splits(length: int, max_splits: int) -> int:
+    """Split count for a decode over `length` keys with partial buffers for max_splits splits."""
+    return int(_lib.load().miso_attn_n_splits(length, max_splits))
+
+
+def attn_prefill_items(n: int) -> int:
+    return int(_lib.load().miso_attn_prefill_items(n))
+
+
+def attn_prep(qg, k, v, q_norm, k_norm, inv_freq, k_cache, v_cache, q, pos: int, max_ctx: int,
+              eps: float, stream=None) -> None:
+    """RMSNorm + RoPE of one token's 16 query and 2 key heads; appends K/V at `pos`."""
+    f32 = torch.float32
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(k, "k", f32, KV_HEADS * DIM)
+    _need(v, "v", f32, KV_HEADS * DIM)
+    _need(q_norm, "q_norm", f32, DIM)
+    _need(k_norm, "k_norm", f32, DIM)
+    _need(inv_freq, "inv_freq", f32, 32)
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
+    _need(q, "q", f32, Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_prep(
+        _ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(inv_freq), _ptr(k_cache),
+        _ptr(v_cache), _ptr(q), pos, max_ctx, eps, _stream(stream)))
+
+
+def attn_prep_batch(qg, k, v, q_norm, k_norm, inv_freq, k_cache, v_cache, q, pos0: int,
+                    max_ctx: int, eps: float, n: int, proj_stride: int, stream=None) -> None:
+    """attn_prep for n tokens; qg/k/v are views into a token-major projection buffer whose
+    rows are proj_stride floats apart."""
+    f32 = torch.float32
+    for name, t in (("qg", qg), ("k", k), ("v", v)):
+        if not t.is_cuda or t.dtype != f32:
+            raise ValueError(f"{name} must be a float32 device tensor")
+    _need(q_norm, "q_norm", f32, DIM)
+    _need(k_norm, "k_norm", f32, DIM)
+    _need(inv_freq, "inv_freq", f32, 32)
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
+    _need(q, "q", f32, n * Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_prep_batch(
+        _ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(inv_freq), _ptr(k_cache),
+        _ptr(v_cache), _ptr(q), pos0, max_ctx, eps, n, proj_stride, _stream(stream)))
+
+
+def attn_split(q, k_cache, v_cache, part_m, part_l, part_o, length: int, max_ctx: int,
+               n_splits: int, stream=None) -> None:
+    f32 = torch.float32
+    _need(q, "q", f32, Q_HEADS * DIM)
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
+    _need(part_m, "part_m", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_l, "part_l", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_o, "part_o", f32, KV_HEADS * n_splits * GROUP * DIM)
+    _lib.check(_lib.load().miso_attn_split(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(part_m), _ptr(part_l), _ptr(part_o), length,
+        max_ctx, n_splits, _stream(stream)))
+
+
+def attn_combine(part_m, part_l, part_o, qg, core, n_splits: int, stream=None) -> None:
+    f32 = torch.float32
+    _need(part_m, "part_m", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_l, "part_l", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_o, "part_o", f32, KV_HEADS * n_splits * GROUP * DIM)
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(core, "core", f32, Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_combine(
+        _ptr(part_m), _ptr(part_l), _ptr(part_o), _ptr(qg), _ptr(core), n_splits,
+        _stream(stream)))
+
+
+def attn_combine_variant(variant: int, part_m, part_l, part_o, qg, core, n_splits: int,
+                         first: int = 0, count: int = 0, grid: int = 0, stream=None) -> None:
+    """The header API's combine template variants (0: <256>, 1: <64>, 2: <64,true>,
+    3: <64,true,4>) with the reference's launch shapes, or with count > 0 the range form
+    attn_combine_op<64,...>(p, first, count) on `grid` 64-thread workgroups."""
+    f32 = torch.float32
+    _need(part_m, "part_m", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_l, "part_l", f32, KV_HEADS * n_splits * GROUP)
+    _need(part_o, "part_o", f32, KV_HEADS * n_splits * GROUP * DIM)
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(core, "core", f32, Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_combine_variant(
+        variant, _ptr(part_m), _ptr(part_l), _ptr(part_o), _ptr(qg), _ptr(core), n_splits, first,
+        count, grid, _stream(stream)))
+
+
+class DecodeScratch:
+    """Caller-owned split partials with capacity for max_splits splits (the role of
+    AttentionScratch::part_m/part_l/part_o in the reference engine)."""
+
+    def __init__(self, max_splits: int, device="cuda"):
+        self.max_splits = max_splits
+        n = KV_HEADS * max_splits * GROUP
+        self.part_m = torch.empty(n, dtype=torch.float32, device=device)
+        self.part_l = torch.empty(n, dtype=torch.float32, device=device)
+        self.part_o = torch.empty(n * DIM, dtype=torch.float32, device=device)
+
+
+def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: int,
+                max_ctx: int, n_splits: Optional[int] = None, stream=None) -> int:
+    """Split + combine for one decode token over keys [0, length). Returns n_splits used."""
+    if n_splits is None:
+        n_splits = attn_n_splits(length, scratch.max_splits)
+    if n_splits > scratch.max_splits:
+        raise ValueError("n_splits exceeds the scratch capacity")
+    f32 = torch.float32
+    _need(q, "q", f32, Q_HEADS * DIM)
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
+    _need(core, "core", f32, Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_decode(
+        _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), _ptr(scratch.part_m),
+        _ptr(scratch.part_l), _ptr(scratch.part_o), length, max_ctx, n_splits, _stream(stream)))
+    return n_splits
+
+
+def attn_prefill(q, qg, k_cache, v_cache, core, pos0: int, n: int, max_ctx: int,
+                 qg_stride: int = QG_STRIDE, stream=None) -> None:
+    f32 = torch.float32
+    _need(q, "q", f32, n * Q_HEADS * DIM)
+    _need(qg, "qg", f32, (n - 1) * qg_stride + Q_HEADS * 2 * DIM if n else 0)
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
+    _need(core, "core", f32, n * Q_HEADS * DIM)
+    _lib.check(_lib.load().miso_attn_prefill(
+        _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), pos0, n, max_ctx, qg_stride,
+        _stream(stream)))
+
+
+def ragged_partials(batch: int, max_len: int) -> int:
+    return int(_lib.load().miso_attn_ragged_partials(batch, max_len))
+
+
+class RaggedScratch:
+    def __init__(self, batch: int, max_len: int, device="cuda"):
+        n = ragged_partials(batch, max_len)
+        self.batch, self.max_len = batch, max_len
+        self.part_m = torch.empty(n, dtype=torch.float32, device=device)
+        self.part_l = torch.empty(n, dtype=torch.float32, device=device)
+        self.part_o = torch.empty(n * DIM, dtype=torch.float32, device=device)
+
+
+def attn_decode_ragged(q, gate, k_cache, v_cache, kv_offsets, lens, core,
+                       scratch: RaggedScratch, stream=None) -> None:
+    """Batched decode: sequence s attends over lens[s] keys stored as K/V [2][lens[s]][256]
+    starting kv_offsets[s] halves into k_cache / v_cache (device int64 / int32 arrays)."""
+    batch, max_len = scratch.batch, scratch.max_len
+    f32 = torch.float32
+    _need(q, "q", f32, batch * Q_HEADS * DIM)
+    _need(gate, "gate", f32, batch * Q_HEADS * DIM)
+    _need(core, "core", f32, batch * Q_HEADS * DIM)
+    _need(kv_offsets, "kv_offsets", torch.int64, batch)
+    _need(lens, "lens", torch.int32, batch)
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if not t.is_cuda or t.dtype not in (torch.float16, torch.int16):
+            raise ValueError(f"{name} must be a float16 device tensor")
+    _lib.check(_lib.load().miso_attn_decode_ragged(
+        _ptr(q), _ptr(gate), _ptr(k_cache), _ptr(v_cache), _ptr(kv_offsets), _ptr(lens), batch,
+        max_len, _ptr(core), _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o),
+        _stream(stream)))

@@ -1,0 +1,66 @@
+"""Build the product library libmiso_attn.so (gfx950) in-tree with hipcc.
+
+    python -m miso_amd.build            # or: python miso_amd/build.py
+
+The shared library lands in miso_amd/lib/ and is what miso_amd.attention, the GPU tests,
+__graft_entry__.smoke() and bench.py load. No JIT and no site-packages install: the built file
+travels with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+LIB_DIR = PKG / "lib"
+LIB = LIB_DIR / "libmiso_attn.so"
+SOURCES = [PKG / "csrc" / "miso_attn_capi.hip"]
+HEADERS = sorted((PKG / "kernels").glob("*.hpp")) + [ROOT / "include" / "miso_attn.h"]
+
+# Packed FP32 VALU forms are disabled for all device code built here.
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++20",
+    "--offload-arch=gfx950",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    "-Wextra",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wl,-Bsymbolic",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libmiso_attn.so for gfx950 (always recompiles)."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIP_FLAGS, "-I", str(PKG / "kernels"), "-I", str(ROOT / "include"),
+           *map(str, SOURCES), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 target feature; that warning is expected.
+    noise = ("packed-fp32-ops", "not a recognized feature")
+    err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

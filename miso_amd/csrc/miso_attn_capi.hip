@@ -1,0 +1,204 @@
+// C ABI of the MI355X attention library: argument validation on the host, then launches of the
+// kernels the header API defines (miso_amd/kernels/*.hpp), with the reference callers' launch
+// shapes. Declarations and contracts: include/miso_attn.h.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/miso_attn.h"
+#include "attention_decode.hpp"
+#include "attention_prefill.hpp"
+
+namespace k = miso::kernels;
+using k::attn::half_t;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fn, const char* msg) {
+  g_last_error = std::string(fn) + ": " + msg;
+  return MISO_ATTN_EINVAL;
+}
+
+// The reference checks hipGetLastError() after its launches (MISO_HIP_CHECK) and throws with the
+// error's name; here the same error becomes the return code and the message.
+int launched(const char* fn) {
+  const hipError_t err = hipGetLastError();
+  if (err == hipSuccess)
+    return 0;
+  g_last_error = std::string(fn) + ": " + hipGetErrorName(err) + " (" + hipGetErrorString(err) + ")";
+  return static_cast<int>(err);
+}
+
+template <bool kPrepared, int kPipeline>
+__global__ void __launch_bounds__(64) combine_range_kernel(k::AttnCombineParams p, unsigned first,
+                                                           unsigned count) {
+  k::attn_combine_op<64, kPrepared, kPipeline>(p, first, count);
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+const half_t* as_half(const uint16_t* p) { return reinterpret_cast<const half_t*>(p); }
+half_t* as_half(uint16_t* p) { return reinterpret_cast<half_t*>(p); }
+
+}  // namespace
+
+extern "C" {
+
+const char* miso_attn_last_error(void) { return g_last_error.c_str(); }
+
+const char* miso_attn_version(void) { return "miso_attn gfx950 r1"; }
+
+uint32_t miso_attn_n_splits(uint32_t len, uint32_t max_splits) {
+  return k::attn_n_splits(len, max_splits);
+}
+
+uint32_t miso_attn_prefill_items(uint32_t n) { return k::attn_prefill_items(n); }
+
+int miso_attn_prep(const float* qg, const float* kp, const float* v, const float* q_norm,
+                   const float* k_norm, const float* inv_freq, uint16_t* k_cache,
+                   uint16_t* v_cache, float* q, uint32_t pos, uint32_t max_ctx, float eps,
+                   void* stream) {
+  if (pos >= max_ctx)
+    return fail("miso_attn_prep", "KV cache is full (pos >= max_ctx)");
+  const k::AttnPrepParams p{qg,     kp,          v,           q_norm, k_norm, inv_freq,
+                            as_half(k_cache), as_half(v_cache), q, pos, max_ctx, eps};
+  k::attn_prep_kernel<256><<<18, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prep");
+}
+
+int miso_attn_prep_batch(const float* qg, const float* kp, const float* v, const float* q_norm,
+                         const float* k_norm, const float* inv_freq, uint16_t* k_cache,
+                         uint16_t* v_cache, float* q, uint32_t pos0, uint32_t max_ctx, float eps,
+                         uint32_t n, uint32_t proj_stride, void* stream) {
+  if (n == 0)
+    return 0;
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail("miso_attn_prep_batch", "KV cache is full (pos0 + n > max_ctx)");
+  if (proj_stride < 8192 + 1024)
+    return fail("miso_attn_prep_batch", "proj_stride must cover [q+gate 8192 | k 512 | v 512]");
+  const k::AttnPrepBatchParams p{{qg, kp, v, q_norm, k_norm, inv_freq, as_half(k_cache),
+                                  as_half(v_cache), q, pos0, max_ctx, eps},
+                                 n,
+                                 proj_stride};
+  k::attn_prep_batch_kernel<256><<<n * 18, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prep_batch");
+}
+
+int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                    float* part_m, float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
+                    uint32_t n_splits, void* stream) {
+  if (len == 0)
+    return fail("miso_attn_split", "len must be >= 1");
+  if (len > max_ctx)
+    return fail("miso_attn_split", "len exceeds max_ctx");
+  if (n_splits == 0)
+    return fail("miso_attn_split", "n_splits must be >= 1");
+  const k::AttnSplitParams p{q,      as_half(k_cache), as_half(v_cache), part_m, part_l,
+                             part_o, len,              max_ctx,          n_splits};
+  k::attn_split_kernel<256><<<dim3(n_splits, 2), 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_split");
+}
+
+int miso_attn_combine(const float* part_m, const float* part_l, const float* part_o,
+                      const float* qg, float* core, uint32_t n_splits, void* stream) {
+  if (n_splits == 0)
+    return fail("miso_attn_combine", "n_splits must be >= 1");
+  const k::AttnCombineParams p{part_m, part_l, part_o, qg, core, n_splits};
+  k::attn_combine_kernel<64, true, 4><<<64, 64, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_combine");
+}
+
+int miso_attn_combine_variant(int variant, const float* part_m, const float* part_l,
+                              const float* part_o, const float* qg, float* core,
+                              uint32_t n_splits, uint32_t first, uint32_t count, uint32_t grid,
+                              void* stream) {
+  if (n_splits == 0)
+    return fail("miso_attn_combine_variant", "n_splits must be >= 1");
+  if (variant < 0 || variant > 3)
+    return fail("miso_attn_combine_variant", "variant must be 0..3");
+  constexpr uint32_t kTiles = 16 * (256 / 64);
+  if (count > 0 && (variant == 0 || grid == 0 || first > kTiles || count > kTiles - first))
+    return fail("miso_attn_combine_variant", "range form needs variant 1..3, grid >= 1 and "
+                "first + count <= 64");
+  const k::AttnCombineParams p{part_m, part_l, part_o, qg, core, n_splits};
+  const hipStream_t st = as_stream(stream);
+  if (count == 0) {
+    switch (variant) {
+      case 0: k::attn_combine_kernel<256><<<16, 256, 0, st>>>(p); break;
+      case 1: k::attn_combine_kernel<64><<<64, 64, 0, st>>>(p); break;
+      case 2: k::attn_combine_kernel<64, true><<<64, 64, 0, st>>>(p); break;
+      default: k::attn_combine_kernel<64, true, 4><<<64, 64, 0, st>>>(p); break;
+    }
+  } else {
+    switch (variant) {
+      case 1: combine_range_kernel<false, 1><<<grid, 64, 0, st>>>(p, first, count); break;
+      case 2: combine_range_kernel<true, 1><<<grid, 64, 0, st>>>(p, first, count); break;
+      default: combine_range_kernel<true, 4><<<grid, 64, 0, st>>>(p, first, count); break;
+    }
+  }
+  return launched("miso_attn_combine_variant");
+}
+
+int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
+                     const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                     float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
+                     void* stream) {
+  const int rc =
+      miso_attn_split(q, k_cache, v_cache, part_m, part_l, part_o, len, max_ctx, n_splits, stream);
+  if (rc != 0)
+    return rc;
+  return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
+}
+
+int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
+                      const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
+                      uint32_t max_ctx, uint32_t qg_stride, void* stream) {
+  if (n == 0)
+    return fail("miso_attn_prefill", "n must be >= 1");
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail("miso_attn_prefill", "KV cache is full (pos0 + n > max_ctx)");
+  if (qg_stride < 8192)
+    return fail("miso_attn_prefill", "qg_stride must be >= 8192");
+  const k::AttnPrefillParams p{q,    qg, as_half(k_cache), as_half(v_cache), core, pos0,
+                               n,    max_ctx, qg_stride};
+  k::attn_prefill_kernel<256><<<k::attn_prefill_items(n), 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prefill");
+}
+
+uint32_t miso_attn_ragged_splits(uint32_t max_len) { return k::attn_ragged_splits(max_len); }
+
+uint64_t miso_attn_ragged_partials(uint32_t batch, uint32_t max_len) {
+  return uint64_t{batch} * k::attn::kKvHeads * k::attn_ragged_splits(max_len) *
+         (k::attn::kQHeads / k::attn::kKvHeads);
+}
+
+int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k_cache,
+                            const uint16_t* v_cache, const uint64_t* kv_offsets,
+                            const uint32_t* lens, uint32_t batch, uint32_t max_len, float* core,
+                            float* part_m, float* part_l, float* part_o, void* stream) {
+  if (batch == 0)
+    return fail("miso_attn_decode_ragged", "batch must be >= 1");
+  if (max_len == 0)
+    return fail("miso_attn_decode_ragged", "max_len must be >= 1");
+  const unsigned s_max = k::attn_ragged_splits(max_len);
+  const k::AttnRaggedParams p{q,      gate,   as_half(k_cache), as_half(v_cache), kv_offsets,
+                              lens,   core,   part_m,           part_l,           part_o,
+                              batch,  s_max};
+  const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
+  if (items > 0x7FFFFFFFull)
+    return fail("miso_attn_decode_ragged", "batch x splits too large for one grid");
+  k::attn_ragged_split_kernel<256>
+      <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
+  int rc = launched("miso_attn_decode_ragged(split)");
+  if (rc != 0)
+    return rc;
+  const unsigned tiles = batch * k::attn::kQHeads * (k::attn::kDim / 64);
+  k::attn_ragged_combine_kernel<<<tiles, 64, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_decode_ragged(combine)");
+}
+
+}  // extern "C"

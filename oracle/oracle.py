@@ -1,0 +1,314 @@
+"""Python wrapper of the CPU oracle (oracle/attn_oracle.c) and of the reference kernels built
+from the reference's own sources (oracle/_ref).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker. The product (miso_amd/) never imports this module.
+
+Each function cites the reference code it restates in attn_oracle.c's header.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "libattn_oracle.so"
+REF_PATH = HERE / "_ref" / "libmiso_ref_kernels.so"
+
+Q_HEADS, KV_HEADS, DIM, GROUP = 16, 2, 256, 8
+QG_STRIDE = Q_HEADS * 2 * DIM
+
+_lib = None
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(c_void_p)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(str(LIB_PATH))
+        V = c_void_p
+        sig = {
+            "oracle_splitmix64": (c_uint64, [POINTER(c_uint64)]),
+            "oracle_xoshiro_stream": (None, [c_uint64, V, ctypes.c_size_t]),
+            "oracle_xoshiro_raw": (None, [V, V, ctypes.c_size_t]),
+            "oracle_fill_normal": (None, [c_uint64, c_float, V, ctypes.c_size_t]),
+            "oracle_fill_normal_f16": (None, [c_uint64, V, ctypes.c_size_t]),
+            "oracle_f32_to_f16": (c_uint16, [c_float]),
+            "oracle_f16_to_f32": (c_float, [c_uint16]),
+            "oracle_f32_to_f16_array": (None, [V, V, ctypes.c_size_t]),
+            "oracle_f16_to_f32_array": (None, [V, V, ctypes.c_size_t]),
+            "oracle_decode_f64": (None, [V, V, V, V, c_uint32, c_uint32, V, c_int]),
+            "oracle_ragged_f64": (None, [V, V, V, V, V, V, c_uint32, V, c_int]),
+            "oracle_prefill_f64": (None, [V, V, c_uint32, V, V, c_uint32, c_uint32, V, c_uint32,
+                                          V, c_int]),
+            "oracle_partials_f64": (None, [V, V, V, c_uint32, c_uint32, c_uint32, c_uint32, V, V,
+                                           V]),
+            "oracle_combine_f32": (None, [V, V, V, V, c_uint32, V]),
+            "oracle_inv_freq": (None, [c_float, V]),
+            "oracle_prep_f64": (None, [V, V, V, V, V, V, c_uint32, c_float, V, V, V]),
+            "oracle_ref_n_splits": (c_uint32, [c_uint32, c_uint32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def default_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# ------------------------------------------------------------------------------------------------
+# Generator and binary16
+# ------------------------------------------------------------------------------------------------
+
+def splitmix64_stream(seed: int, n: int) -> np.ndarray:
+    st = c_uint64(seed)
+    return np.array([lib().oracle_splitmix64(ctypes.byref(st)) for _ in range(n)], dtype=np.uint64)
+
+
+def xoshiro_stream(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint64)
+    lib().oracle_xoshiro_stream(seed, _ptr(out), n)
+    return out
+
+
+def xoshiro_raw(state, n: int) -> np.ndarray:
+    st = np.ascontiguousarray(state, dtype=np.uint64)
+    out = np.empty(n, dtype=np.uint64)
+    lib().oracle_xoshiro_raw(_ptr(st), _ptr(out), n)
+    return out
+
+
+def normal(seed: int, n: int, scale: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().oracle_fill_normal(seed, scale, _ptr(out), n)
+    return out
+
+
+def normal_f16(seed: int, n: int) -> np.ndarray:
+    """binary16 bit patterns (uint16) of N(0,1) values."""
+    out = np.empty(n, dtype=np.uint16)
+    lib().oracle_fill_normal_f16(seed, _ptr(out), n)
+    return out
+
+
+def f32_to_f16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16_array(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# Seeded inputs of the configs (identical on every machine)
+# ------------------------------------------------------------------------------------------------
+
+def decode_inputs(seed: int, length: int, max_ctx: int | None = None, q_scale: float = 1.0):
+    """q [16][256] = q_scale * N(0,1); qg [16][512] N(0,1) (gate = second half of each head);
+    K/V caches [2][max_ctx][256] binary16 of N(0,1). Streams: seed*8 + {0,1,2,3}."""
+    max_ctx = length if max_ctx is None else max_ctx
+    return {
+        "q": normal(seed * 8 + 0, Q_HEADS * DIM, q_scale),
+        "qg": normal(seed * 8 + 1, Q_HEADS * 2 * DIM),
+        "k": normal_f16(seed * 8 + 2, KV_HEADS * max_ctx * DIM),
+        "v": normal_f16(seed * 8 + 3, KV_HEADS * max_ctx * DIM),
+        "len": length,
+        "max_ctx": max_ctx,
+    }
+
+
+def prefill_inputs(seed: int, pos0: int, n: int, max_ctx: int | None = None,
+                   q_scale: float = 1.0, qg_stride: int = QG_STRIDE):
+    """q [n][16][256]; qg [n][qg_stride] N(0,1) (gate of head h at h*512 + 256); K/V caches
+    [2][max_ctx][256] holding keys [0, pos0 + n) (whole cache filled)."""
+    max_ctx = pos0 + n if max_ctx is None else max_ctx
+    return {
+        "q": normal(seed * 8 + 4, n * Q_HEADS * DIM, q_scale),
+        "qg": normal(seed * 8 + 5, n * qg_stride),
+        "k": normal_f16(seed * 8 + 6, KV_HEADS * max_ctx * DIM),
+        "v": normal_f16(seed * 8 + 7, KV_HEADS * max_ctx * DIM),
+        "pos0": pos0,
+        "n": n,
+        "max_ctx": max_ctx,
+        "qg_stride": qg_stride,
+    }
+
+
+def ragged_lengths(seed: int, batch: int, lo: int, hi: int) -> np.ndarray:
+    """Lengths uniform in [lo, hi] from the xoshiro stream of `seed`."""
+    raw = xoshiro_stream(seed, batch)
+    return (lo + (raw % np.uint64(hi - lo + 1))).astype(np.uint32)
+
+
+def ragged_inputs(seed: int, lens: np.ndarray):
+    lens = np.asarray(lens, dtype=np.uint32)
+    batch = lens.size
+    sizes = lens.astype(np.uint64) * np.uint64(KV_HEADS * DIM)
+    offsets = np.zeros(batch, dtype=np.uint64)
+    offsets[1:] = np.cumsum(sizes)[:-1]
+    total = int(sizes.sum())
+    return {
+        "q": normal(seed * 8 + 0, batch * Q_HEADS * DIM),
+        "gate": normal(seed * 8 + 1, batch * Q_HEADS * DIM),
+        "k": normal_f16(seed * 8 + 2, total),
+        "v": normal_f16(seed * 8 + 3, total),
+        "lens": lens,
+        "offsets": offsets,
+    }
+
+
+# ------------------------------------------------------------------------------------------------
+# References
+# ------------------------------------------------------------------------------------------------
+
+def decode_f64(q, qg, k, v, length: int, max_ctx: int, threads: int = 0) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    qg = np.ascontiguousarray(qg, np.float32)
+    k = np.ascontiguousarray(k, np.uint16)
+    v = np.ascontiguousarray(v, np.uint16)
+    out = np.empty((Q_HEADS, DIM), dtype=np.float64)
+    lib().oracle_decode_f64(_ptr(q), _ptr(qg), _ptr(k), _ptr(v), length, max_ctx, _ptr(out),
+                            threads or default_threads())
+    return out
+
+
+def prefill_f64(q, qg, qg_stride: int, k, v, pos0: int, max_ctx: int, tokens,
+                threads: int = 0) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    qg = np.ascontiguousarray(qg, np.float32)
+    k = np.ascontiguousarray(k, np.uint16)
+    v = np.ascontiguousarray(v, np.uint16)
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+    out = np.empty((tok.size, Q_HEADS, DIM), dtype=np.float64)
+    lib().oracle_prefill_f64(_ptr(q), _ptr(qg), qg_stride, _ptr(k), _ptr(v), pos0, max_ctx,
+                             _ptr(tok), tok.size, _ptr(out), threads or default_threads())
+    return out
+
+
+def ragged_f64(q, gate, k, v, offsets, lens, threads: int = 0) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    gate = np.ascontiguousarray(gate, np.float32)
+    k = np.ascontiguousarray(k, np.uint16)
+    v = np.ascontiguousarray(v, np.uint16)
+    offsets = np.ascontiguousarray(offsets, np.uint64)
+    lens = np.ascontiguousarray(lens, np.uint32)
+    out = np.empty((lens.size, Q_HEADS, DIM), dtype=np.float64)
+    lib().oracle_ragged_f64(_ptr(q), _ptr(gate), _ptr(k), _ptr(v), _ptr(offsets), _ptr(lens),
+                            lens.size, _ptr(out), threads or default_threads())
+    return out
+
+
+def partials_f64(q, k, v, kvh: int, max_ctx: int, j0: int, j1: int):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.uint16)
+    v = np.ascontiguousarray(v, np.uint16)
+    m = np.empty(GROUP, np.float64)
+    l = np.empty(GROUP, np.float64)
+    o = np.empty((GROUP, DIM), np.float64)
+    lib().oracle_partials_f64(_ptr(q), _ptr(k), _ptr(v), kvh, max_ctx, j0, j1, _ptr(m), _ptr(l),
+                              _ptr(o))
+    return m, l, o
+
+
+def combine_f32(pm, pl, po, qg, n_splits: int) -> np.ndarray:
+    pm = np.ascontiguousarray(pm, np.float32)
+    pl = np.ascontiguousarray(pl, np.float32)
+    po = np.ascontiguousarray(po, np.float32)
+    qg = np.ascontiguousarray(qg, np.float32)
+    out = np.empty((Q_HEADS, DIM), np.float32)
+    lib().oracle_combine_f32(_ptr(pm), _ptr(pl), _ptr(po), _ptr(qg), n_splits, _ptr(out))
+    return out
+
+
+def inv_freq(base: float) -> np.ndarray:
+    out = np.empty(32, np.float32)
+    lib().oracle_inv_freq(base, _ptr(out))
+    return out
+
+
+def prep_f64(qg, k, v, q_norm, k_norm, inv_freq_arr, pos: int, eps: float):
+    """One token: returns (q [16][256] float64, k_f16 [2][256] uint16, v_f16 [2][256] uint16)."""
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (qg, k, v, q_norm, k_norm, inv_freq_arr)]
+    q_out = np.empty((Q_HEADS, DIM), np.float64)
+    k_out = np.empty((KV_HEADS, DIM), np.uint16)
+    v_out = np.empty((KV_HEADS, DIM), np.uint16)
+    lib().oracle_prep_f64(*[_ptr(a) for a in arrs], pos, eps, _ptr(q_out), _ptr(k_out),
+                          _ptr(v_out))
+    return q_out, k_out, v_out
+
+
+def ref_n_splits(length: int, max_splits: int) -> int:
+    return int(lib().oracle_ref_n_splits(length, max_splits))
+
+
+# ------------------------------------------------------------------------------------------------
+# Tolerance of the north star: |got - ref| <= 2e-3 + 1e-2 |ref| per element (f32 output)
+# ------------------------------------------------------------------------------------------------
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def compare(got: np.ndarray, ref: np.ndarray, atol: float = ATOL, rtol: float = RTOL) -> dict:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    big = np.abs(ref) >= atol / rtol
+    rel = err[big] / np.abs(ref[big]) if big.any() else np.zeros(1)
+    bad = err > atol + rtol * np.abs(ref)
+    finite = bool(np.isfinite(got).all())
+    return {
+        "ok": finite and not bool(bad.any()),
+        "finite": finite,
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "max_rel": float(rel.max()) if rel.size else 0.0,
+        "n_bad": int(bad.sum()),
+        "rel_l2": float(np.sqrt(((got - ref) ** 2).sum() / max((ref ** 2).sum(), 1e-300))),
+    }
+
+
+# ------------------------------------------------------------------------------------------------
+# The reference's kernels compiled from its sources (GPU; optional second checker)
+# ------------------------------------------------------------------------------------------------
+
+_ref = None
+
+
+def ref_kernels():
+    """ctypes handle of oracle/_ref/libmiso_ref_kernels.so, or None if it was not built."""
+    global _ref
+    if _ref is None and REF_PATH.exists():
+        L = ctypes.CDLL(str(REF_PATH))
+        V, U = c_void_p, c_uint32
+        sig = {
+            "ref_attn_n_splits": (U, [U, U]),
+            "ref_attn_split": (c_int, [V, V, V, V, V, V, U, U, U]),
+            "ref_attn_combine": (c_int, [c_int, V, V, V, V, V, U]),
+            "ref_attn_prefill": (c_int, [V, V, V, V, V, U, U, U, U]),
+            "ref_attn_prep": (c_int, [V, V, V, V, V, V, V, V, V, U, U, c_float]),
+            "ref_attn_prep_batch": (c_int, [V, V, V, V, V, V, V, V, V, U, U, c_float, U, U]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _ref = L
+    return _ref

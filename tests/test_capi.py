@@ -1,0 +1,116 @@
+"""CPU tests of the C ABI boundary (include/miso_attn.h, miso_amd/lib/libmiso_attn.so): the
+library loads without a GPU, exports exactly the declared entry points, validates arguments on
+the host (no launch happens for a rejected call), and the split / grid policies keep their
+contracts. No compute call is made here.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "miso_attn.h"
+EINVAL = 0x4D41
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(miso_attn_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from miso_amd import _lib
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+    from miso_amd import _lib
+    assert sorted(_lib.SIGNATURES) == names  # the ctypes table matches the header
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(miso_attn_\w+)\b", out))
+    assert exported == set(names)
+
+
+def test_version_string(lib):
+    assert lib.miso_attn_version().decode().startswith("miso_attn gfx950")
+
+
+def rejected(rc, lib, needle):
+    assert rc == EINVAL
+    msg = lib.miso_attn_last_error().decode()
+    assert needle in msg, msg
+
+
+def test_host_validation_rejects_bad_arguments(lib):
+    N = None
+    rejected(lib.miso_attn_split(N, N, N, N, N, N, 0, 10, 1, N), lib, "len must be >= 1")
+    rejected(lib.miso_attn_split(N, N, N, N, N, N, 11, 10, 1, N), lib, "exceeds max_ctx")
+    rejected(lib.miso_attn_split(N, N, N, N, N, N, 5, 10, 0, N), lib, "n_splits")
+    rejected(lib.miso_attn_combine(N, N, N, N, N, 0, N), lib, "n_splits")
+    rejected(lib.miso_attn_decode(N, N, N, N, N, N, N, N, 0, 10, 4, N), lib, "len must be")
+    rejected(lib.miso_attn_prefill(N, N, N, N, N, 0, 0, 10, 8192, N), lib, "n must be >= 1")
+    rejected(lib.miso_attn_prefill(N, N, N, N, N, 8, 3, 10, 8192, N), lib, "KV cache is full")
+    rejected(lib.miso_attn_prefill(N, N, N, N, N, 0, 3, 10, 100, N), lib, "qg_stride")
+    rejected(lib.miso_attn_prep(N, N, N, N, N, N, N, N, N, 10, 10, 1e-6, N), lib, "full")
+    rejected(lib.miso_attn_prep_batch(N, N, N, N, N, N, N, N, N, 8, 10, 1e-6, 3, 9216, N), lib,
+             "full")
+    rejected(lib.miso_attn_prep_batch(N, N, N, N, N, N, N, N, N, 0, 10, 1e-6, 3, 8192, N), lib,
+             "proj_stride")
+    rejected(lib.miso_attn_decode_ragged(N, N, N, N, N, N, 0, 10, N, N, N, N, N), lib, "batch")
+    rejected(lib.miso_attn_decode_ragged(N, N, N, N, N, N, 3, 0, N, N, N, N, N), lib, "max_len")
+    rejected(lib.miso_attn_combine_variant(7, N, N, N, N, N, 4, 0, 0, 0, N), lib, "variant")
+    rejected(lib.miso_attn_combine_variant(0, N, N, N, N, N, 4, 0, 8, 2, N), lib, "range form")
+    rejected(lib.miso_attn_combine_variant(1, N, N, N, N, N, 4, 60, 8, 2, N), lib, "range form")
+
+
+def test_python_layer_raises_runtime_error_with_message():
+    from miso_amd import _lib
+    with pytest.raises(RuntimeError, match="n_splits must be >= 1"):
+        _lib.check(_lib.load().miso_attn_combine(None, None, None, None, None, 0, None))
+
+
+def test_split_policy_contract(lib):
+    f = lib.miso_attn_n_splits
+    assert f(0, 60) == 1 and f(0, 0) == 1 and f(5, 0) == 1
+    prev = 1
+    for length in list(range(1, 3000, 7)) + [32767, 32768, 32769, 10**6]:
+        for cap in (1, 3, 16, 60, 128, 256):
+            n = f(length, cap)
+            assert 1 <= n <= cap and n <= 128
+            assert n <= (length + 31) // 32
+        n60 = f(length, 60)
+        assert n60 >= prev or length < 32  # non-decreasing in length
+        prev = n60
+    assert f(32768, 60) == 60 and f(32768, 1000) == 128 and f(512, 60) == 16
+
+
+def test_prefill_grid_covers_every_block(lib):
+    for n in (1, 15, 16, 17, 63, 64, 65, 2048, 8192, 10**5):
+        items = lib.miso_attn_prefill_items(n)
+        blocks = (n + 15) // 16
+        assert items % 8 == 0 and items >= 2 * blocks and items < 2 * blocks + 8
+        # item -> (kv head, rank): a bijection onto {0,1} x [0, blocks) plus idle slots
+        seen = set()
+        for item in range(items):
+            slot = item % 8
+            rank = (item // 8) * 4 + slot % 4
+            if rank < blocks:
+                seen.add((slot // 4, rank))
+        assert len(seen) == 2 * blocks
+
+
+def test_ragged_scratch_sizes(lib):
+    assert lib.miso_attn_ragged_splits(1) == 1
+    assert lib.miso_attn_ragged_splits(512) == 1 and lib.miso_attn_ragged_splits(513) == 2
+    assert lib.miso_attn_ragged_splits(16384) == 32
+    assert lib.miso_attn_ragged_partials(64, 16384) == 64 * 2 * 32 * 8

@@ -1,0 +1,54 @@
+"""Drop-in check of the C++ header API (CPU, compile-only): the reference's own callers of the
+attention kernels -- src/engine/attention.hip, tests/test_attn_splitk.hip and
+bench/attention/*.hip -- compile UNCHANGED for gfx950 with this repository's
+miso_amd/kernels ahead of the reference's kernels/ on the include path, and the preprocessor
+really picks this repository's attention headers (while the reference's own rmsnorm.hpp and
+wave.hpp stay reachable in the same translation unit without clashes).
+
+Runs only where the reference tree and hipcc exist (this container); nothing is copied, objects
+go to a temporary directory.
+"""
+from __future__ import annotations
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+REF = Path("/root/reference")
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+# (caller, includes the attention kernel headers itself)
+CALLERS = [
+    ("src/engine/attention.hip", True),
+    ("tests/test_attn_splitk.hip", True),
+    ("bench/attention/bench_combine.hip", True),
+    ("bench/attention/bench_attention.hip", False),  # only through engine/attention.hpp
+]
+
+pytestmark = pytest.mark.skipif(not (REF / "kernels").is_dir() or not Path(HIPCC).exists(),
+                                reason="reference tree or hipcc not available")
+
+
+@pytest.mark.parametrize("caller,direct", CALLERS)
+def test_reference_caller_compiles_against_our_headers(caller, direct, tmp_path):
+    src = REF / caller
+    cmd = [HIPCC, "-std=c++20", "-O1", "--offload-arch=gfx950", "-c", str(src),
+           "-o", str(tmp_path / "x.o"), "-H",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-I", str(ROOT / "miso_amd" / "kernels"),
+           "-I", str(REF / "kernels"), "-I", str(REF / "src"),
+           "-isystem", str(REF / "third_party"),
+           '-DMISO_ORNITH_GGUF="/nonexistent.gguf"']
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-4000:]
+    included = [l.lstrip(". ").strip() for l in res.stderr.splitlines() if l.startswith(".")]
+    ours = str(ROOT / "miso_amd" / "kernels")
+    for name in ("attention_decode.hpp", "attention_prefill.hpp"):
+        hits = [p for p in included if p.endswith("/" + name)]
+        if hits:  # every resolution of the attention headers is ours
+            assert all(Path(p).resolve().as_posix().startswith(ours) for p in hits), hits
+    if direct:
+        assert any(p.endswith("/attention_decode.hpp") for p in included)

@@ -1,0 +1,57 @@
+"""Ragged batched decode parity (BASELINE C5; no reference counterpart -- the reference is
+batch-1): each sequence against the FP64 oracle of decode with a dense sigmoid gate.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import report, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+H, D = 16, 256
+
+
+def run(O, attn, torch, lens, seed, max_len=None):
+    r = O.ragged_inputs(seed, lens)
+    batch = len(lens)
+    max_len = int(max(lens)) if max_len is None else max_len
+    sc = attn.RaggedScratch(batch, max_len)
+    core = torch.full((batch * H * D,), -9123.5, device="cuda")
+    attn.attn_decode_ragged(to_dev(torch, r["q"]), to_dev(torch, r["gate"]),
+                            to_dev(torch, r["k"]), to_dev(torch, r["v"]),
+                            to_dev(torch, r["offsets"]), to_dev(torch, r["lens"]), core, sc)
+    torch.cuda.synchronize()
+    return r, to_host(core).reshape(batch, H, D)
+
+
+def test_ragged_c5(O, attn, torch_mod):
+    """C5: 64 sequences, lengths uniform in [1024, 16384] from seed 64."""
+    lens = O.ragged_lengths(64, 64, 1024, 16384)
+    r, got = run(O, attn, torch_mod, lens, 64)
+    ref = O.ragged_f64(r["q"], r["gate"], r["k"], r["v"], r["offsets"], lens)
+    st = O.compare(got, ref)
+    report(f"C5 sum_len={int(lens.sum())}", st)
+    assert st["ok"], st
+
+
+def test_ragged_edges(O, attn, torch_mod):
+    """Lengths at and around the span unit and chunk boundaries, a single-key sequence, and a
+    max_len below the true maximum (spans grow instead of keys being dropped)."""
+    lens = np.array([1, 7, 8, 9, 511, 512, 513, 2049, 3], np.uint32)
+    for max_len in (None, 600):
+        r, got = run(O, attn, torch_mod, lens, 5, max_len)
+        ref = O.ragged_f64(r["q"], r["gate"], r["k"], r["v"], r["offsets"], lens)
+        st = O.compare(got, ref)
+        assert st["ok"], (max_len, st)
+
+
+def test_ragged_empty_sequence_is_zero(O, attn, torch_mod):
+    lens = np.array([5, 0, 9], np.uint32)
+    r, got = run(O, attn, torch_mod, lens, 6, 16)
+    assert not got[1].any()
+    ref = O.ragged_f64(r["q"], r["gate"], r["k"], r["v"], r["offsets"],
+                       np.array([5, 1, 9], np.uint32))
+    for s in (0, 2):
+        assert O.compare(got[s], ref[s])["ok"]
