@@ -169,7 +169,7 @@ struct Unit {
   uint4 k[4], v[4];
 };
 
-__device__ inline void load_unit(Unit& u, const attn::half_t* K, const attn::half_t* V,
+__device__ __attribute__((always_inline)) inline void load_unit(Unit& u, const attn::half_t* K, const attn::half_t* V,
                                  unsigned u0, unsigned last_row, unsigned lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -190,7 +190,7 @@ struct WaveState {
 
 // Online-softmax update of one unit. qh[h][j]: the lane's query slice (dims 8c + 2j, 8c + 2j + 1)
 // of head h, pre-scaled by log2(e)/16, as f16 pairs.
-__device__ inline void process_unit(WaveState& st, const Unit& u, const half2_t (&qh)[kGroup][4],
+__device__ __attribute__((always_inline)) inline void process_unit(WaveState& st, const Unit& u, const half2_t (&qh)[kGroup][4],
                                     unsigned u0, unsigned span_end, _Float16 (*pbuf)[2][kGroup][2],
                                     unsigned lane) {
   const unsigned c = lane & 31u, a = lane >> 5;
@@ -265,8 +265,9 @@ __device__ inline void process_unit(WaveState& st, const Unit& u, const half2_t 
 
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh, written at `base` (=
 // kvh * n_splits + split) in the reference's partial layout. Each wave streams every fourth unit
-// with a one-unit register prefetch; the four waves merge through LDS at the end.
-__device__ inline void split_partial(const float* __restrict__ q, const attn::half_t* K,
+// through a kDepth-unit register ring; the four waves merge through LDS at the end.
+constexpr int kDepth = 4;
+__device__ __attribute__((always_inline)) inline void split_partial(const float* __restrict__ q, const attn::half_t* K,
                                      const attn::half_t* V, unsigned len, AttnSpan span,
                                      unsigned kvh, float* part_m, float* part_l, float* part_o,
                                      std::size_t base, SplitShared& sh) {
@@ -292,23 +293,30 @@ __device__ inline void split_partial(const float* __restrict__ q, const attn::ha
     for (int e = 0; e < 8; ++e)
       st.o[h][e] = 0.0f;
 
+  // Register ring of kDepth units: while unit t is processed, units t + 1 .. t + kDepth - 1
+  // are in flight (kDepth - 1 units = 8 (kDepth - 1) KiB per wave).
   const unsigned last_row = len - 1;
   constexpr unsigned kStride = kWaves * kAttnDecodeUnit;
   unsigned u0 = span.begin + wave * kAttnDecodeUnit;
-  Unit ua, ub;
-  if (u0 < span.end)
-    load_unit(ua, K, V, u0, last_row, lane);
-  while (u0 < span.end) {
-    if (u0 + kStride < span.end)
-      load_unit(ub, K, V, u0 + kStride, last_row, lane);
-    process_unit(st, ua, qh, u0, span.end, sh.p[wave], lane);
-    u0 += kStride;
-    if (u0 >= span.end)
-      break;
-    if (u0 + kStride < span.end)
-      load_unit(ua, K, V, u0 + kStride, last_row, lane);
-    process_unit(st, ub, qh, u0, span.end, sh.p[wave], lane);
-    u0 += kStride;
+  Unit ring[kDepth];
+#pragma unroll
+  for (int i = 0; i + 1 < kDepth; ++i)
+    if (u0 + i * kStride < span.end)
+      load_unit(ring[i], K, V, u0 + i * kStride, last_row, lane);
+  bool more = u0 < span.end;
+  while (more) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
+      if (u0 >= span.end) {
+        more = false;
+        break;
+      }
+      const unsigned ahead = u0 + (kDepth - 1) * kStride;
+      if (ahead < span.end)
+        load_unit(ring[(j + kDepth - 1) % kDepth], K, V, ahead, last_row, lane);
+      process_unit(st, ring[j], qh, u0, span.end, sh.p[wave], lane);
+      u0 += kStride;
+    }
   }
 
   // Wave totals: l over the head's 8 lanes; o over the two row parities. swap32 of heads
@@ -409,34 +417,49 @@ struct AttnCombineParams {
 
 namespace decode_detail {
 
-// The merge of one (head, dim) in the reference's frozen FP32 order: M = max_c m_c; for c in split
-// order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o); core = o / L / (1 + __expf(
-// -gate)). Every template variant and the fused decode use exactly this sequence, so they are
-// bit-identical to one another. The o loads are issued four splits ahead of their FMAs.
-__device__ inline float combine_one(const float* __restrict__ pm, const float* __restrict__ pl,
-                                    const float* __restrict__ po, unsigned n_splits,
-                                    unsigned stride_m, float gate) {
+// The merge of one head at dimension d, computed by a full wave whose 64 lanes own 64 adjacent
+// dimensions of the same head. The result follows the reference's frozen FP32 order exactly:
+// M = max_c m_c; for c in split order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o);
+// core = o / L / (1 + __expf(-gate)). Lanes first own splits (lane c of each 64-split chunk) to
+// load m_c, l_c and form w_c in parallel -- a max is order-free and each w_c depends only on m_c
+// and M -- and the ordered FMA chain then takes w_c, l_c from that lane (readlane) while the o_c
+// loads are issued eight splits ahead. Every template variant and batched path uses this routine,
+// so all are bit-identical to one another and to a one-thread-per-dimension serial loop.
+__device__ __attribute__((always_inline)) inline float combine_wave(const float* __restrict__ pm, const float* __restrict__ pl,
+                                     const float* __restrict__ po, unsigned n_splits,
+                                     unsigned stride_m, float gate) {
+  const unsigned lane = cdna4::lane_id();
   float M = -__builtin_inff();
-  for (unsigned c = 0; c < n_splits; ++c)
+  for (unsigned c = lane; c < n_splits; c += cdna4::kLanes)
     M = fmaxf(M, pm[c * stride_m]);
+  M = cdna4::wave_allmax(M);
   float L = 0.0f, o = 0.0f;
-  unsigned c = 0;
-  for (; c + 4 <= n_splits; c += 4) {
-    float ov[4];
+  for (unsigned base = 0; base < n_splits; base += cdna4::kLanes) {
+    const unsigned mine = base + lane;
+    const float w_l = mine < n_splits ? __expf(pm[mine * stride_m] - M) : 0.0f;
+    const float l_l = mine < n_splits ? pl[mine * stride_m] : 0.0f;
+    const unsigned cnt = n_splits - base < cdna4::kLanes ? n_splits - base : cdna4::kLanes;
+    const float* oc = po + std::size_t{base} * stride_m * attn::kDim;
+    unsigned j = 0;
+    for (; j + 8 <= cnt; j += 8) {
+      float ov[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      ov[r] = po[std::size_t{c + r} * stride_m * attn::kDim];
+      for (int r = 0; r < 8; ++r)
+        ov[r] = oc[std::size_t{j + r} * stride_m * attn::kDim];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float w = __expf(pm[(c + r) * stride_m] - M);
-      L = __builtin_fmaf(w, pl[(c + r) * stride_m], L);
-      o = __builtin_fmaf(w, ov[r], o);
+      for (int r = 0; r < 8; ++r) {
+        const float w = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(w_l), j + r));
+        const float l = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(l_l), j + r));
+        L = __builtin_fmaf(w, l, L);
+        o = __builtin_fmaf(w, ov[r], o);
+      }
     }
-  }
-  for (; c < n_splits; ++c) {
-    const float w = __expf(pm[c * stride_m] - M);
-    L = __builtin_fmaf(w, pl[c * stride_m], L);
-    o = __builtin_fmaf(w, po[std::size_t{c} * stride_m * attn::kDim], o);
+    for (; j < cnt; ++j) {
+      const float w = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(w_l), j));
+      const float l = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(l_l), j));
+      L = __builtin_fmaf(w, l, L);
+      o = __builtin_fmaf(w, oc[std::size_t{j} * stride_m * attn::kDim], o);
+    }
   }
   return o / L / (1.0f + __expf(-gate));
 }
@@ -457,7 +480,7 @@ __device__ void attn_combine_op(const AttnCombineParams& p, unsigned first, unsi
     const unsigned h = item / kTiles, d = (item % kTiles) * kBlock + threadIdx.x;
     const unsigned kvh = h / kGroup, hl = h % kGroup;
     const std::size_t i0 = std::size_t{kvh} * p.n_splits * kGroup + hl;
-    p.core[h * kDim + d] = decode_detail::combine_one(
+    p.core[h * kDim + d] = decode_detail::combine_wave(
         p.part_m + i0, p.part_l + i0, p.part_o + i0 * kDim + d, p.n_splits, kGroup,
         p.qg[h * 2 * kDim + kDim + d]);
   }
@@ -524,7 +547,7 @@ __global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedPar
                                sh);
 }
 
-// One 64-thread workgroup per (sequence, head, 64-dim tile); the merge order is combine_one's.
+// One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's.
 __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParams p) {
   constexpr unsigned kGroup = attn::kQHeads / attn::kKvHeads, kTiles = attn::kDim / 64;
   const unsigned item = blockIdx.x;
@@ -540,7 +563,7 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
   }
   const unsigned kvh = h / kGroup, hl = h % kGroup;
   const std::size_t i0 = (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max * kGroup + hl;
-  p.core[out] = decode_detail::combine_one(p.part_m + i0, p.part_l + i0,
+  p.core[out] = decode_detail::combine_wave(p.part_m + i0, p.part_l + i0,
                                            p.part_o + i0 * attn::kDim + d, n_splits, kGroup,
                                            p.gate[out]);
 }

@@ -97,6 +97,47 @@ __device__ inline float lane_xor32(float v) {
   return lane_id() < 32 ? p.b : p.a;
 }
 
+// ------------------------------------------------------------------------------------------------
+// Direct global -> LDS loads (gfx950 global_load_lds_dwordx4).
+//
+// One instruction moves 16 bytes per lane: lane i's global address -> LDS byte lds_base + 16 i
+// (lds_base is wave-uniform and travels in M0; an instruction offset would shift both addresses,
+// so none is used). The load is issued from inline assembly and waited for with an explicit
+// vmcnt: the compiler then neither tracks it nor inserts its own conservative full wait before
+// later LDS reads. An explicit vmcnt(n) is always safe as long as n counts only the LDS loads this
+// wave issued after the one being waited for -- any other vector-memory op in between only makes
+// the wait stricter, since vmcnt drains in issue order.
+// ------------------------------------------------------------------------------------------------
+
+__device__ inline unsigned lds_offset(const void* p) {
+  return static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+
+// M0 is saved and restored around the load, so code the compiler generated around it keeps
+// whatever M0 held.
+__device__ __attribute__((always_inline)) inline void lds_load16(const void* gaddr,
+                                                                 unsigned lds_base) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gaddr), "s"(lds_base)
+      : "memory");
+}
+
+// Wait until at most N vector-memory ops of this wave are outstanding (LDS and VGPR loads both
+// count); also a compiler barrier for memory.
+template <int N>
+__device__ __attribute__((always_inline)) inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 // One reduce-scatter step over a pair of values (lo, hi). Lanes whose class bit is clear keep
 // lo + partner's lo; lanes whose bit is set keep hi + partner's hi. The partner (given by
 // `exchange`) always has the opposite class bit.
@@ -112,7 +153,7 @@ __device__ inline float scatter_step(float lo, float hi, bool upper, Exchange ex
 // lane c returns sum over the 32 lanes c' of its half of v[c'][c]: the complete value with index
 // c. Exchanges: lane ^ 16 (swap16), lane ^ 8, the 8-lane mirror (pairs i with 7 - i, so the opposite bit 2),
 // lane ^ 2, lane ^ 1 -- every original lane is summed exactly once.
-__device__ inline float reduce_scatter32(float (&v)[32]) {
+__device__ __attribute__((always_inline)) inline float reduce_scatter32(float (&v)[32]) {
   const unsigned c = lane_id() & 31u;
   float r16[16], r8[8], r4[4], r2[2];
 #pragma unroll
