@@ -153,46 +153,88 @@ using cdna4::half2_t;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.693147180559945309417f;
 constexpr int kGroup = attn::kQHeads / attn::kKvHeads;  // 8 query heads per KV head
-constexpr int kWaves = 4;                               // 256-thread workgroup
+constexpr int kWaves = 4;                               // 256-thread workgroup (header API)
 
-// LDS of one split workgroup: per-wave softmax numerators (f16 pairs) and the cross-wave merge.
-struct SplitShared {
-  _Float16 p[kWaves][2][2][kGroup][2];  // [wave][row parity][pair][head][row of the pair]
-  float o[kWaves][kGroup][attn::kDim];
-  float m[kWaves][kGroup];
-  float l[kWaves][kGroup];
+constexpr int kRing = 4;                    // units per wave in the LDS ring (4-wave workgroups)
+constexpr unsigned kUnitBytes = 8192;       // 8 rows of K + 8 rows of V
+constexpr float kRescaleSlack = 8.0f;       // log2 units: numerators stay <= 2^8 between rescales
+
+// LDS of one split workgroup: each wave's ring of K/V units (direct global->LDS loads), the query
+// rows, per-wave softmax numerators (f16 pairs); the cross-wave merge reuses the ring.
+template <int W, int R>
+struct SplitSharedT {
+  static constexpr int kWaveCount = W, kRingUnits = R;
+  union {
+    unsigned char ring[W][R][kUnitBytes];
+    struct {
+      float o[W][kGroup][attn::kDim];
+      float m[W][kGroup];
+      float mt[W][kGroup];
+      float l[W][kGroup];
+    } merge;
+  };
+  float q[kGroup][attn::kDim];
+  _Float16 p[W][2][2][kGroup][2];  // [wave][row parity][pair][head][row of the pair]
 };
+using SplitShared = SplitSharedT<kWaves, kRing>;  // 4 waves x 4 units: 136.5 KiB
 
 // A unit: rows u0 + 2 i + (lane / 32), i = 0..3, bytes [16 c, 16 c + 16) of each row (c = lane %
-// 32). One 16-byte load per row-pair covers 1 KiB contiguous: fully coalesced.
+// 32), for K and for V. In global memory each row pair is 1 KiB contiguous; in the ring slot,
+// K row pair i is at byte 1024 i and V row pair i at 4096 + 1024 i, lane-linear, so a lane's 16
+// bytes land exactly where it reads them back.
 struct Unit {
   uint4 k[4], v[4];
 };
 
-__device__ __attribute__((always_inline)) inline void load_unit(Unit& u, const attn::half_t* K, const attn::half_t* V,
-                                 unsigned u0, unsigned last_row, unsigned lane) {
+__device__ __attribute__((always_inline)) inline void load_unit(
+    const attn::half_t* K, const attn::half_t* V, unsigned u0, unsigned last_row,
+    unsigned slot_lds, unsigned lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     unsigned row = u0 + 2 * i + (lane >> 5);
     row = row < last_row ? row : last_row;  // rows past the span are masked, never out of bounds
     const std::size_t at = std::size_t{row} * attn::kDim + (lane & 31u) * 8;
-    u.k[i] = *reinterpret_cast<const uint4*>(K + at);
-    u.v[i] = *reinterpret_cast<const uint4*>(V + at);
+    cdna4::lds_load16(K + at, slot_lds + 1024 * i);
+    cdna4::lds_load16(V + at, slot_lds + 4096 + 1024 * i);
   }
 }
 
-// Running state of one wave: head h's max (log2 units) and sum live in the 8 lanes whose
-// (lane % 32) / 4 == h; o[h][e] is this lane's share of head h at dims 8 c + e for its row parity.
+__device__ __attribute__((always_inline)) inline Unit read_unit(const unsigned char* slot,
+                                                                unsigned lane) {
+  Unit u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u.k[i] = *reinterpret_cast<const uint4*>(slot + 1024 * i + 16 * lane);
+    u.v[i] = *reinterpret_cast<const uint4*>(slot + 4096 + 1024 * i + 16 * lane);
+  }
+  return u;
+}
+
+// Wait until the unit whose loads were followed by `after` (< 4) more units' loads has landed.
+__device__ __attribute__((always_inline)) inline void wait_units_after(unsigned after) {
+  switch (after) {
+    case 0: cdna4::wait_vmcnt<0>(); break;
+    case 1: cdna4::wait_vmcnt<8>(); break;
+    case 2: cdna4::wait_vmcnt<16>(); break;
+    default: cdna4::wait_vmcnt<24>(); break;
+  }
+}
+
+// Running state of one wave: head h's reference max m, true max mt (log2 units) and sum l live in
+// the 8 lanes whose (lane % 32) / 4 == h; o[h][e] is this lane's share of head h at dims 8 c + e for
+// its row parity. l and o are relative to m.
 struct WaveState {
-  float m, l;
+  float m, mt, l;
   float o[kGroup][8];
 };
 
 // Online-softmax update of one unit. qh[h][j]: the lane's query slice (dims 8c + 2j, 8c + 2j + 1)
-// of head h, pre-scaled by log2(e)/16, as f16 pairs.
-__device__ __attribute__((always_inline)) inline void process_unit(WaveState& st, const Unit& u, const half2_t (&qh)[kGroup][4],
-                                    unsigned u0, unsigned span_end, _Float16 (*pbuf)[2][kGroup][2],
-                                    unsigned lane) {
+// of head h, pre-scaled by log2(e)/16, as f16 pairs. The reference max m moves only when a score
+// exceeds it by more than kRescaleSlack (then o and l are rescaled exactly), so numerators
+// exp2(s - m) stay below 2^kRescaleSlack and most units skip the rescale.
+__device__ __attribute__((always_inline)) inline void process_unit(
+    WaveState& st, const Unit& u, const half2_t (&qh)[kGroup][4], unsigned u0, unsigned span_end,
+    _Float16 (*pbuf)[2][kGroup][2], unsigned lane) {
   const unsigned c = lane & 31u, a = lane >> 5;
   // Scores: partial dot products over this lane's 8 dims, then a reduce-scatter over the 32
   // lanes of the row parity leaves the complete score of (head c / 4, row u0 + 2 (c % 4) + a).
@@ -214,22 +256,16 @@ __device__ __attribute__((always_inline)) inline void process_unit(WaveState& st
   if (my_row >= span_end)
     s = -__builtin_inff();
   // Head max over its 8 lanes (quad of rows, both parities). Row u0 is always in the span, so
-  // every head has at least one finite score and m_new is finite.
+  // every head has at least one finite score.
   float mu = fmaxf(s, cdna4::dpp_mov<cdna4::kQuadXor1>(s));
   mu = fmaxf(mu, cdna4::dpp_mov<cdna4::kQuadXor2>(mu));
   mu = cdna4::max_xor32(mu);
-  const float m_new = fmaxf(st.m, mu);
-  const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first unit (m = -inf)
-  const float pj = __builtin_amdgcn_exp2f(s - m_new);       // 0 for masked rows
-  st.l = st.l * corr + pj;
-  st.m = m_new;
-  // Numerators to LDS as f16: slot [parity a][pair (row index % 2)][head][row index / 2].
-  {
-    const unsigned ri = c & 3u, h = c >> 2;
-    pbuf[a][ri & 1u][h][ri >> 1] = static_cast<_Float16>(pj);
-  }
-  // Rescale the accumulators when some head's max moved (wave-uniform branch).
-  if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+  st.mt = fmaxf(st.mt, mu);
+  if (__builtin_amdgcn_ballot_w64(mu > st.m + kRescaleSlack)) {  // wave-uniform branch
+    const float m_new = fmaxf(st.m, mu);
+    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first unit (m = -inf)
+    st.l *= corr;
+    st.m = m_new;
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) {
       const float ch = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), 4 * h));
@@ -237,6 +273,13 @@ __device__ __attribute__((always_inline)) inline void process_unit(WaveState& st
       for (int e = 0; e < 8; ++e)
         st.o[h][e] *= ch;
     }
+  }
+  const float pj = __builtin_amdgcn_exp2f(s - st.m);  // 0 for masked rows
+  st.l += pj;
+  // Numerators to LDS as f16: slot [parity a][pair (row index % 2)][head][row index / 2].
+  {
+    const unsigned ri = c & 3u, h = c >> 2;
+    pbuf[a][ri & 1u][h][ri >> 1] = static_cast<_Float16>(pj);
   }
   // P V: rows (i, i + 2) of the parity pair up in one dot2 per (head, dim).
   half2_t pp[2][kGroup];
@@ -264,21 +307,46 @@ __device__ __attribute__((always_inline)) inline void process_unit(WaveState& st
 }
 
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh, written at `base` (=
-// kvh * n_splits + split) in the reference's partial layout. Each wave streams every fourth unit
-// through a kDepth-unit register ring; the four waves merge through LDS at the end.
-constexpr int kDepth = 4;
-__device__ __attribute__((always_inline)) inline void split_partial(const float* __restrict__ q, const attn::half_t* K,
-                                     const attn::half_t* V, unsigned len, AttnSpan span,
-                                     unsigned kvh, float* part_m, float* part_l, float* part_o,
-                                     std::size_t base, SplitShared& sh) {
-  const unsigned t = threadIdx.x, lane = t & 63u, wave = t >> 6, c = lane & 31u;
+// kvh * n_splits + split) in the reference's partial layout. Wave w streams units w, w + 4, ...
+// of the span through its kRing-unit LDS ring (kRing - 1 units in flight while one is processed);
+// the four waves merge through LDS at the end. Every vector-memory load of the kernel is a direct
+// LDS load with an explicit wait.
+template <class Shared>
+__device__ __attribute__((always_inline)) inline void split_partial(
+    const float* __restrict__ q, const attn::half_t* K, const attn::half_t* V, unsigned len,
+    AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base,
+    Shared& sh) {
+  constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
+  static_assert(kR >= 2 && kR <= 4 && kGroup % kW == 0, "ring depth / wave count");
+  const unsigned t = threadIdx.x, lane = t & 63u, c = lane & 31u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const unsigned last_row = len - 1;
+  constexpr unsigned kStride = kW * kAttnDecodeUnit;
+  const unsigned first = span.begin + wave * kAttnDecodeUnit;
+  const unsigned n_units = first < span.end ? (span.end - first + kStride - 1) / kStride : 0;
+  const unsigned ring0 = cdna4::lds_offset(sh.ring[wave][0]);
+
+  // This wave's query heads of the KV head (1 KiB each), then the first kR - 1 units.
+  constexpr int kHeadsPerWave = kGroup / kW;
+#pragma unroll
+  for (int i = 0; i < kHeadsPerWave; ++i) {
+    const unsigned h = kHeadsPerWave * wave + i;
+    cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
+                      cdna4::lds_offset(sh.q[h]));
+  }
+#pragma unroll
+  for (unsigned k = 0; k + 1 < kR; ++k)
+    if (k < n_units)
+      load_unit(K, V, first + k * kStride, last_row, ring0 + k * kUnitBytes, lane);
+  wait_units_after(n_units < kR - 1 ? n_units : kR - 1);  // the query loads are older
+  __syncthreads();
+
   half2_t qh[kGroup][4];
   constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
 #pragma unroll
   for (int h = 0; h < kGroup; ++h) {
-    const float4* src =
-        reinterpret_cast<const float4*>(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 8 * c);
-    const float4 x0 = src[0], x1 = src[1];
+    const float4 x0 = *reinterpret_cast<const float4*>(&sh.q[h][8 * c]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&sh.q[h][8 * c + 4]);
     qh[h][0] = half2_t{static_cast<_Float16>(x0.x * kScale), static_cast<_Float16>(x0.y * kScale)};
     qh[h][1] = half2_t{static_cast<_Float16>(x0.z * kScale), static_cast<_Float16>(x0.w * kScale)};
     qh[h][2] = half2_t{static_cast<_Float16>(x1.x * kScale), static_cast<_Float16>(x1.y * kScale)};
@@ -286,6 +354,7 @@ __device__ __attribute__((always_inline)) inline void split_partial(const float*
   }
   WaveState st;
   st.m = -__builtin_inff();
+  st.mt = -__builtin_inff();
   st.l = 0.0f;
 #pragma unroll
   for (int h = 0; h < kGroup; ++h)
@@ -293,30 +362,15 @@ __device__ __attribute__((always_inline)) inline void split_partial(const float*
     for (int e = 0; e < 8; ++e)
       st.o[h][e] = 0.0f;
 
-  // Register ring of kDepth units: while unit t is processed, units t + 1 .. t + kDepth - 1
-  // are in flight (kDepth - 1 units = 8 (kDepth - 1) KiB per wave).
-  const unsigned last_row = len - 1;
-  constexpr unsigned kStride = kWaves * kAttnDecodeUnit;
-  unsigned u0 = span.begin + wave * kAttnDecodeUnit;
-  Unit ring[kDepth];
-#pragma unroll
-  for (int i = 0; i + 1 < kDepth; ++i)
-    if (u0 + i * kStride < span.end)
-      load_unit(ring[i], K, V, u0 + i * kStride, last_row, lane);
-  bool more = u0 < span.end;
-  while (more) {
-#pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      if (u0 >= span.end) {
-        more = false;
-        break;
-      }
-      const unsigned ahead = u0 + (kDepth - 1) * kStride;
-      if (ahead < span.end)
-        load_unit(ring[(j + kDepth - 1) % kDepth], K, V, ahead, last_row, lane);
-      process_unit(st, ring[j], qh, u0, span.end, sh.p[wave], lane);
-      u0 += kStride;
-    }
+  for (unsigned k = 0; k < n_units; ++k) {
+    const unsigned ahead = k + kR - 1;
+    if (ahead < n_units)  // its slot held unit k - 1, already read back into registers
+      load_unit(K, V, first + ahead * kStride, last_row, ring0 + (ahead % kR) * kUnitBytes,
+                lane);
+    const unsigned after = n_units - 1 - k;
+    wait_units_after(after < kR - 1 ? after : kR - 1);
+    const Unit u = read_unit(sh.ring[wave][k % kR], lane);
+    process_unit(st, u, qh, first + k * kStride, span.end, sh.p[wave], lane);
   }
 
   // Wave totals: l over the head's 8 lanes; o over the two row parities. swap32 of heads
@@ -324,6 +378,7 @@ __device__ __attribute__((always_inline)) inline void split_partial(const float*
   float l = st.l + cdna4::dpp_mov<cdna4::kQuadXor1>(st.l);
   l += cdna4::dpp_mov<cdna4::kQuadXor2>(l);
   l = cdna4::sum_xor32(l);
+  __syncthreads();  // every wave is done with its ring: the merge area aliases it
   {
     const unsigned a = lane >> 5;
 #pragma unroll
@@ -334,42 +389,47 @@ __device__ __attribute__((always_inline)) inline void split_partial(const float*
         const cdna4::Pair pr = cdna4::swap32(st.o[h][e], st.o[h + kGroup / 2][e]);
         tot[e] = pr.a + pr.b;
       }
-      float4* dst = reinterpret_cast<float4*>(&sh.o[wave][h + a * (kGroup / 2)][8 * c]);
+      float4* dst = reinterpret_cast<float4*>(&sh.merge.o[wave][h + a * (kGroup / 2)][8 * c]);
       dst[0] = float4{tot[0], tot[1], tot[2], tot[3]};
       dst[1] = float4{tot[4], tot[5], tot[6], tot[7]};
     }
   }
   if (lane < 32 && (c & 3u) == 0) {
-    sh.m[wave][c >> 2] = st.m;
-    sh.l[wave][c >> 2] = l;
+    sh.merge.m[wave][c >> 2] = st.m;
+    sh.merge.mt[wave][c >> 2] = st.mt;
+    sh.merge.l[wave][c >> 2] = l;
   }
   __syncthreads();
-  // Merge the four waves: thread t owns head t / 32, dims 8 (t % 32) .. + 8.
+  // Merge the waves relative to the split's true max M: the kW * 64 threads split into 8 heads x
+  // kTh threads of kDims dims. The partial is then exactly (max, sum exp(s - max), sum exp(s -
+  // max) v).
   {
-    const unsigned h = t >> 5, d0 = 8 * (t & 31u);
+    constexpr unsigned kTh = kW * 64 / kGroup, kDims = attn::kDim / kTh;
+    const unsigned h = t / kTh, d0 = kDims * (t % kTh);
     float M = -__builtin_inff();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      M = fmaxf(M, sh.m[w][h]);
-    float L = 0.0f, o[8] = {};
+    for (int w = 0; w < kW; ++w)
+      M = fmaxf(M, sh.merge.mt[w][h]);
+    float L = 0.0f, o[kDims] = {};
     if (M != -__builtin_inff()) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float sc = __builtin_amdgcn_exp2f(sh.m[w][h] - M);
-        L += sc * sh.l[w][h];
+      for (int w = 0; w < kW; ++w) {
+        const float sc = __builtin_amdgcn_exp2f(sh.merge.m[w][h] - M);
+        L += sc * sh.merge.l[w][h];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          o[e] += sc * sh.o[w][h][d0 + e];
+        for (unsigned e = 0; e < kDims; ++e)
+          o[e] += sc * sh.merge.o[w][h][d0 + e];
       }
     }
     const std::size_t at = base * kGroup + h;
-    if ((t & 31u) == 0) {
+    if (t % kTh == 0) {
       part_m[at] = M * kLn2;  // -inf stays -inf for an empty span
       part_l[at] = L;
     }
     float4* dst = reinterpret_cast<float4*>(part_o + at * attn::kDim + d0);
-    dst[0] = float4{o[0], o[1], o[2], o[3]};
-    dst[1] = float4{o[4], o[5], o[6], o[7]};
+#pragma unroll
+    for (unsigned e = 0; e < kDims; e += 4)
+      dst[e / 4] = float4{o[e], o[e + 1], o[e + 2], o[e + 3]};
   }
   __syncthreads();  // LDS is reused by the next item
 }
@@ -402,6 +462,22 @@ __global__ void __launch_bounds__(kBlock) attn_split_kernel(AttnSplitParams p) {
   attn_split_op<kBlock>(p, 0, attn::kKvHeads * p.n_splits);
 }
 
+// The same split partials from 512-thread workgroups (8 waves, two per SIMD, 2-unit rings): one
+// workgroup per (KV head, split), grid dim3(n_splits, 2). A second resident wave per SIMD hides
+// the dependency stalls of the first.
+__global__ void __launch_bounds__(512) attn_split_wide_kernel(AttnSplitParams p) {
+  __shared__ decode_detail::SplitSharedT<8, 2> sh;
+  const unsigned item = blockIdx.y * gridDim.x + blockIdx.x;
+  if (item >= attn::kKvHeads * p.n_splits)
+    return;
+  const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
+  const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
+  const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
+  decode_detail::split_partial(p.q, K, V, p.len, attn_split_span(p.len, p.n_splits, split), kvh,
+                               p.part_m, p.part_l, p.part_o,
+                               std::size_t{kvh} * p.n_splits + split, sh);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Combine: LSE merge x sigmoid gate (reference: kernels/attention_decode.hpp:238-309)
 // ------------------------------------------------------------------------------------------------
@@ -420,46 +496,56 @@ namespace decode_detail {
 // The merge of one head at dimension d, computed by a full wave whose 64 lanes own 64 adjacent
 // dimensions of the same head. The result follows the reference's frozen FP32 order exactly:
 // M = max_c m_c; for c in split order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o);
-// core = o / L / (1 + __expf(-gate)). Lanes first own splits (lane c of each 64-split chunk) to
-// load m_c, l_c and form w_c in parallel -- a max is order-free and each w_c depends only on m_c
-// and M -- and the ordered FMA chain then takes w_c, l_c from that lane (readlane) while the o_c
-// loads are issued eight splits ahead. Every template variant and batched path uses this routine,
-// so all are bit-identical to one another and to a one-thread-per-dimension serial loop.
-__device__ __attribute__((always_inline)) inline float combine_wave(const float* __restrict__ pm, const float* __restrict__ pl,
-                                     const float* __restrict__ po, unsigned n_splits,
-                                     unsigned stride_m, float gate) {
+// core = o / L / (1 + __expf(-gate)). Split statistics are per head, hence the same for the whole
+// wave: lane c of each 64-split chunk loads m_c, l_c and forms w_c (a max is order-free and w_c
+// depends only on m_c and M), the wave publishes (w_c, l_c) through LDS, and every lane then runs
+// the ordered FMA chain over the chunk with all 64 o_c loads already in flight. A chunk past the
+// last split is padded with w = 0 and a clamped, finite o: fma(0, x, acc) == acc exactly, so the
+// padding cannot change a bit. Every template variant and the batched path use this routine, so
+// all are bit-identical to one another and to a one-thread-per-dimension serial loop.
+struct CombineLds {
+  float w[cdna4::kLanes], l[cdna4::kLanes];
+};
+
+__device__ __attribute__((always_inline)) inline float combine_wave(
+    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po,
+    unsigned n_splits, float gate, CombineLds& lds) {
+  constexpr unsigned kChunk = cdna4::kLanes, kStride = kGroup;  // partial rows per split
+  constexpr std::size_t kOStride = std::size_t{kStride} * attn::kDim;
   const unsigned lane = cdna4::lane_id();
   float M = -__builtin_inff();
-  for (unsigned c = lane; c < n_splits; c += cdna4::kLanes)
-    M = fmaxf(M, pm[c * stride_m]);
+  for (unsigned c = lane; c < n_splits; c += kChunk)
+    M = fmaxf(M, pm[c * kStride]);
   M = cdna4::wave_allmax(M);
+  const unsigned last = n_splits - 1;
   float L = 0.0f, o = 0.0f;
-  for (unsigned base = 0; base < n_splits; base += cdna4::kLanes) {
+  for (unsigned base = 0; base < n_splits; base += kChunk) {
+    float ov[kChunk];
+#pragma unroll
+    for (unsigned r = 0; r < kChunk; ++r) {
+      const unsigned c = base + r < last ? base + r : last;
+      ov[r] = po[c * kOStride];
+    }
     const unsigned mine = base + lane;
-    const float w_l = mine < n_splits ? __expf(pm[mine * stride_m] - M) : 0.0f;
-    const float l_l = mine < n_splits ? pl[mine * stride_m] : 0.0f;
-    const unsigned cnt = n_splits - base < cdna4::kLanes ? n_splits - base : cdna4::kLanes;
-    const float* oc = po + std::size_t{base} * stride_m * attn::kDim;
-    unsigned j = 0;
-    for (; j + 8 <= cnt; j += 8) {
-      float ov[8];
+    const float w_l = mine < n_splits ? __expf(pm[mine * kStride] - M) : 0.0f;
+    const float l_l = mine < n_splits ? pl[mine * kStride] : 0.0f;
+    lds.w[lane] = w_l;
+    lds.l[lane] = l_l;
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-        ov[r] = oc[std::size_t{j + r} * stride_m * attn::kDim];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float w = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(w_l), j + r));
-        const float l = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(l_l), j + r));
-        L = __builtin_fmaf(w, l, L);
-        o = __builtin_fmaf(w, ov[r], o);
-      }
+    for (unsigned r = 0; r < kChunk; r += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
+      const float4 l4 = *reinterpret_cast<const float4*>(&lds.l[r]);
+      L = __builtin_fmaf(w4.x, l4.x, L);
+      o = __builtin_fmaf(w4.x, ov[r], o);
+      L = __builtin_fmaf(w4.y, l4.y, L);
+      o = __builtin_fmaf(w4.y, ov[r + 1], o);
+      L = __builtin_fmaf(w4.z, l4.z, L);
+      o = __builtin_fmaf(w4.z, ov[r + 2], o);
+      L = __builtin_fmaf(w4.w, l4.w, L);
+      o = __builtin_fmaf(w4.w, ov[r + 3], o);
     }
-    for (; j < cnt; ++j) {
-      const float w = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(w_l), j));
-      const float l = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(l_l), j));
-      L = __builtin_fmaf(w, l, L);
-      o = __builtin_fmaf(w, oc[std::size_t{j} * stride_m * attn::kDim], o);
-    }
+    __builtin_amdgcn_wave_barrier();  // the next chunk overwrites the broadcast slots
   }
   return o / L / (1.0f + __expf(-gate));
 }
@@ -476,13 +562,14 @@ __device__ void attn_combine_op(const AttnCombineParams& p, unsigned first, unsi
   static_assert(kBlock % cdna4::kLanes == 0 && kDim % kBlock == 0);
   static_assert(!kPrepared || kBlock == cdna4::kLanes);
   static_assert(kPipeline == 1 || (kPrepared && kPipeline == 4));
+  __shared__ decode_detail::CombineLds lds[kBlock / cdna4::kLanes];
   for (unsigned item = first + blockIdx.x; item < first + count; item += gridDim.x) {
     const unsigned h = item / kTiles, d = (item % kTiles) * kBlock + threadIdx.x;
     const unsigned kvh = h / kGroup, hl = h % kGroup;
     const std::size_t i0 = std::size_t{kvh} * p.n_splits * kGroup + hl;
     p.core[h * kDim + d] = decode_detail::combine_wave(
-        p.part_m + i0, p.part_l + i0, p.part_o + i0 * kDim + d, p.n_splits, kGroup,
-        p.qg[h * 2 * kDim + kDim + d]);
+        p.part_m + i0, p.part_l + i0, p.part_o + i0 * kDim + d, p.n_splits,
+        p.qg[h * 2 * kDim + kDim + d], lds[threadIdx.x / cdna4::kLanes]);
   }
 }
 
@@ -563,9 +650,10 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
   }
   const unsigned kvh = h / kGroup, hl = h % kGroup;
   const std::size_t i0 = (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max * kGroup + hl;
+  __shared__ decode_detail::CombineLds lds;
   p.core[out] = decode_detail::combine_wave(p.part_m + i0, p.part_l + i0,
-                                           p.part_o + i0 * attn::kDim + d, n_splits, kGroup,
-                                           p.gate[out]);
+                                           p.part_o + i0 * attn::kDim + d, n_splits, p.gate[out],
+                                           lds);
 }
 
 }  // namespace miso::kernels
