@@ -56,7 +56,22 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain 64 MiB device copies (counter calibration for "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
     return ap.parse_args()
+
+
+def copy_calibration(torch):
+    """Three device-to-device copies of exactly 64 MiB: the known-size reference that scales the
+    FETCH_SIZE / WRITE_SIZE counters of the attention kernels to HBM bytes."""
+    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("copy calibration: 3 x 64 MiB device copies")
 
 
 def graph_of(torch, fn, count):
@@ -242,6 +257,8 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.copy_calibration:
+        copy_calibration(torch)
     dec = bench_decode(torch, A, args)
     pre = None if args.no_prefill else bench_prefill(torch, A, args)
 

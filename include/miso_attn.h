@@ -8,7 +8,10 @@
  * repository (penta2himajin/miso).
  *
  * Conventions
- *   - Pointers are device pointers (hipMalloc'd or equivalent), 16-byte aligned.
+ *   - Pointers are device pointers (hipMalloc'd or equivalent). Every tensor pointer must be
+ *     non-NULL and 16-byte aligned (the kernels move 16 bytes per lane), except part_m / part_l
+ *     (4-byte aligned); a NULL or misaligned pointer is rejected with MISO_ATTN_EINVAL before
+ *     any launch.
  *   - f16 buffers hold IEEE binary16 bit patterns (uint16_t).
  *   - Shapes are fixed by the model: 16 query heads, 2 KV heads, head_dim 256; the KV cache is
  *     [2][max_ctx][256] per tensor (K and V separate).
@@ -18,7 +21,7 @@
  *     MISO_ATTN_EINVAL for arguments rejected on the host before any launch; the message is then
  *     available from miso_attn_last_error() (thread-local). The reference throws
  *     std::runtime_error in both situations (src/hip_util.hpp:12-17, src/engine/attention.hip:
- *     164-165, 203-204).
+ *     81-82, 110, 120-121, 145).
  */
 #ifndef MISO_ATTN_H
 #define MISO_ATTN_H
@@ -38,7 +41,7 @@ const char* miso_attn_last_error(void);
 const char* miso_attn_version(void);
 
 /* Split-count policy: replaces attn_n_splits(len, max_splits), kernels/attention_decode.hpp:92,
- * as used by src/engine/attention.hip:185. Returns 1 <= n <= max(max_splits, 1); 1 for len 0.
+ * as used by src/engine/attention.hip:102. Returns 1 <= n <= max(max_splits, 1); 1 for len 0.
  * The MI355X policy differs from the reference's MI50 tuning (same contract). */
 uint32_t miso_attn_n_splits(uint32_t len, uint32_t max_splits);
 
@@ -46,7 +49,7 @@ uint32_t miso_attn_n_splits(uint32_t len, uint32_t max_splits);
 uint32_t miso_attn_prefill_items(uint32_t n);
 
 /* Decode prep: replaces attn_prep_kernel<256><<<18, 256, 0, stream>>>(AttnPrepParams{...}),
- * src/engine/attention.hip:180-183 (kernels/attention_decode.hpp:19-83). Per-head RMSNorm of the
+ * src/engine/attention.hip:97-100 (kernels/attention_decode.hpp:19-83). Per-head RMSNorm of the
  * 16 query heads (qg, gate half untouched) and 2 key heads, NEOX RoPE on dims [0, 64) at `pos`,
  * writes q [16][256] and appends K/V at position pos of the caches. Rejects pos >= max_ctx. */
 int miso_attn_prep(const float* qg, const float* k, const float* v, const float* q_norm,
@@ -55,7 +58,7 @@ int miso_attn_prep(const float* qg, const float* k, const float* v, const float*
                    void* stream);
 
 /* Batched prep for n tokens: replaces attn_prep_batch_kernel<256><<<n * 18, 256, 0, stream>>>,
- * src/engine/attention.hip:218-223 (kernels/attention_prefill.hpp:20-40). Token t reads qg/k/v
+ * src/engine/attention.hip:133-139 (kernels/attention_prefill.hpp:20-40). Token t reads qg/k/v
  * at t * proj_stride floats, writes q at t * 4096 floats and the cache at pos0 + t.
  * Rejects pos0 + n > max_ctx. */
 int miso_attn_prep_batch(const float* qg, const float* k, const float* v, const float* q_norm,
@@ -64,7 +67,7 @@ int miso_attn_prep_batch(const float* qg, const float* k, const float* v, const 
                          uint32_t n, uint32_t proj_stride, void* stream);
 
 /* Split-K partials: replaces attn_split_kernel<256><<<dim3(n_splits, 2), 256, 0, stream>>>(
- * AttnSplitParams{...}), src/engine/attention.hip:186-189 and tests/test_attn_splitk.hip:125-134
+ * AttnSplitParams{...}), src/engine/attention.hip:103-106 and tests/test_attn_splitk.hip:125-134
  * (kernels/attention_decode.hpp:117-236). Writes part_m/part_l [2][n_splits][8] and part_o
  * [2][n_splits][8][256] for keys [0, len). Rejects len == 0, len > max_ctx, n_splits == 0. */
 int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -72,7 +75,7 @@ int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_c
                     uint32_t n_splits, void* stream);
 
 /* LSE merge x sigmoid gate: replaces attn_combine_kernel<64, true, 4><<<64, 64, 0, stream>>>(
- * AttnCombineParams{...}), src/engine/attention.hip:190-192 (kernels/attention_decode.hpp:
+ * AttnCombineParams{...}), src/engine/attention.hip:107-109 (kernels/attention_decode.hpp:
  * 238-309). core [16][256] = merge of the partials x 1 / (1 + exp(-gate)), gate at qg[h*512 +
  * 256 + d]. Bit-identical to the reference's frozen merge order. Rejects n_splits == 0. */
 int miso_attn_combine(const float* part_m, const float* part_l, const float* part_o,
@@ -89,7 +92,7 @@ int miso_attn_combine_variant(int variant, const float* part_m, const float* par
                               uint32_t n_splits, uint32_t first, uint32_t count, uint32_t grid,
                               void* stream);
 
-/* One decode step's attention: the split + combine pair of src/engine/attention.hip:185-192 in
+/* One decode step's attention: the split + combine pair of src/engine/attention.hip:102-109 in
  * one call, with n_splits chosen by the caller (miso_attn_n_splits(len, capacity)). The partial
  * buffers are caller-owned scratch of capacity >= n_splits. */
 int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
@@ -98,10 +101,11 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
                      void* stream);
 
 /* Causal prefill: replaces attn_prefill_kernel<256><<<attn_prefill_items(n), 256, 0, stream>>>(
- * AttnPrefillParams{...}), src/engine/attention.hip:225-227 and tests/test_attn_splitk.hip:224-233
+ * AttnPrefillParams{...}), src/engine/attention.hip:141-144 and tests/test_attn_splitk.hip:224-233
  * (kernels/attention_prefill.hpp:42-161). Tokens pos0 .. pos0 + n - 1; q [n][16][256] (unscaled),
  * gate at qg[t * qg_stride + h * 512 + 256 + d], keys [0, pos0 + n) already in the cache;
- * core [n][16][256]. Rejects n == 0, pos0 + n > max_ctx, qg_stride < 8192. */
+ * core [n][16][256]. Rejects n == 0, pos0 + n > max_ctx, qg_stride < 8192 or not a multiple of
+ * 4 (the gate is read 16 bytes at a time). */
 int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
                       const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
                       uint32_t max_ctx, uint32_t qg_stride, void* stream);
@@ -111,8 +115,9 @@ int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
  * q [batch][16][256] (unscaled), gate [batch][16][256], core [batch][16][256] = per-sequence
  * softmax(q K^T / 16) V x 1 / (1 + exp(-gate)). Sequence s has lens[s] keys stored contiguously
  * as K/V [2][lens[s]][256] (f16) starting kv_offsets[s] halves into k_cache / v_cache; lens and
- * kv_offsets are DEVICE arrays. max_len sizes the grid and the partial scratch: every sequence is
- * split into at most miso_attn_ragged_splits(max_len) spans (a longer sequence still gets all of
+ * kv_offsets are DEVICE arrays (not validated on the host: kv_offsets[s] must be a multiple of 8
+ * and the K/V of every sequence inside the caches). max_len sizes the grid and the partial
+ * scratch: every sequence is split into at most miso_attn_ragged_splits(max_len) spans (a longer sequence still gets all of
  * its keys, in longer spans). part_m/part_l need miso_attn_ragged_partials(batch, max_len) floats,
  * part_o 256 times that. A sequence with lens[s] == 0 yields core = 0. Rejects batch == 0 and
  * max_len == 0. */

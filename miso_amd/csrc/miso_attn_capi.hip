@@ -40,6 +40,20 @@ __global__ void __launch_bounds__(64) combine_range_kernel(k::AttnCombineParams 
   k::attn_combine_op<64, kPrepared, kPipeline>(p, first, count);
 }
 
+// Tensor pointers must be non-null and 16-byte aligned: the kernels move 16 bytes per lane.
+// The per-split scalars part_m / part_l are read one float at a time and need 4-byte alignment.
+bool bad_ptr(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+bool bad_scalars(const float* p) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 3u) != 0;
+}
+
+template <class... P>
+bool any_bad(const P*... p) {
+  return (bad_ptr(p) || ...);
+}
+
+constexpr const char* kBadPtr = "a tensor pointer is NULL or not 16-byte aligned";
+
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 const half_t* as_half(const uint16_t* p) { return reinterpret_cast<const half_t*>(p); }
 half_t* as_half(uint16_t* p) { return reinterpret_cast<half_t*>(p); }
@@ -62,6 +76,8 @@ int miso_attn_prep(const float* qg, const float* kp, const float* v, const float
                    const float* k_norm, const float* inv_freq, uint16_t* k_cache,
                    uint16_t* v_cache, float* q, uint32_t pos, uint32_t max_ctx, float eps,
                    void* stream) {
+  if (any_bad(qg, kp, v, q_norm, k_norm, inv_freq, k_cache, v_cache, q))
+    return fail("miso_attn_prep", kBadPtr);
   if (pos >= max_ctx)
     return fail("miso_attn_prep", "KV cache is full (pos >= max_ctx)");
   const k::AttnPrepParams p{qg,     kp,          v,           q_norm, k_norm, inv_freq,
@@ -76,6 +92,8 @@ int miso_attn_prep_batch(const float* qg, const float* kp, const float* v, const
                          uint32_t n, uint32_t proj_stride, void* stream) {
   if (n == 0)
     return 0;
+  if (any_bad(qg, kp, v, q_norm, k_norm, inv_freq, k_cache, v_cache, q))
+    return fail("miso_attn_prep_batch", kBadPtr);
   if (static_cast<uint64_t>(pos0) + n > max_ctx)
     return fail("miso_attn_prep_batch", "KV cache is full (pos0 + n > max_ctx)");
   if (proj_stride < 8192 + 1024)
@@ -91,6 +109,8 @@ int miso_attn_prep_batch(const float* qg, const float* kp, const float* v, const
 int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     float* part_m, float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                     uint32_t n_splits, void* stream) {
+  if (any_bad(q, k_cache, v_cache, part_o) || bad_scalars(part_m) || bad_scalars(part_l))
+    return fail("miso_attn_split", kBadPtr);
   if (len == 0)
     return fail("miso_attn_split", "len must be >= 1");
   if (len > max_ctx)
@@ -105,6 +125,8 @@ int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_c
 
 int miso_attn_combine(const float* part_m, const float* part_l, const float* part_o,
                       const float* qg, float* core, uint32_t n_splits, void* stream) {
+  if (any_bad(part_o, qg, core) || bad_scalars(part_m) || bad_scalars(part_l))
+    return fail("miso_attn_combine", kBadPtr);
   if (n_splits == 0)
     return fail("miso_attn_combine", "n_splits must be >= 1");
   const k::AttnCombineParams p{part_m, part_l, part_o, qg, core, n_splits};
@@ -116,6 +138,8 @@ int miso_attn_combine_variant(int variant, const float* part_m, const float* par
                               const float* part_o, const float* qg, float* core,
                               uint32_t n_splits, uint32_t first, uint32_t count, uint32_t grid,
                               void* stream) {
+  if (any_bad(part_o, qg, core) || bad_scalars(part_m) || bad_scalars(part_l))
+    return fail("miso_attn_combine_variant", kBadPtr);
   if (n_splits == 0)
     return fail("miso_attn_combine_variant", "n_splits must be >= 1");
   if (variant < 0 || variant > 3)
@@ -157,12 +181,14 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
 int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
                       const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
                       uint32_t max_ctx, uint32_t qg_stride, void* stream) {
+  if (any_bad(q, qg, k_cache, v_cache, core))
+    return fail("miso_attn_prefill", kBadPtr);
   if (n == 0)
     return fail("miso_attn_prefill", "n must be >= 1");
   if (static_cast<uint64_t>(pos0) + n > max_ctx)
     return fail("miso_attn_prefill", "KV cache is full (pos0 + n > max_ctx)");
-  if (qg_stride < 8192)
-    return fail("miso_attn_prefill", "qg_stride must be >= 8192");
+  if (qg_stride < 8192 || qg_stride % 4 != 0)
+    return fail("miso_attn_prefill", "qg_stride must be >= 8192 and a multiple of 4");
   const k::AttnPrefillParams p{q,    qg, as_half(k_cache), as_half(v_cache), core, pos0,
                                n,    max_ctx, qg_stride};
   k::attn_prefill_kernel<256><<<k::attn_prefill_items(n), 256, 0, as_stream(stream)>>>(p);
@@ -180,6 +206,10 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
                             const uint16_t* v_cache, const uint64_t* kv_offsets,
                             const uint32_t* lens, uint32_t batch, uint32_t max_len, float* core,
                             float* part_m, float* part_l, float* part_o, void* stream) {
+  if (any_bad(q, gate, k_cache, v_cache, core, part_o) || bad_scalars(part_m) ||
+      bad_scalars(part_l) ||
+      kv_offsets == nullptr || lens == nullptr)
+    return fail("miso_attn_decode_ragged", kBadPtr);
   if (batch == 0)
     return fail("miso_attn_decode_ragged", "batch must be >= 1");
   if (max_len == 0)

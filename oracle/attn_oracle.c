@@ -21,7 +21,7 @@
  *                          o += w o_c; core = o / L / (1 + exp(-gate))), with libm expf.
  *   - oracle_prep_f64:     per-head RMSNorm + NEOX RoPE + f16 KV append,
  *                          kernels/attention_decode.hpp:41-71, inv_freq as
- *                          src/engine/attention.hip:148-152.
+ *                          src/engine/attention.hip:60-71.
  *   - oracle_ref_n_splits: the reference split-count policy, kernels/attention_decode.hpp:92-115.
  *   - oracle_ragged_f64:   oracle_decode_f64 per sequence with a dense [B][16][256] gate
  *                          (no reference function: the reference is batch-1).
@@ -422,7 +422,7 @@ void oracle_combine_f32(const float* part_m, const float* part_l, const float* p
 /* Prep: per-head RMSNorm + NEOX RoPE on the first 64 dims + KV append                         */
 /* ------------------------------------------------------------------------------------------ */
 
-/* inv_freq[i] = 1 / base^(2i/64) in FP32, as src/engine/attention.hip:148-152. */
+/* inv_freq[i] = 1 / base^(2i/64) in FP32, as src/engine/attention.hip:60-71. */
 void oracle_inv_freq(float base, float* inv /* [32] */) {
   for (int i = 0; i < 32; ++i) inv[i] = 1.0f / powf(base, (float)(2 * i) / 64.0f);
 }

@@ -3,8 +3,8 @@
 // by GPU tests, as a second checker next to the CPU oracle; never linked into the product.
 //
 // Launch shapes are the reference callers': split <<<dim3(n_splits, 2), 256>>>
-// (src/engine/attention.hip:189), combine variants as tests/test_attn_splitk.hip:78-91 and
-// src/engine/attention.hip:192, prefill <<<attn_prefill_items(n), 256>>> (:227), prep
+// (src/engine/attention.hip:106), combine variants as tests/test_attn_splitk.hip:78-91 and
+// src/engine/attention.hip:109, prefill <<<attn_prefill_items(n), 256>>> (:143-144), prep
 // <<<18, 256>>> (:183), prep_batch <<<n * 18, 256>>> (:223).
 
 #include <hip/hip_runtime.h>

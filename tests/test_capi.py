@@ -52,31 +52,54 @@ def rejected(rc, lib, needle):
 
 
 def test_host_validation_rejects_bad_arguments(lib):
-    N = None
-    rejected(lib.miso_attn_split(N, N, N, N, N, N, 0, 10, 1, N), lib, "len must be >= 1")
-    rejected(lib.miso_attn_split(N, N, N, N, N, N, 11, 10, 1, N), lib, "exceeds max_ctx")
-    rejected(lib.miso_attn_split(N, N, N, N, N, N, 5, 10, 0, N), lib, "n_splits")
-    rejected(lib.miso_attn_combine(N, N, N, N, N, 0, N), lib, "n_splits")
-    rejected(lib.miso_attn_decode(N, N, N, N, N, N, N, N, 0, 10, 4, N), lib, "len must be")
-    rejected(lib.miso_attn_prefill(N, N, N, N, N, 0, 0, 10, 8192, N), lib, "n must be >= 1")
-    rejected(lib.miso_attn_prefill(N, N, N, N, N, 8, 3, 10, 8192, N), lib, "KV cache is full")
-    rejected(lib.miso_attn_prefill(N, N, N, N, N, 0, 3, 10, 100, N), lib, "qg_stride")
-    rejected(lib.miso_attn_prep(N, N, N, N, N, N, N, N, N, 10, 10, 1e-6, N), lib, "full")
-    rejected(lib.miso_attn_prep_batch(N, N, N, N, N, N, N, N, N, 8, 10, 1e-6, 3, 9216, N), lib,
+    # P: a non-null, 16-byte aligned address that is never dereferenced -- every call below must
+    # be rejected on the host before any launch.
+    N, P = None, 0x10000
+    rejected(lib.miso_attn_split(P, P, P, P, P, P, 0, 10, 1, N), lib, "len must be >= 1")
+    rejected(lib.miso_attn_split(P, P, P, P, P, P, 11, 10, 1, N), lib, "exceeds max_ctx")
+    rejected(lib.miso_attn_split(P, P, P, P, P, P, 5, 10, 0, N), lib, "n_splits")
+    rejected(lib.miso_attn_combine(P, P, P, P, P, 0, N), lib, "n_splits")
+    rejected(lib.miso_attn_decode(P, P, P, P, P, P, P, P, 0, 10, 4, N), lib, "len must be")
+    rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 0, 10, 8192, N), lib, "n must be >= 1")
+    rejected(lib.miso_attn_prefill(P, P, P, P, P, 8, 3, 10, 8192, N), lib, "KV cache is full")
+    rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 3, 10, 100, N), lib, "qg_stride")
+    rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 3, 10, 8194, N), lib, "multiple of 4")
+    rejected(lib.miso_attn_prep(P, P, P, P, P, P, P, P, P, 10, 10, 1e-6, N), lib, "full")
+    rejected(lib.miso_attn_prep_batch(P, P, P, P, P, P, P, P, P, 8, 10, 1e-6, 3, 9216, N), lib,
              "full")
-    rejected(lib.miso_attn_prep_batch(N, N, N, N, N, N, N, N, N, 0, 10, 1e-6, 3, 8192, N), lib,
+    rejected(lib.miso_attn_prep_batch(P, P, P, P, P, P, P, P, P, 0, 10, 1e-6, 3, 8192, N), lib,
              "proj_stride")
-    rejected(lib.miso_attn_decode_ragged(N, N, N, N, N, N, 0, 10, N, N, N, N, N), lib, "batch")
-    rejected(lib.miso_attn_decode_ragged(N, N, N, N, N, N, 3, 0, N, N, N, N, N), lib, "max_len")
-    rejected(lib.miso_attn_combine_variant(7, N, N, N, N, N, 4, 0, 0, 0, N), lib, "variant")
-    rejected(lib.miso_attn_combine_variant(0, N, N, N, N, N, 4, 0, 8, 2, N), lib, "range form")
-    rejected(lib.miso_attn_combine_variant(1, N, N, N, N, N, 4, 60, 8, 2, N), lib, "range form")
+    rejected(lib.miso_attn_decode_ragged(P, P, P, P, P, P, 0, 10, P, P, P, P, N), lib, "batch")
+    rejected(lib.miso_attn_decode_ragged(P, P, P, P, P, P, 3, 0, P, P, P, P, N), lib, "max_len")
+    rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
+    rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
+    rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")
+
+
+def test_host_validation_rejects_null_and_misaligned_pointers(lib):
+    N, P = None, 0x10000
+    bad = "NULL or not 16-byte aligned"
+    for q in (N, P + 4, P + 8):
+        rejected(lib.miso_attn_split(q, P, P, P, P, P, 5, 10, 1, N), lib, bad)
+        rejected(lib.miso_attn_prefill(P, P, q, P, P, 0, 3, 10, 8192, N), lib, bad)
+        rejected(lib.miso_attn_combine(P, P, P, P, q, 4, N), lib, bad)
+        rejected(lib.miso_attn_decode(P, P, P, P, P, P, P, q, 5, 10, 4, N), lib, bad)
+        rejected(lib.miso_attn_prep(P, P, P, P, P, P, q, P, P, 1, 10, 1e-6, N), lib, bad)
+        rejected(lib.miso_attn_prep_batch(P, P, P, P, P, P, P, P, q, 0, 10, 1e-6, 3, 9216, N),
+                 lib, bad)
+        rejected(lib.miso_attn_decode_ragged(P, P, q, P, P, P, 3, 10, P, P, P, P, N), lib, bad)
+        rejected(lib.miso_attn_combine_variant(3, P, P, q, P, P, 4, 0, 0, 0, N), lib, bad)
+    # part_m / part_l are scalar arrays: 4-byte alignment suffices, NULL and odd addresses do not
+    rejected(lib.miso_attn_split(P, P, P, N, P, P, 5, 10, 1, N), lib, bad)
+    rejected(lib.miso_attn_combine(P, P + 2, P, P, P, 4, N), lib, bad)
+    rejected(lib.miso_attn_decode_ragged(P, P, P, P, N, P, 3, 10, P, P, P, P, N), lib, bad)
 
 
 def test_python_layer_raises_runtime_error_with_message():
     from miso_amd import _lib
     with pytest.raises(RuntimeError, match="n_splits must be >= 1"):
-        _lib.check(_lib.load().miso_attn_combine(None, None, None, None, None, 0, None))
+        P = 0x10000
+        _lib.check(_lib.load().miso_attn_combine(P, P, P, P, P, 0, None))
 
 
 def test_split_policy_contract(lib):

@@ -1,6 +1,6 @@
 """Prep (RMSNorm + RoPE + f16 KV append) parity on MI355X, and the engine's call sequence:
 prep_batch -> prefill for a prompt, then prep -> split -> combine per decoded token, as
-src/engine/attention.hip:159-231 orders them, against the oracle run on the same cache.
+src/engine/attention.hip:76-148 orders them, against the oracle run on the same cache.
 """
 from __future__ import annotations
 
