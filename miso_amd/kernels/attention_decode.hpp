@@ -155,62 +155,77 @@ constexpr float kLn2 = 0.693147180559945309417f;
 constexpr int kGroup = attn::kQHeads / attn::kKvHeads;  // 8 query heads per KV head
 constexpr int kWaves = 4;                               // 256-thread workgroup (header API)
 
-constexpr int kRing = 4;                    // units per wave in the LDS ring (4-wave workgroups)
-constexpr unsigned kUnitBytes = 8192;       // 8 rows of K + 8 rows of V
-constexpr float kRescaleSlack = 8.0f;       // log2 units: numerators stay <= 2^8 between rescales
+constexpr int kRing = 2;               // units per wave in the LDS ring: one loads under one
+constexpr unsigned kUnitBytes = 8192;  // 8 K rows (4 KiB) then 8 V rows (4 KiB), natural order
+constexpr float kRescaleSlack = 8.0f;  // log2 units: numerators stay <= 2^8 between rescales
 
 // LDS of one split workgroup: each wave's ring of K/V units (direct global->LDS loads), the query
-// rows, per-wave softmax numerators (f16 pairs); the cross-wave merge reuses the ring.
+// rows, per-wave softmax numerators (f16 pairs) and per-wave head statistics; the cross-wave
+// merge of the value accumulators reuses the ring.
 template <int W, int R>
 struct SplitSharedT {
   static constexpr int kWaveCount = W, kRingUnits = R;
   union {
     unsigned char ring[W][R][kUnitBytes];
-    struct {
-      float o[W][kGroup][attn::kDim];
-      float m[W][kGroup];
-      float mt[W][kGroup];
-      float l[W][kGroup];
-    } merge;
+    float merge_o[W][2][kGroup][attn::kDim];  // [wave][row parity][head][dim], unscaled
   };
   float q[kGroup][attn::kDim];
-  _Float16 p[W][2][2][kGroup][2];  // [wave][row parity][pair][head][row of the pair]
+  // Numerators of one unit as f16 pairs, [wave][row parity a][pair g][head]: the pair holds rows
+  // 2 g + a and 2 g + 4 + a of the unit.
+  uint32_t p[W][2][2][kGroup];
+  float stat_m[W][kGroup], stat_mt[W][kGroup], stat_l[W][2][kGroup];
+  static_assert(sizeof(float) * W * 2 * kGroup * attn::kDim <= sizeof(unsigned char) * W * R *
+                    kUnitBytes, "the merge area must fit in the ring");
 };
-using SplitShared = SplitSharedT<kWaves, kRing>;  // 4 waves x 4 units: 136.5 KiB
+using SplitShared = SplitSharedT<kWaves, kRing>;
 
-// A unit: rows u0 + 2 i + (lane / 32), i = 0..3, bytes [16 c, 16 c + 16) of each row (c = lane %
-// 32), for K and for V. In global memory each row pair is 1 KiB contiguous; in the ring slot,
-// K row pair i is at byte 1024 i and V row pair i at 4096 + 1024 i, lane-linear, so a lane's 16
-// bytes land exactly where it reads them back.
-struct Unit {
-  uint4 k[4], v[4];
-};
+// Global -> LDS copy of one unit: K rows u0 .. u0 + 7 to slot bytes [0, 4096), V rows to [4096,
+// 8192), row r at 512 r. One instruction moves one row pair (1 KiB, 16 bytes per lane); `kw` / `vw`
+// are this lane's addresses of the first pair (row u0 + lane / 32, bytes 16 (lane % 32) of it).
+// The instruction offset advances the global and the LDS address together, which is exactly the
+// 1 KiB step of both layouts, so one address register serves all four pairs. The loads carry the
+// non-temporal hint: the cache is streamed once per call. M0 is saved and restored.
+__device__ __attribute__((always_inline)) inline void issue_unit(const attn::half_t* kw,
+                                                                 const attn::half_t* vw,
+                                                                 unsigned slot_lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "global_load_lds_dwordx4 %1, off offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %1, off offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %1, off offset:3072 nt\n\t"
+      "s_mov_b32 m0, %4\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off nt\n\t"
+      "global_load_lds_dwordx4 %2, off offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %2, off offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %2, off offset:3072 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(kw), "v"(vw), "s"(slot_lds), "s"(slot_lds + 4096u)
+      : "memory");
+}
 
-__device__ __attribute__((always_inline)) inline void load_unit(
+// The same copy for the unit that crosses the end of the cache (len): rows past len - 1 are
+// clamped to it (they are masked at use), so no load leaves [0, len). Also 8 instructions.
+__device__ __attribute__((always_inline)) inline void issue_unit_clamped(
     const attn::half_t* K, const attn::half_t* V, unsigned u0, unsigned last_row,
     unsigned slot_lds, unsigned lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     unsigned row = u0 + 2 * i + (lane >> 5);
-    row = row < last_row ? row : last_row;  // rows past the span are masked, never out of bounds
+    row = row < last_row ? row : last_row;
     const std::size_t at = std::size_t{row} * attn::kDim + (lane & 31u) * 8;
-    cdna4::lds_load16(K + at, slot_lds + 1024 * i);
-    cdna4::lds_load16(V + at, slot_lds + 4096 + 1024 * i);
+    cdna4::lds_load16_nt(K + at, slot_lds + 1024 * i);
+    cdna4::lds_load16_nt(V + at, slot_lds + 4096 + 1024 * i);
   }
 }
 
-__device__ __attribute__((always_inline)) inline Unit read_unit(const unsigned char* slot,
-                                                                unsigned lane) {
-  Unit u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    u.k[i] = *reinterpret_cast<const uint4*>(slot + 1024 * i + 16 * lane);
-    u.v[i] = *reinterpret_cast<const uint4*>(slot + 4096 + 1024 * i + 16 * lane);
-  }
-  return u;
-}
-
-// Wait until the unit whose loads were followed by `after` (< 4) more units' loads has landed.
+// Wait until the unit whose copy was followed by `after` (< 4) more units' copies has landed
+// (8 vector-memory instructions per unit).
 __device__ __attribute__((always_inline)) inline void wait_units_after(unsigned after) {
   switch (after) {
     case 0: cdna4::wait_vmcnt<0>(); break;
@@ -220,46 +235,92 @@ __device__ __attribute__((always_inline)) inline void wait_units_after(unsigned 
   }
 }
 
-// Running state of one wave: head h's reference max m, true max mt (log2 units) and sum l live in
-// the 8 lanes whose (lane % 32) / 4 == h; o[h][e] is this lane's share of head h at dims 8 c + e for
-// its row parity. l and o are relative to m.
+// Running state of one wave.
+//   Scores: lane = (hq = lane / 32, rq = lane / 16 % 2, dc = lane % 16) owns head 4 hq + dc / 4
+//   and unit row 4 rq + dc % 4 after the reduction; m (reference max), mt (true max), both log2
+//   units and uniform over the head's 8 lanes, and l (this lane's share of the head's sum) follow
+//   that head.
+//   Values: lane = (a = lane / 32, c = lane % 32) accumulates o[h][e] = head h, dimension 8 c + e,
+//   over the unit rows of parity a, relative to m.
 struct WaveState {
   float m, mt, l;
   float o[kGroup][8];
 };
 
-// Online-softmax update of one unit. qh[h][j]: the lane's query slice (dims 8c + 2j, 8c + 2j + 1)
-// of head h, pre-scaled by log2(e)/16, as f16 pairs. The reference max m moves only when a score
-// exceeds it by more than kRescaleSlack (then o and l are rescaled exactly), so numerators
-// exp2(s - m) stay below 2^kRescaleSlack and most units skip the rescale.
+// Lane holding head h's statistics (rq = 0, dc = 4 (h % 4)).
+__device__ inline unsigned head_lane(int h) { return 32u * (h >> 2) + 4u * (h & 3); }
+
+// v_dot2_f32_f16 with a zero accumulator (the VOP3 form takes the inline constant, so no register
+// has to be cleared first).
+__device__ __attribute__((always_inline)) inline float dot2_first(half2_t a, unsigned b) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// One unit (8 rows) of the online softmax.
+//
+// S: the lane's 16 partial dot products (4 heads x 4 rows, 16 of its dimensions each) are laid
+// out so that a reduce-scatter over the 16 lanes of dc needs one DPP add per value and level:
+// register slot s = 4 hh + rr holds head 4 hq + (hh ^ dc / 4) and row 4 rq + (rr ^ dc % 4), i.e.
+// value index s ^ dc. At a level with lane mask mu (8, 7, 2, 1: highest bits 3..0) every lane
+// keeps slots j < mu's top bit and adds the partner's slot j ^ mu, which holds the same value
+// index; after four levels lane dc holds value dc. The query slots hh are permuted per lane once
+// at the start; the row permutation is folded into the lane's LDS read addresses.
+// P V: rows (2 g + a, 2 g + 4 + a) pair up in one v_dot2_f32_f16 per (head, dimension); their
+// numerators arrive as f16 pairs through a 128-byte per-wave LDS buffer.
 __device__ __attribute__((always_inline)) inline void process_unit(
-    WaveState& st, const Unit& u, const half2_t (&qh)[kGroup][4], unsigned u0, unsigned span_end,
-    _Float16 (*pbuf)[2][kGroup][2], unsigned lane) {
-  const unsigned c = lane & 31u, a = lane >> 5;
-  // Scores: partial dot products over this lane's 8 dims, then a reduce-scatter over the 32
-  // lanes of the row parity leaves the complete score of (head c / 4, row u0 + 2 (c % 4) + a).
-  float part[32];
+    WaveState& st, const unsigned char* slot, const unsigned (&koff)[4],
+    const half2_t (&qh)[4][8], unsigned u0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
+    unsigned lane) {
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  // All of the unit's K and V reads first, so their LDS latency overlaps.
+  uint4 kr[4][2], vr[4];
 #pragma unroll
-  for (int h = 0; h < kGroup; ++h) {
+  for (int rr = 0; rr < 4; ++rr) {
+    kr[rr][0] = *reinterpret_cast<const uint4*>(slot + koff[rr]);
+    kr[rr][1] = *reinterpret_cast<const uint4*>(slot + koff[rr] + 256);
+  }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 kw = u.k[i];
-      float acc = __builtin_amdgcn_fdot2(qh[h][0], cdna4::as_half2(kw.x), 0.0f, false);
-      acc = __builtin_amdgcn_fdot2(qh[h][1], cdna4::as_half2(kw.y), acc, false);
-      acc = __builtin_amdgcn_fdot2(qh[h][2], cdna4::as_half2(kw.z), acc, false);
-      acc = __builtin_amdgcn_fdot2(qh[h][3], cdna4::as_half2(kw.w), acc, false);
-      part[h * 4 + i] = acc;
+  for (int i = 0; i < 4; ++i)
+    vr[i] = *reinterpret_cast<const uint4*>(slot + 4096 + 1024 * i + 16 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+  float part[16];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const uint4 k0 = kr[rr][0], k1 = kr[rr][1];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      float acc = dot2_first(qh[hh][0], k0.x);
+      acc = __builtin_amdgcn_fdot2(qh[hh][1], cdna4::as_half2(k0.y), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][2], cdna4::as_half2(k0.z), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][3], cdna4::as_half2(k0.w), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][4], cdna4::as_half2(k1.x), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][5], cdna4::as_half2(k1.y), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][6], cdna4::as_half2(k1.z), acc, false);
+      acc = __builtin_amdgcn_fdot2(qh[hh][7], cdna4::as_half2(k1.w), acc, false);
+      part[4 * hh + rr] = acc;
     }
   }
-  float s = cdna4::reduce_scatter32(part);
-  const unsigned my_row = u0 + 2 * (c & 3u) + a;
-  if (my_row >= span_end)
+  float r8[8], r4[4], r2[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    r8[j] = part[j] + cdna4::dpp_mov<cdna4::kRowRor8>(part[j ^ 8]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    r4[j] = r8[j] + cdna4::dpp_mov<cdna4::kRowHalfMirror>(r8[j ^ 7]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    r2[j] = r4[j] + cdna4::dpp_mov<cdna4::kQuadXor2>(r4[j ^ 2]);
+  float s = r2[0] + cdna4::dpp_mov<cdna4::kQuadXor1>(r2[1]);
+  const unsigned row = 4 * rq + (dc & 3u);
+  if (u0 + row >= span_end)
     s = -__builtin_inff();
-  // Head max over its 8 lanes (quad of rows, both parities). Row u0 is always in the span, so
-  // every head has at least one finite score.
+  // Head max over its 8 lanes (dc % 4 and rq). Row u0 is always in the span, so every head has
+  // a finite score.
   float mu = fmaxf(s, cdna4::dpp_mov<cdna4::kQuadXor1>(s));
   mu = fmaxf(mu, cdna4::dpp_mov<cdna4::kQuadXor2>(mu));
-  mu = cdna4::max_xor32(mu);
+  mu = cdna4::max_xor16(mu);
   st.mt = fmaxf(st.mt, mu);
   if (__builtin_amdgcn_ballot_w64(mu > st.m + kRescaleSlack)) {  // wave-uniform branch
     const float m_new = fmaxf(st.m, mu);
@@ -268,30 +329,29 @@ __device__ __attribute__((always_inline)) inline void process_unit(
     st.m = m_new;
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) {
-      const float ch = cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), 4 * h));
+      const float ch =
+          cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), head_lane(h)));
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         st.o[h][e] *= ch;
     }
   }
-  const float pj = __builtin_amdgcn_exp2f(s - st.m);  // 0 for masked rows
-  st.l += pj;
-  // Numerators to LDS as f16: slot [parity a][pair (row index % 2)][head][row index / 2].
+  const _Float16 p16 = static_cast<_Float16>(__builtin_amdgcn_exp2f(s - st.m));  // 0 if masked
+  st.l += static_cast<float>(p16);  // the sum of exactly the numerators P V uses
   {
-    const unsigned ri = c & 3u, h = c >> 2;
-    pbuf[a][ri & 1u][h][ri >> 1] = static_cast<_Float16>(pj);
+    const unsigned head = 4 * hq + (dc >> 2);
+    _Float16* ph = reinterpret_cast<_Float16*>(&pbuf[row & 1u][(row >> 1) & 1u][head]);
+    ph[row >> 2] = p16;
   }
-  // P V: rows (i, i + 2) of the parity pair up in one dot2 per (head, dim).
-  half2_t pp[2][kGroup];
-#pragma unroll
-  for (int g = 0; g < 2; ++g)
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-      __builtin_memcpy(&pp[g][h], &pbuf[a][g][h][0], sizeof(half2_t));
+  // P V over this lane's rows 2 i + a, dimensions 8 c .. 8 c + 7.
+  const unsigned a = lane >> 5;
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    const unsigned r0[4] = {u.v[g].x, u.v[g].y, u.v[g].z, u.v[g].w};
-    const unsigned r1[4] = {u.v[g + 2].x, u.v[g + 2].y, u.v[g + 2].z, u.v[g + 2].w};
+    const uint4 p0 = *reinterpret_cast<const uint4*>(&pbuf[a][g][0]);
+    const uint4 p1 = *reinterpret_cast<const uint4*>(&pbuf[a][g][4]);
+    const unsigned pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    const unsigned r0[4] = {vr[g].x, vr[g].y, vr[g].z, vr[g].w};
+    const unsigned r1[4] = {vr[g + 2].x, vr[g + 2].y, vr[g + 2].z, vr[g + 2].w};
     half2_t pv[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -302,20 +362,21 @@ __device__ __attribute__((always_inline)) inline void process_unit(
     for (int h = 0; h < kGroup; ++h)
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        st.o[h][e] = __builtin_amdgcn_fdot2(pp[g][h], pv[e], st.o[h][e], false);
+        st.o[h][e] = __builtin_amdgcn_fdot2(cdna4::as_half2(pp[h]), pv[e], st.o[h][e], false);
   }
 }
 
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh, written at `base` (=
-// kvh * n_splits + split) in the reference's partial layout. Wave w streams units w, w + 4, ...
-// of the span through its kRing-unit LDS ring (kRing - 1 units in flight while one is processed);
-// the four waves merge through LDS at the end. Every vector-memory load of the kernel is a direct
-// LDS load with an explicit wait.
+// kvh * n_splits + split) in the reference's partial layout. Wave w streams units w, w + W, ...
+// of the span through its R-unit LDS ring (R - 1 units in flight while one is processed); the
+// waves merge through LDS at the end. Every vector-memory load of the kernel is a direct LDS
+// load with an explicit wait. `more` says whether the workgroup runs another item afterwards
+// (its LDS is then reused).
 template <class Shared>
 __device__ __attribute__((always_inline)) inline void split_partial(
     const float* __restrict__ q, const attn::half_t* K, const attn::half_t* V, unsigned len,
     AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base,
-    Shared& sh) {
+    Shared& sh, bool more) {
   constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
   static_assert(kR >= 2 && kR <= 4 && kGroup % kW == 0, "ring depth / wave count");
   const unsigned t = threadIdx.x, lane = t & 63u, c = lane & 31u;
@@ -325,6 +386,17 @@ __device__ __attribute__((always_inline)) inline void split_partial(
   const unsigned first = span.begin + wave * kAttnDecodeUnit;
   const unsigned n_units = first < span.end ? (span.end - first + kStride - 1) / kStride : 0;
   const unsigned ring0 = cdna4::lds_offset(sh.ring[wave][0]);
+  // This lane's address of row pair 0 of unit 0; unit k is kStride rows further.
+  const std::size_t lane_at = std::size_t{first + (lane >> 5)} * attn::kDim + c * 8;
+  constexpr std::size_t kUnitStep = std::size_t{kStride} * attn::kDim;
+  auto issue = [&](unsigned k) {
+    const unsigned u0 = first + k * kStride;
+    const unsigned slot = ring0 + (k % kR) * kUnitBytes;
+    if (u0 + kAttnDecodeUnit <= len)  // wave-uniform
+      issue_unit(K + lane_at + k * kUnitStep, V + lane_at + k * kUnitStep, slot);
+    else
+      issue_unit_clamped(K, V, u0, last_row, slot, lane);
+  };
 
   // This wave's query heads of the KV head (1 KiB each), then the first kR - 1 units.
   constexpr int kHeadsPerWave = kGroup / kW;
@@ -337,21 +409,38 @@ __device__ __attribute__((always_inline)) inline void split_partial(
 #pragma unroll
   for (unsigned k = 0; k + 1 < kR; ++k)
     if (k < n_units)
-      load_unit(K, V, first + k * kStride, last_row, ring0 + k * kUnitBytes, lane);
+      issue(k);
   wait_units_after(n_units < kR - 1 ? n_units : kR - 1);  // the query loads are older
   __syncthreads();
 
-  half2_t qh[kGroup][4];
+  // Query slices as f16 pairs pre-scaled by log2(e)/16: slot hh = head 4 hq + (hh ^ dc / 4),
+  // dimensions 8 dc .. 8 dc + 7 (pairs 0-3) and 128 + 8 dc .. 128 + 8 dc + 7 (pairs 4-7).
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  half2_t qh[4][8];
   constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
 #pragma unroll
-  for (int h = 0; h < kGroup; ++h) {
-    const float4 x0 = *reinterpret_cast<const float4*>(&sh.q[h][8 * c]);
-    const float4 x1 = *reinterpret_cast<const float4*>(&sh.q[h][8 * c + 4]);
-    qh[h][0] = half2_t{static_cast<_Float16>(x0.x * kScale), static_cast<_Float16>(x0.y * kScale)};
-    qh[h][1] = half2_t{static_cast<_Float16>(x0.z * kScale), static_cast<_Float16>(x0.w * kScale)};
-    qh[h][2] = half2_t{static_cast<_Float16>(x1.x * kScale), static_cast<_Float16>(x1.y * kScale)};
-    qh[h][3] = half2_t{static_cast<_Float16>(x1.z * kScale), static_cast<_Float16>(x1.w * kScale)};
+  for (int hh = 0; hh < 4; ++hh) {
+    const unsigned h = 4 * hq + (hh ^ (dc >> 2));
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const float4 x0 = *reinterpret_cast<const float4*>(&sh.q[h][128 * half + 8 * dc]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&sh.q[h][128 * half + 8 * dc + 4]);
+      qh[hh][4 * half + 0] = half2_t{static_cast<_Float16>(x0.x * kScale),
+                                     static_cast<_Float16>(x0.y * kScale)};
+      qh[hh][4 * half + 1] = half2_t{static_cast<_Float16>(x0.z * kScale),
+                                     static_cast<_Float16>(x0.w * kScale)};
+      qh[hh][4 * half + 2] = half2_t{static_cast<_Float16>(x1.x * kScale),
+                                     static_cast<_Float16>(x1.y * kScale)};
+      qh[hh][4 * half + 3] = half2_t{static_cast<_Float16>(x1.z * kScale),
+                                     static_cast<_Float16>(x1.w * kScale)};
+    }
   }
+  // K read offsets in a slot: row 4 rq + (rr ^ dc % 4), 16-byte chunk dc (and dc + 16, +256 B).
+  unsigned koff[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr)
+    koff[rr] = (4 * rq + (rr ^ (dc & 3u))) * 512 + 16 * dc;
+
   WaveState st;
   st.m = -__builtin_inff();
   st.mt = -__builtin_inff();
@@ -362,76 +451,98 @@ __device__ __attribute__((always_inline)) inline void split_partial(
     for (int e = 0; e < 8; ++e)
       st.o[h][e] = 0.0f;
 
-  for (unsigned k = 0; k < n_units; ++k) {
-    const unsigned ahead = k + kR - 1;
-    if (ahead < n_units)  // its slot held unit k - 1, already read back into registers
-      load_unit(K, V, first + ahead * kStride, last_row, ring0 + (ahead % kR) * kUnitBytes,
-                lane);
-    const unsigned after = n_units - 1 - k;
-    wait_units_after(after < kR - 1 ? after : kR - 1);
-    const Unit u = read_unit(sh.ring[wave][k % kR], lane);
-    process_unit(st, u, qh, first + k * kStride, span.end, sh.p[wave], lane);
+  // Steady state: one unit issued and one consumed per iteration, a fixed wait. Its slot held
+  // unit k - 1, already read back into registers.
+  unsigned k = 0;
+  for (; k + kR - 1 < n_units; ++k) {
+    issue(k + kR - 1);
+    cdna4::wait_vmcnt<8 * (kR - 1)>();
+    process_unit(st, sh.ring[wave][k % kR], koff, qh, first + k * kStride, span.end, sh.p[wave],
+                 lane);
+  }
+  // Drain: the last units, already in flight.
+  for (; k < n_units; ++k) {
+    wait_units_after(n_units - 1 - k);
+    process_unit(st, sh.ring[wave][k % kR], koff, qh, first + k * kStride, span.end, sh.p[wave],
+                 lane);
   }
 
-  // Wave totals: l over the head's 8 lanes; o over the two row parities. swap32 of heads
-  // (h, h + 4) leaves head h's total in the low half and head h + 4's in the high half.
-  float l = st.l + cdna4::dpp_mov<cdna4::kQuadXor1>(st.l);
-  l += cdna4::dpp_mov<cdna4::kQuadXor2>(l);
-  l = cdna4::sum_xor32(l);
-  __syncthreads();  // every wave is done with its ring: the merge area aliases it
+  // Cross-wave merge relative to the split's true max M_h = max_w mt_w,h, so the partial is
+  // exactly (max, sum exp(s - max), sum exp(s - max) v). Each wave stores its raw accumulators
+  // (both row parities) and head statistics, then after one barrier every thread produces two
+  // float4 chunks of the partial: o = sum_w exp2(m_w,h - M_h) (o_w,0 + o_w,1).
   {
+    float l = st.l + cdna4::dpp_mov<cdna4::kQuadXor1>(st.l);
+    l += cdna4::dpp_mov<cdna4::kQuadXor2>(l);  // head total over dc % 4, for this rq
+    const unsigned h = 4 * hq + (dc >> 2);
+    if ((lane & 3u) == 0)
+      sh.stat_l[wave][rq][h] = l;
+    if ((lane & 0x13u) == 0) {  // rq = 0, dc % 4 = 0: one lane per head
+      sh.stat_m[wave][h] = st.m;
+      sh.stat_mt[wave][h] = st.mt;
+    }
     const unsigned a = lane >> 5;
 #pragma unroll
-    for (int h = 0; h < kGroup / 2; ++h) {
-      float tot[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const cdna4::Pair pr = cdna4::swap32(st.o[h][e], st.o[h + kGroup / 2][e]);
-        tot[e] = pr.a + pr.b;
-      }
-      float4* dst = reinterpret_cast<float4*>(&sh.merge.o[wave][h + a * (kGroup / 2)][8 * c]);
-      dst[0] = float4{tot[0], tot[1], tot[2], tot[3]};
-      dst[1] = float4{tot[4], tot[5], tot[6], tot[7]};
+    for (int hh = 0; hh < kGroup; ++hh) {
+      float4* dst = reinterpret_cast<float4*>(&sh.merge_o[wave][a][hh][8 * c]);
+      dst[0] = float4{st.o[hh][0], st.o[hh][1], st.o[hh][2], st.o[hh][3]};
+      dst[1] = float4{st.o[hh][4], st.o[hh][5], st.o[hh][6], st.o[hh][7]};
     }
-  }
-  if (lane < 32 && (c & 3u) == 0) {
-    sh.merge.m[wave][c >> 2] = st.m;
-    sh.merge.mt[wave][c >> 2] = st.mt;
-    sh.merge.l[wave][c >> 2] = l;
   }
   __syncthreads();
-  // Merge the waves relative to the split's true max M: the kW * 64 threads split into 8 heads x
-  // kTh threads of kDims dims. The partial is then exactly (max, sum exp(s - max), sum exp(s -
-  // max) v).
   {
-    constexpr unsigned kTh = kW * 64 / kGroup, kDims = attn::kDim / kTh;
-    const unsigned h = t / kTh, d0 = kDims * (t % kTh);
-    float M = -__builtin_inff();
+    // 8 heads x 256 floats = 512 float4 chunks; thread t makes chunks t + kThreads j (heads
+    // (t + kThreads j) / 64). All LDS reads are issued before any arithmetic (no branches), so
+    // the phase costs one LDS round trip.
+    constexpr unsigned kChunks = kGroup * attn::kDim / 4, kThreads = kW * 64;
+    constexpr unsigned kPer = kChunks / kThreads, kHeadChunks = attn::kDim / 4;
+    static_assert(kChunks % kThreads == 0, "chunks per thread");
+    const float4* src = reinterpret_cast<const float4*>(&sh.merge_o[0][0][0][0]);
+    float4* dst = reinterpret_cast<float4*>(part_o + base * kGroup * attn::kDim);
+    float m[kPer][kW], mt[kPer][kW], lw[kPer][kW];
+    float4 x[kPer][kW][2];
 #pragma unroll
-    for (int w = 0; w < kW; ++w)
-      M = fmaxf(M, sh.merge.mt[w][h]);
-    float L = 0.0f, o[kDims] = {};
-    if (M != -__builtin_inff()) {
+    for (unsigned j = 0; j < kPer; ++j) {
+      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
 #pragma unroll
       for (int w = 0; w < kW; ++w) {
-        const float sc = __builtin_amdgcn_exp2f(sh.merge.m[w][h] - M);
-        L += sc * sh.merge.l[w][h];
-#pragma unroll
-        for (unsigned e = 0; e < kDims; ++e)
-          o[e] += sc * sh.merge.o[w][h][d0 + e];
+        m[j][w] = sh.stat_m[w][h];
+        mt[j][w] = sh.stat_mt[w][h];
+        lw[j][w] = sh.stat_l[w][0][h] + sh.stat_l[w][1][h];
+        x[j][w][0] = src[(w * 2 + 0) * kChunks + i];
+        x[j][w][1] = src[(w * 2 + 1) * kChunks + i];
       }
     }
-    const std::size_t at = base * kGroup + h;
-    if (t % kTh == 0) {
-      part_m[at] = M * kLn2;  // -inf stays -inf for an empty span
-      part_l[at] = L;
-    }
-    float4* dst = reinterpret_cast<float4*>(part_o + at * attn::kDim + d0);
 #pragma unroll
-    for (unsigned e = 0; e < kDims; e += 4)
-      dst[e / 4] = float4{o[e], o[e + 1], o[e + 2], o[e + 3]};
+    for (unsigned j = 0; j < kPer; ++j) {
+      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
+      float M = mt[j][0];
+#pragma unroll
+      for (int w = 1; w < kW; ++w)
+        M = fmaxf(M, mt[j][w]);
+      const bool empty = M == -__builtin_inff();  // no key in the span
+      const float Mc = empty ? 0.0f : M;          // exp2(-inf - 0) = 0 for every wave
+      float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      float L = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) {
+        const float sc = __builtin_amdgcn_exp2f(m[j][w] - Mc);
+        const float4 x0 = x[j][w][0], x1 = x[j][w][1];
+        acc.x = __builtin_fmaf(sc, x0.x + x1.x, acc.x);
+        acc.y = __builtin_fmaf(sc, x0.y + x1.y, acc.y);
+        acc.z = __builtin_fmaf(sc, x0.z + x1.z, acc.z);
+        acc.w = __builtin_fmaf(sc, x0.w + x1.w, acc.w);
+        L = __builtin_fmaf(sc, lw[j][w], L);
+      }
+      dst[i] = acc;
+      if (i % kHeadChunks == 0) {
+        part_m[base * kGroup + h] = M * kLn2;  // -inf stays -inf for an empty span
+        part_l[base * kGroup + h] = L;
+      }
+    }
   }
-  __syncthreads();  // LDS is reused by the next item
+  if (more)
+    __syncthreads();  // LDS is reused by the next item
 }
 
 }  // namespace decode_detail
@@ -453,29 +564,14 @@ __device__ void attn_split_op(const AttnSplitParams& p, unsigned first, unsigned
     const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
     decode_detail::split_partial(p.q, K, V, p.len, attn_split_span(p.len, p.n_splits, split),
                                  kvh, p.part_m, p.part_l, p.part_o,
-                                 std::size_t{kvh} * p.n_splits + split, sh);
+                                 std::size_t{kvh} * p.n_splits + split, sh,
+                                 item + gridDim.x * gridDim.y < first + count);
   }
 }
 
 template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_split_kernel(AttnSplitParams p) {
   attn_split_op<kBlock>(p, 0, attn::kKvHeads * p.n_splits);
-}
-
-// The same split partials from 512-thread workgroups (8 waves, two per SIMD, 2-unit rings): one
-// workgroup per (KV head, split), grid dim3(n_splits, 2). A second resident wave per SIMD hides
-// the dependency stalls of the first.
-__global__ void __launch_bounds__(512) attn_split_wide_kernel(AttnSplitParams p) {
-  __shared__ decode_detail::SplitSharedT<8, 2> sh;
-  const unsigned item = blockIdx.y * gridDim.x + blockIdx.x;
-  if (item >= attn::kKvHeads * p.n_splits)
-    return;
-  const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
-  const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
-  const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
-  decode_detail::split_partial(p.q, K, V, p.len, attn_split_span(p.len, p.n_splits, split), kvh,
-                               p.part_m, p.part_l, p.part_o,
-                               std::size_t{kvh} * p.n_splits + split, sh);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -631,7 +727,7 @@ __global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedPar
                                p.k_cache + kv0, p.v_cache + kv0, len,
                                attn_split_span(len, n_splits, split), kvh, p.part_m, p.part_l,
                                p.part_o, (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
-                               sh);
+                               sh, false);
 }
 
 // One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's.

@@ -130,6 +130,21 @@ __device__ __attribute__((always_inline)) inline void lds_load16(const void* gad
       : "memory");
 }
 
+// The same load with the non-temporal hint, for data streamed once (the KV cache in decode).
+__device__ __attribute__((always_inline)) inline void lds_load16_nt(const void* gaddr,
+                                                                    unsigned lds_base) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gaddr), "s"(lds_base)
+      : "memory");
+}
+
 // Wait until at most N vector-memory ops of this wave are outstanding (LDS and VGPR loads both
 // count); also a compiler barrier for memory.
 template <int N>
