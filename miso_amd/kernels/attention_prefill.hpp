@@ -14,6 +14,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "attention_decode.hpp"
 #include "cdna4_wave.hpp"
@@ -60,8 +61,8 @@ struct AttnPrefillParams {
   unsigned qg_stride;  // 8192 packed, or 9216 when q/k/v share a proj buffer
 };
 
-// Tokens per workgroup: 4 waves x 4 tokens x 8 query heads = 32 query rows per wave, the N side
-// of one 32x32 MFMA tile.
+// Tokens per workgroup: 4 waves x 8 tokens x 8 query heads = 64 query rows per wave, two 32-row
+// MFMA column blocks.
 constexpr unsigned kAttnQBlock = 16;
 constexpr int kAttnQBlocksPerWave = 1;
 
@@ -81,25 +82,70 @@ using cdna4::half8_t;
 typedef __fp16 lds_fp16x4 __attribute__((vector_size(8)));
 
 constexpr int kKeys = 32;                      // keys per K/V tile (the M side of S^T = K Q^T)
-constexpr int kStages = 3;                     // LDS ring depth: tiles i+1, i+2 load under tile i
+constexpr int kStages = 3;                     // LDS ring depth
 constexpr int kRowBytes = attn::kDim * 2;      // 512: one f16 row
 constexpr int kTileBytes = kKeys * kRowBytes;  // 16 KiB per K or V tile
+constexpr int kNB = kAttnQBlocksPerWave;       // 32-row MFMA column blocks per wave
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: numerators stay <= 2^8 between rescales
 
-struct Shared {
-  alignas(16) unsigned char k[kStages][kTileBytes];
-  alignas(16) unsigned char v[kStages][kTileBytes];
+// K tiles in the first 48 KiB, V tiles in the next 48 KiB, so every operand address is a per-lane
+// base plus a compile-time offset below 64 KiB (the ring slot is folded into the offset).
+constexpr unsigned kVBase = kStages * kTileBytes;
+// 1 KiB alignment keeps the base clear of the address bits the swizzle XORs (4-8).
+struct alignas(1024) Shared {
+  unsigned char kv[2 * kStages * kTileBytes];
 };
 
-// 16-byte chunk c of tile row r lives at chunk position c ^ 2 (r % 16) of that row: 16 rows read
-// at one chunk (S^T operands) and 4 rows read at two chunks (transpose reads) hit distinct banks.
+// 16-byte chunk c of tile row r lives at chunk position c ^ 2 (r % 16) of that row: the 32 rows
+// read at one chunk (S^T operands) and the transpose reads spread over the banks. The XOR only
+// touches address bits 4-8, so operand addresses are lane bases XOR compile-time constants.
 __device__ inline unsigned swz(unsigned row, unsigned chunk) { return chunk ^ ((row & 15u) << 1); }
 
-// This wave's share of the LDS loads of one tile: K and V rows 8 w .. 8 w + 7, one 1 KiB
-// instruction per row pair and tensor (8 per wave). Rows past the last valid key are clamped
-// into range and masked at use.
-__device__ __attribute__((always_inline)) inline void load_tile(
+// Global -> LDS copy of tile rows [8 w, 8 w + 8) of K and V (one 1 KiB instruction per row pair
+// and tensor). `off[i]` is this lane's byte offset of instruction i inside a tile (row 8 w + 2 i +
+// lane / 32, chunk swz(row, lane % 32)); kt / vt are the tile's first rows (wave-uniform), so the
+// copy needs no per-tile address arithmetic. M0 is saved and restored.
+__device__ __attribute__((always_inline)) inline void copy_tile(const void* kt, const void* vt,
+                                                                const unsigned (&off)[4],
+                                                                unsigned k_lds, unsigned v_lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %7\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %5\n\t"
+      "s_add_u32 m0, %7, 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %5\n\t"
+      "s_add_u32 m0, %7, 0x800\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %3, %5\n\t"
+      "s_add_u32 m0, %7, 0xc00\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %4, %5\n\t"
+      "s_mov_b32 m0, %8\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %6\n\t"
+      "s_add_u32 m0, %8, 0x400\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %6\n\t"
+      "s_add_u32 m0, %8, 0x800\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %3, %6\n\t"
+      "s_add_u32 m0, %8, 0xc00\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %4, %6\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(kt), "s"(vt), "s"(k_lds),
+        "s"(v_lds)
+      : "memory", "scc");
+}
+
+// The same copy for the tile that crosses the end of the keys: rows past last_row are clamped to
+// it (they are masked at use), so no load leaves [0, last_row]. Also 8 instructions.
+__device__ __attribute__((always_inline)) inline void copy_tile_clamped(
     const attn::half_t* K, const attn::half_t* V, unsigned k0, unsigned last_row,
     unsigned k_lds, unsigned v_lds, unsigned wave, unsigned lane) {
 #pragma unroll
@@ -114,39 +160,188 @@ __device__ __attribute__((always_inline)) inline void load_tile(
   }
 }
 
-__device__ inline half4_t read_tr(const unsigned char* base) {
+__device__ __attribute__((always_inline)) inline half8_t lds_read_b128(unsigned addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) half8_t*>(addr);
+}
+
+__device__ __attribute__((always_inline)) inline half4_t read_tr(unsigned addr) {
   const lds_fp16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-      (__attribute__((address_space(3))) lds_fp16x4*)(base));
+      reinterpret_cast<__attribute__((address_space(3))) lds_fp16x4*>(addr));
   return __builtin_bit_cast(half4_t, raw);
+}
+
+// Per-lane state of one wave: 64 query rows as two 32-row column blocks.
+struct Rows {
+  half8_t q[kNB][16];  // Q^T B operands: dims 16 s + 8 hi + j of the lane's rows, x log2(e)/16
+  float m[kNB], l[kNB];
+};
+
+// S^T[key][row] = K Q^T for one tile (32 keys x 64 rows): 16 k-steps over head_dim, each K
+// operand read once and used by both column blocks. kb: the lane's operand address in the tile's
+// slot before the per-step XOR.
+__device__ __attribute__((always_inline)) inline void scores(float16_t (&s)[kNB], const Rows& rw,
+                                                            unsigned kb) {
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb)
+    s[nb] = float16_t{};
+#pragma unroll
+  for (unsigned st = 0; st < 16; ++st) {
+    const half8_t a = lds_read_b128(kb ^ (32u * st));
+#pragma unroll
+    for (int nb = 0; nb < kNB; ++nb)
+      s[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, rw.q[nb][st], s[nb], 0, 0, 0);
+  }
+}
+
+// O^T[d][row] += V^T[d][key] P^T[key][row] for one tile; k-slot 8 hi + j of a step holds key
+// 16 step + 4 hi + (j < 4 ? j : j + 4), which is how the S^T accumulator rows lie in the lane, so
+// P^T is the softmax output as is. vb[b][u]: the lane's transpose-read addresses for 32-dim block
+// b (u = 1: rows + 8) in tile slot 0; slot_off moves them to the tile's slot.
+__device__ __attribute__((always_inline)) inline void accumulate(float16_t (&o)[kNB][8],
+                                                                const half8_t (&p)[kNB][2],
+                                                                const unsigned (&vb)[8][2],
+                                                                unsigned slot_off) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const unsigned a0 = vb[b][0] + slot_off, a1 = vb[b][1] + slot_off;
+#pragma unroll
+    for (unsigned step = 0; step < 2; ++step) {
+      const half4_t lo = read_tr(a0 + 8192u * step);
+      const half4_t up = read_tr(a1 + 8192u * step);
+      const half8_t a = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+#pragma unroll
+      for (int nb = 0; nb < kNB; ++nb)
+        o[nb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[nb][step], o[nb][b], 0, 0, 0);
+    }
+  }
+}
+
+// Online softmax of one tile's scores (log2 units) into f16 numerators. kMasked: key k0 + key(r)
+// is visible to the lane's row nb iff it is <= lim[nb]. The reference max moves only when a tile
+// exceeds it by more than the slack; that wave-uniform case returns true after setting `corr`
+// (the factor the accumulators must be scaled by before the next tile is added).
+template <bool kMasked>
+__device__ __attribute__((always_inline)) inline bool softmax(const float16_t (&s)[kNB],
+                                                             Rows& rw, half8_t (&p)[kNB][2],
+                                                             float (&corr)[kNB], unsigned k0,
+                                                             const unsigned (&lim)[kNB],
+                                                             unsigned hi) {
+  float x[kNB][16], mx[kNB];
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      x[nb][r] = s[nb][r];
+  }
+  if (kMasked) {  // the diagonal tiles only
+#pragma unroll
+    for (int nb = 0; nb < kNB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
+        x[nb][r] = key <= lim[nb] ? x[nb][r] : -__builtin_inff();
+      }
+  }
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb) {
+    float a = fmaxf(fmaxf(x[nb][0], x[nb][1]), x[nb][2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2)
+      a = fmaxf(fmaxf(a, x[nb][r]), x[nb][r + 1]);
+    mx[nb] = fmaxf(a, x[nb][15]);
+  }
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb)
+    mx[nb] = cdna4::max_xor32(mx[nb]);  // the other 16 keys of the column are in lane ^ 32
+  bool need = false;
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb)
+    need |= mx[nb] > rw.m[nb] + kRescaleSlack;
+  const bool rescale = __builtin_amdgcn_ballot_w64(need) != 0;
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb) {
+    const float m_new = rescale ? fmaxf(rw.m[nb], mx[nb]) : rw.m[nb];
+    corr[nb] = __builtin_amdgcn_exp2f(rw.m[nb] - m_new);  // 0 on the first tile (m = -inf)
+    rw.m[nb] = m_new;
+    float ls = 0.0f;
+    float e[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      e[r] = __builtin_amdgcn_exp2f(x[nb][r] - m_new);  // 0 for masked keys
+      ls += e[r];
+    }
+    rw.l[nb] = rw.l[nb] * corr[nb] + ls;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      p[nb][h] = half8_t{static_cast<_Float16>(e[8 * h + 0]), static_cast<_Float16>(e[8 * h + 1]),
+                         static_cast<_Float16>(e[8 * h + 2]), static_cast<_Float16>(e[8 * h + 3]),
+                         static_cast<_Float16>(e[8 * h + 4]), static_cast<_Float16>(e[8 * h + 5]),
+                         static_cast<_Float16>(e[8 * h + 6]), static_cast<_Float16>(e[8 * h + 7])};
+  }
+  return rescale;
+}
+
+__device__ __attribute__((always_inline)) inline void rescale_o(float16_t (&o)[kNB][8],
+                                                               const float (&corr)[kNB]) {
+#pragma unroll
+  for (int nb = 0; nb < kNB; ++nb)
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        o[nb][b][r] *= corr[nb];
 }
 
 }  // namespace prefill_detail
 
 // Items [first, first + count) (grid-stride). Item -> (KV head, token block) as described at
-// attn_prefill_items. Per workgroup: tokens [16 b, 16 b + 16) x 8 heads of one KV head; wave w
-// owns tokens 16 b + 4 w .. + 4 as one MFMA column block of 32 query rows (row n = token offset
+// attn_prefill_items. Per workgroup: tokens [32 b, 32 b + 32) x 8 heads of one KV head; wave w
+// owns tokens 32 b + 8 w .. + 8 as two MFMA column blocks of 32 query rows (row n = token offset
 // n / 8, head n % 8).
 //
-// K/V tiles of 32 keys stream into a 3-stage LDS ring with direct global->LDS loads (no VGPR
-// staging); one barrier per tile. Per tile each wave computes S^T = K Q^T (16 MFMAs over
-// head_dim 256; Q^T resident in registers as f16,
-// pre-scaled by 1/16), masks causally, updates the online softmax in log2 units on the lane's own
-// query columns (rescaling the accumulators only when a max grows by more than 2^8), and
-// accumulates O^T += V^T P^T (16 MFMAs: P^T stays in the S^T accumulator layout, V^T comes
-// from ds_read_b64_tr_b16 with keys ordered to match). The gate and 1/l are applied at the store.
+// K/V tiles of 32 keys stream into a 3-stage LDS ring by direct global->LDS loads; one barrier
+// per tile. Software pipeline per tile i: S^T(i + 1) = K Q^T (32 MFMAs, each K operand feeding
+// both column blocks, Q^T resident as f16 pre-scaled by log2(e)/16), then O^T += V^T P^T(i) (32
+// MFMAs, V^T from ds_read_b64_tr_b16), then the online softmax of tile i + 1 -- independent of
+// the P V MFMAs, so it runs under them. Keys past a row's causal limit are masked only in the
+// (at most two) diagonal tiles of a wave; the gate and 1/l are applied at the store.
 template <int kBlock>
 __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsigned count) {
   using namespace prefill_detail;
   using attn::kDim;
   static_assert(kBlock == 256, "four waves per prefill workgroup");
   constexpr int kGroup = attn::kQHeads / attn::kKvHeads;
-  constexpr int kNB = kAttnQBlocksPerWave;  // 32-row MFMA column blocks per wave
+  constexpr unsigned kWaveTokens = 4 * kNB;
   __shared__ Shared sh;
   const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned col = lane & 31u, hi = lane >> 5;  // MFMA column / lane half
   const unsigned blocks = (p.n + kAttnQBlock - 1) / kAttnQBlock;
-  const unsigned k_lds0 = cdna4::lds_offset(sh.k[0]), v_lds0 = cdna4::lds_offset(sh.v[0]);
+  const unsigned lds0 = cdna4::lds_offset(sh.kv);
+
+  // Per-lane constant addresses. Copy: instruction i moves rows 8 w + 2 i + lane / 32.
+  unsigned copy_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned row = 8 * wave + 2 * i + (lane >> 5);
+    copy_off[i] = row * kRowBytes + swz(row, lane & 31u) * 16;
+  }
+  // S^T A operand (key row col, chunk 2 st + hi): (col 512 + 16 hi + 32 (col % 16)) ^ 32 st.
+  const unsigned kb = lds0 + col * kRowBytes + 16 * hi + 32 * (col & 15u);
+  // V^T transpose reads: rows 16 step + vrow (+ 8), chunk 4 b + vchunk, byte vbyte, i.e.
+  // (512 vrow + vbyte + 16 (vchunk ^ 2 vrow)) ^ (64 b) [^ 256, + 4096 for rows + 8] + 8192 step.
+  unsigned vb[8][2];  // tile slot 0; + slot * 16 KiB for the others
+  {
+    const unsigned g = lane >> 4, j = lane & 15u;
+    const unsigned vrow = 4 * (g >> 1) + j / 4, vchunk = 2 * (g & 1u) + (j % 4) / 2;
+    const unsigned vbyte = 8 * ((j % 4) & 1u);
+    const unsigned base = vrow * kRowBytes + vbyte + 16 * (vchunk ^ (2 * vrow));
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      vb[b][0] = lds0 + kVBase + (base ^ (64u * b));
+      vb[b][1] = lds0 + kVBase + 4096 + (base ^ (64u * b) ^ 256u);
+    }
+  }
 
   for (unsigned item = first + blockIdx.x; item < first + count; item += gridDim.x) {
     const unsigned slot = item % 8, kvh = slot / 4;
@@ -160,14 +355,25 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * kDim;
     const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * kDim;
     const unsigned tiles = (kv_end + kKeys - 1) / kKeys;
+    auto copy = [&](unsigned ti) __attribute__((always_inline)) {
+      const unsigned st = ti % kStages;
+      const unsigned k_lds = lds0 + st * kTileBytes + wave * 4096;
+      const unsigned v_lds = lds0 + kVBase + st * kTileBytes + wave * 4096;
+      if ((ti + 1) * kKeys <= kv_end)
+        copy_tile(K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
+                  copy_off, k_lds, v_lds);
+      else
+        copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, k_lds - wave * 4096,
+                          v_lds - wave * 4096, wave, lane);
+    };
 
     // Start streaming before anything else: tiles 0 and 1.
-    load_tile(K, V, 0, kv_end - 1, k_lds0, v_lds0, wave, lane);
+    copy(0);
     if (tiles > 1)
-      load_tile(K, V, kKeys, kv_end - 1, k_lds0 + kTileBytes, v_lds0 + kTileBytes, wave, lane);
+      copy(1);
 
-    // This lane's query rows: block nb -> token tq[nb], head kvh * 8 + hq.
-    const unsigned tw = t0 + 4 * kNB * wave, hq = col % kGroup;
+    // This wave's rows: block nb -> token tq[nb] = tw + 4 nb + col / 8, head kvh * 8 + col % 8.
+    const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
     unsigned tq[kNB], lim[kNB];
     bool q_valid[kNB];
 #pragma unroll
@@ -178,25 +384,29 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
       lim[nb] = p.pos0 + tq[nb];  // last visible key
     }
     const bool wave_active = tw < p.n;
-    const unsigned wave_lim = p.pos0 + min(tw + 4 * kNB - 1, p.n - 1);  // last key any row sees
-    const unsigned wave_lim_lo = p.pos0 + tw;                 // every row sees keys <= this
+    // Tiles this wave needs, and how many of them every row of the wave sees in full.
+    const unsigned wave_tiles =
+        wave_active ? (p.pos0 + min(tw + kWaveTokens - 1, p.n - 1)) / kKeys + 1 : 0;
+    const unsigned full_tiles = wave_active ? (p.pos0 + tw + 1) / kKeys : 0;
 
-    // Q^T operands: dims 16 s + 8 hi + j of the lane's rows, scaled by 1/16 (exact in f16).
-    half8_t qb[kNB][16];
+    Rows rw;
+    constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
 #pragma unroll
     for (int nb = 0; nb < kNB; ++nb) {
       const float* src =
           p.q + (std::size_t{tq[nb]} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
-      const float z = q_valid[nb] ? 0.0625f : 0.0f;
+      const float z = q_valid[nb] ? kScale : 0.0f;
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * s);
-        const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * s + 4);
-        qb[nb][s] = half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
-                            static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
-                            static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
-                            static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
+      for (int st = 0; st < 16; ++st) {
+        const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
+        rw.q[nb][st] = half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
+                               static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
+                               static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
+                               static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
       }
+      rw.m[nb] = -__builtin_inff();
+      rw.l[nb] = 0.0f;
     }
     float16_t oacc[kNB][8];
 #pragma unroll
@@ -204,109 +414,73 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
 #pragma unroll
       for (int b = 0; b < 8; ++b)
         oacc[nb][b] = float16_t{};
-    float m_run[kNB], l_run[kNB];
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb)
-      m_run[nb] = -__builtin_inff(), l_run[nb] = 0.0f;
+    half8_t pb[kNB][2];
+    float corr[kNB];
 
-    // Per-lane LDS byte offsets of the S^T (K) and P V (V^T, transpose) operands within a tile.
-    const unsigned g = lane >> 4, j = lane & 15u;
-    const unsigned vrow = 4 * (g >> 1) + j / 4;                   // + 16 step (+ 8 upper half)
-    const unsigned vchunk = 2 * (g & 1u) + (j % 4) / 2;           // + 4 b
-    const unsigned vbyte = 8 * ((j % 4) & 1u);
-
-    for (unsigned ti = 0; ti < tiles; ++ti) {
-      // Tile ti has landed once at most the 8 loads of tile ti + 1 are still in flight.
-      if (ti + 1 < tiles)
-        cdna4::wait_vmcnt<8>();
-      else
+    // Scores and softmax of tile ti; true if the accumulators must then be rescaled by corr.
+    auto front = [&](auto masked_tag, unsigned ti) __attribute__((always_inline)) -> bool {
+      float16_t s[kNB];
+      scores(s, rw, kb + (ti % kStages) * kTileBytes);
+      return softmax<decltype(masked_tag)::value>(s, rw, pb, corr, ti * kKeys, lim, hi);
+    };
+    using Full = std::integral_constant<bool, false>;
+    using Masked = std::integral_constant<bool, true>;
+    // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (it is the
+    // only copy in flight), every wave's by the barrier, which also says that all waves are done
+    // with tile ti - 1, whose slot then receives tile ti + 2.
+    auto sync_copy = [&](unsigned ti) __attribute__((always_inline)) {
+      if (ti + 1 < tiles) {
         cdna4::wait_vmcnt<0>();
-      __syncthreads();  // every wave's share of tile ti is in LDS; tile ti - 1 is fully read
-      if (ti + 2 < tiles) {
-        const unsigned st = (ti + 2) % kStages;
-        load_tile(K, V, (ti + 2) * kKeys, kv_end - 1, k_lds0 + st * kTileBytes,
-                  v_lds0 + st * kTileBytes, wave, lane);
+        __syncthreads();
+        if (ti + 2 < tiles)
+          copy(ti + 2);
       }
-      const unsigned k0 = ti * kKeys, buf = ti % kStages;
-      if (!wave_active || k0 > wave_lim)
-        continue;  // wave-uniform: no row of this wave sees these keys
-      const unsigned char* kt = sh.k[buf];
-      const unsigned char* vt = sh.v[buf];
+    };
 
-      // S^T[key][row] for 32 keys x 2 x 32 rows.
-      float16_t sacc[kNB];
-#pragma unroll
-      for (int nb = 0; nb < kNB; ++nb)
-        sacc[nb] = float16_t{};
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const half8_t a =
-            *reinterpret_cast<const half8_t*>(kt + col * kRowBytes + swz(col, 2 * s + hi) * 16);
-#pragma unroll
-        for (int nb = 0; nb < kNB; ++nb)
-          sacc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[nb][s], sacc[nb], 0, 0, 0);
-      }
-      const bool full = k0 + kKeys - 1 <= wave_lim_lo;  // no key of the tile is masked
-      half8_t pb[kNB][2];
-#pragma unroll
-      for (int nb = 0; nb < kNB; ++nb) {
-        float x[16];
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
-          x[r] = (full || key <= lim[nb]) ? sacc[nb][r] * kLog2e : -__builtin_inff();
-          mx = fmaxf(mx, x[r]);
-        }
-        mx = cdna4::max_xor32(mx);
-        // Lazy rescale: keep the reference max unless this tile exceeds it by the slack.
-        if (__builtin_amdgcn_ballot_w64(mx > m_run[nb] + kRescaleSlack)) {
-          const float m_new = fmaxf(m_run[nb], mx);
-          const float corr = __builtin_amdgcn_exp2f(m_run[nb] - m_new);  // 0 on the first tile
-          l_run[nb] *= corr;
-#pragma unroll
-          for (int b = 0; b < 8; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              oacc[nb][b][r] *= corr;
-          m_run[nb] = m_new;
-        }
-        float ls = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pr = __builtin_amdgcn_exp2f(x[r] - m_run[nb]);
-          ls += pr;
-          pb[nb][r / 8][r % 8] = static_cast<_Float16>(pr);
-        }
-        l_run[nb] += ls;
-      }
-      // O^T[d][row] += V^T[d][key] P^T[key][row]; k-slot 8 hi + j <-> key 16 step + 4 hi +
-      // (j < 4 ? j : j + 4), matching the S^T accumulator rows this lane holds.
-#pragma unroll
-      for (int step = 0; step < 2; ++step) {
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const unsigned r0 = 16 * step + vrow, r1 = r0 + 8, ch = 4 * b + vchunk;
-          const half4_t lo = read_tr(vt + r0 * kRowBytes + swz(r0, ch) * 16 + vbyte);
-          const half4_t up = read_tr(vt + r1 * kRowBytes + swz(r1, ch) * 16 + vbyte);
-          const half8_t a = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-#pragma unroll
-          for (int nb = 0; nb < kNB; ++nb)
-            oacc[nb][b] =
-                __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[nb][step], oacc[nb][b], 0, 0, 0);
-        }
-      }
+    cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
+    __syncthreads();
+    // Tile 0 is visible to every row (key 0); o is still zero, so it needs no rescale.
+    if (wave_tiles > 0) {
+      if (full_tiles > 0)
+        front(Full{}, 0);
+      else
+        front(Masked{}, 0);
+    }
+    // Each iteration: P V of tile ti, then the scores and softmax of tile ti + 1, which do not
+    // depend on those MFMAs; the accumulators are rescaled (rarely) only after tile ti is in.
+    // First the tiles every row of the wave sees in full (no mask code at all), ...
+    // A rescale leaves the inner loop, so inside it the accumulators change only through MFMAs.
+    unsigned ti = 0;
+    while (ti + 1 < full_tiles) {
+      bool rescale = false;
+      do {
+        sync_copy(ti);
+        accumulate(oacc, pb, vb, (ti % kStages) * kTileBytes);
+        rescale = front(Full{}, ti + 1);
+        ++ti;
+      } while (!rescale && ti + 1 < full_tiles);
+      if (rescale)
+        rescale_o(oacc, corr);
+    }
+    // ... then the diagonal tiles (at most two for the wave) and the ones it skips.
+    for (; ti < tiles; ++ti) {
+      sync_copy(ti);
+      if (ti >= wave_tiles)
+        continue;  // wave-uniform: no row of this wave sees these keys (barriers stay aligned)
+      accumulate(oacc, pb, vb, (ti % kStages) * kTileBytes);
+      if (ti + 1 < wave_tiles && front(Masked{}, ti + 1))
+        rescale_o(oacc, corr);
     }
     __syncthreads();  // the ring is reused by the next item
 
     // Row totals: each column's keys per tile were split between the lane halves.
 #pragma unroll
     for (int nb = 0; nb < kNB; ++nb) {
-      const float l_tot = cdna4::sum_xor32(l_run[nb]);
+      const float l_tot = cdna4::sum_xor32(rw.l[nb]);
       if (!q_valid[nb])
         continue;
       const unsigned head = kvh * kGroup + hq;
-      const float inv_l = 1.0f / l_tot;
+      const float inv_l = __builtin_amdgcn_rcpf(l_tot);
       const float* gate = p.qg + std::size_t{tq[nb]} * p.qg_stride + head * 2 * kDim + kDim;
       float* out = p.core + (std::size_t{tq[nb]} * attn::kQHeads + head) * kDim;
 #pragma unroll
@@ -316,10 +490,10 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
           const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
           const float4 gv = *reinterpret_cast<const float4*>(gate + d0);
           float4 o;
-          o.x = oacc[nb][b][4 * r4 + 0] * inv_l / (1.0f + __expf(-gv.x));
-          o.y = oacc[nb][b][4 * r4 + 1] * inv_l / (1.0f + __expf(-gv.y));
-          o.z = oacc[nb][b][4 * r4 + 2] * inv_l / (1.0f + __expf(-gv.z));
-          o.w = oacc[nb][b][4 * r4 + 3] * inv_l / (1.0f + __expf(-gv.w));
+          o.x = oacc[nb][b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.x));
+          o.y = oacc[nb][b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.y));
+          o.z = oacc[nb][b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.z));
+          o.w = oacc[nb][b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.w));
           *reinterpret_cast<float4*>(out + d0) = o;
         }
       }
