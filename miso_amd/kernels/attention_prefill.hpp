@@ -281,6 +281,116 @@ __device__ __attribute__((always_inline)) inline bool softmax(const float16_t (&
   return rescale;
 }
 
+// One fully visible tile, software-pipelined (one column block per wave): the online softmax
+// of tile ti (scores s, complete) gives P(ti); the scores of tile ti + 1 accumulate into s_next
+// from the K operands at kb (ring slot of tile ti + 1); O += V^T(ti) P(ti) reads V at vb + v_off.
+// The MFMAs are interleaved with the softmax VALU work and the LDS reads run two operands ahead,
+// in a fixed order (scheduling barriers between the groups):
+//   group 1: row max, rescale decision, S steps 0-1;  [rescale of O, rarely]
+//   group 2: S steps 2-9, each with two exponentials and the running sums;
+//   group 3: the 16 P V MFMAs with S steps 10-15 between them.
+// m, l and O are updated in place (O rescaled before P(ti) is added). kMasked: keys k0 + key(r)
+// past the row's causal limit lim (the diagonal tiles) are excluded; kNext: tile ti + 1 exists
+// for this wave (otherwise no S MFMAs are issued).
+template <bool kMasked, bool kNext>
+__device__ __attribute__((always_inline)) inline void tile_step(float16_t& s, float16_t& s_next,
+                                                               Rows& rw, float16_t (&o)[8],
+                                                               unsigned kb,
+                                                               const unsigned (&vb)[8][2],
+                                                               unsigned v_off, unsigned k0,
+                                                               unsigned lim, unsigned hi) {
+  static_assert(kNB == 1, "the pipelined tile handles one column block");
+  const half8_t(&q)[16] = rw.q[0];
+  half8_t ka[16];
+  auto kread = [&](unsigned st) __attribute__((always_inline)) {
+    if (kNext)
+      ka[st] = lds_read_b128(kb ^ (32u * st));
+  };
+  auto smma = [&](unsigned st) __attribute__((always_inline)) {
+    if (kNext)
+      s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], q[st],
+                                                      st == 0 ? float16_t{} : s_next, 0, 0, 0);
+  };
+  // Group 1.
+  kread(0);
+  kread(1);
+  if (kMasked) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
+      s[r] = key <= lim ? s[r] : -__builtin_inff();
+    }
+  }
+  float a = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2)
+    a = fmaxf(fmaxf(a, s[r]), s[r + 1]);
+  const float mx = cdna4::max_xor32(fmaxf(a, s[15]));
+  const bool rescale = __builtin_amdgcn_ballot_w64(mx > rw.m[0] + kRescaleSlack) != 0;
+  const float m_new = rescale ? fmaxf(rw.m[0], mx) : rw.m[0];
+  const float corr = __builtin_amdgcn_exp2f(rw.m[0] - m_new);
+  rw.m[0] = m_new;
+  kread(2);
+  smma(0);
+  kread(3);
+  smma(1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (rescale) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        o[b][r] *= corr;
+  }
+  // Group 2: numerators of tile ti under S steps 2-9.
+  float e[16], ls = 0.0f;
+#pragma unroll
+  for (unsigned st = 2; st < 10; ++st) {
+    kread(st + 2);
+    smma(st);
+    const unsigned r = 2 * (st - 2);
+    e[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+    e[r + 1] = __builtin_amdgcn_exp2f(s[r + 1] - m_new);
+    ls += e[r] + e[r + 1];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  rw.l[0] = rw.l[0] * corr + ls;
+  half8_t p[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    p[h] = half8_t{static_cast<_Float16>(e[8 * h + 0]), static_cast<_Float16>(e[8 * h + 1]),
+                   static_cast<_Float16>(e[8 * h + 2]), static_cast<_Float16>(e[8 * h + 3]),
+                   static_cast<_Float16>(e[8 * h + 4]), static_cast<_Float16>(e[8 * h + 5]),
+                   static_cast<_Float16>(e[8 * h + 6]), static_cast<_Float16>(e[8 * h + 7])};
+  // Group 3: P V, 32-dim block b and key step; V^T operands read four MFMAs ahead.
+  constexpr unsigned kAhead = 4;
+  half4_t vlo[kAhead], vup[kAhead];
+  auto vread = [&](unsigned i) __attribute__((always_inline)) {
+    const unsigned b = i / 2, step = i % 2;
+    vlo[i % kAhead] = read_tr(vb[b][0] + v_off + 8192u * step);
+    vup[i % kAhead] = read_tr(vb[b][1] + v_off + 8192u * step);
+  };
+#pragma unroll
+  for (unsigned i = 0; i < kAhead; ++i)
+    vread(i);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (unsigned i = 0; i < 16; ++i) {
+    const half4_t lo = vlo[i % kAhead], up = vup[i % kAhead];
+    const half8_t av = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+    if (i + kAhead < 16)
+      vread(i + kAhead);
+    o[i / 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, p[i % 2], o[i / 2], 0, 0, 0);
+    if (i % 3 == 0 && 10 + i / 3 < 16) {  // S steps 10-15 after P V MFMAs 0, 3, ..., 15
+      const unsigned st = 10 + i / 3;
+      if (st + 2 < 16)
+        kread(st + 2);
+      smma(st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 __device__ __attribute__((always_inline)) inline void rescale_o(float16_t (&o)[kNB][8],
                                                                const float (&corr)[kNB]) {
 #pragma unroll
@@ -417,14 +527,6 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     half8_t pb[kNB][2];
     float corr[kNB];
 
-    // Scores and softmax of tile ti; true if the accumulators must then be rescaled by corr.
-    auto front = [&](auto masked_tag, unsigned ti) __attribute__((always_inline)) -> bool {
-      float16_t s[kNB];
-      scores(s, rw, kb + (ti % kStages) * kTileBytes);
-      return softmax<decltype(masked_tag)::value>(s, rw, pb, corr, ti * kKeys, lim, hi);
-    };
-    using Full = std::integral_constant<bool, false>;
-    using Masked = std::integral_constant<bool, true>;
     // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (it is the
     // only copy in flight), every wave's by the barrier, which also says that all waves are done
     // with tile ti - 1, whose slot then receives tile ti + 2.
@@ -439,38 +541,36 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
 
     cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
     __syncthreads();
-    // Tile 0 is visible to every row (key 0); o is still zero, so it needs no rescale.
-    if (wave_tiles > 0) {
-      if (full_tiles > 0)
-        front(Full{}, 0);
-      else
-        front(Masked{}, 0);
-    }
-    // Each iteration: P V of tile ti, then the scores and softmax of tile ti + 1, which do not
-    // depend on those MFMAs; the accumulators are rescaled (rarely) only after tile ti is in.
-    // First the tiles every row of the wave sees in full (no mask code at all), ...
-    // A rescale leaves the inner loop, so inside it the accumulators change only through MFMAs.
+    // s: the scores of tile ti at the top of iteration ti (tile 0: computed here).
+    float16_t s[kNB];
+    if (wave_tiles > 0)
+      scores(s, rw, kb);
+    // One pass over the workgroup's tiles in three phases per wave, each a loop with a single
+    // body (the per-wave bounds differ; every wave still runs sync_copy once per tile, in order):
+    // the tiles its rows see in full, then its diagonal tiles (the last one has no successor),
+    // then the tiles it does not need.
+    float16_t s_next;
     unsigned ti = 0;
-    while (ti + 1 < full_tiles) {
-      bool rescale = false;
-      do {
-        sync_copy(ti);
-        accumulate(oacc, pb, vb, (ti % kStages) * kTileBytes);
-        rescale = front(Full{}, ti + 1);
-        ++ti;
-      } while (!rescale && ti + 1 < full_tiles);
-      if (rescale)
-        rescale_o(oacc, corr);
-    }
-    // ... then the diagonal tiles (at most two for the wave) and the ones it skips.
-    for (; ti < tiles; ++ti) {
+    for (; ti < full_tiles; ++ti) {
       sync_copy(ti);
-      if (ti >= wave_tiles)
-        continue;  // wave-uniform: no row of this wave sees these keys (barriers stay aligned)
-      accumulate(oacc, pb, vb, (ti % kStages) * kTileBytes);
-      if (ti + 1 < wave_tiles && front(Masked{}, ti + 1))
-        rescale_o(oacc, corr);
+      tile_step<false, true>(s[0], s_next, rw, oacc[0], kb + ((ti + 1) % kStages) * kTileBytes, vb,
+                             (ti % kStages) * kTileBytes, 0, 0, hi);
+      s[0] = s_next;
     }
+    for (; ti + 1 < wave_tiles; ++ti) {
+      sync_copy(ti);
+      tile_step<true, true>(s[0], s_next, rw, oacc[0], kb + ((ti + 1) % kStages) * kTileBytes, vb,
+                            (ti % kStages) * kTileBytes, ti * kKeys, lim[0], hi);
+      s[0] = s_next;
+    }
+    if (ti < wave_tiles) {
+      sync_copy(ti);
+      tile_step<true, false>(s[0], s_next, rw, oacc[0], 0, vb, (ti % kStages) * kTileBytes,
+                             ti * kKeys, lim[0], hi);
+      ++ti;
+    }
+    for (; ti < tiles; ++ti)
+      sync_copy(ti);
     __syncthreads();  // the ring is reused by the next item
 
     // Row totals: each column's keys per tile were split between the lane halves.
