@@ -281,6 +281,25 @@ __device__ __attribute__((always_inline)) inline bool softmax(const float16_t (&
   return rescale;
 }
 
+// o *= c for accumulators that live in AGPRs, element by element in place (read to a VGPR,
+// multiply, write back). Written as assembly so the AGPR -> VGPR copies stay inside the caller's
+// (rarely taken) branch: plain C++ lets the compiler hoist all 128 copies to the loop head.
+__device__ __attribute__((always_inline)) inline void scale_acc(float16_t (&o)[8], float c) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = o[b][r], tmp;
+      asm volatile(
+          "v_accvgpr_read_b32 %1, %0\n\t"
+          "v_mul_f32 %1, %1, %2\n\t"
+          "v_accvgpr_write_b32 %0, %1"
+          : "+a"(x), "=&v"(tmp)
+          : "v"(c));
+      o[b][r] = x;
+    }
+}
+
 // One fully visible tile, software-pipelined (one column block per wave): the online softmax
 // of tile ti (scores s, complete) gives P(ti); the scores of tile ti + 1 accumulate into s_next
 // from the K operands at kb (ring slot of tile ti + 1); O += V^T(ti) P(ti) reads V at vb + v_off.
@@ -335,13 +354,8 @@ __device__ __attribute__((always_inline)) inline void tile_step(float16_t& s, fl
   kread(3);
   smma(1);
   __builtin_amdgcn_sched_barrier(0);
-  if (rescale) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        o[b][r] *= corr;
-  }
+  if (rescale)
+    scale_acc(o, corr);
   // Group 2: numerators of tile ti under S steps 2-9.
   float e[16], ls = 0.0f;
 #pragma unroll
