@@ -61,10 +61,9 @@ struct AttnPrefillParams {
   unsigned qg_stride;  // 8192 packed, or 9216 when q/k/v share a proj buffer
 };
 
-// Tokens per workgroup: 4 waves x 8 tokens x 8 query heads = 64 query rows per wave, two 32-row
-// MFMA column blocks.
+// Tokens per workgroup: 4 waves x 4 tokens; a wave's 4 tokens x 8 query heads are the 32 rows of
+// one MFMA column block.
 constexpr unsigned kAttnQBlock = 16;
-constexpr int kAttnQBlocksPerWave = 1;
 
 // Grid size. Items come in groups of 8 (one per XCD of the round-robin dispatch): slots 0-3 of a
 // group serve KV head 0 and slots 4-7 KV head 1, so each XCD's L2 holds one KV head's stream, and
@@ -85,7 +84,6 @@ constexpr int kKeys = 32;                      // keys per K/V tile (the M side 
 constexpr int kStages = 3;                     // LDS ring depth
 constexpr int kRowBytes = attn::kDim * 2;      // 512: one f16 row
 constexpr int kTileBytes = kKeys * kRowBytes;  // 16 KiB per K or V tile
-constexpr int kNB = kAttnQBlocksPerWave;       // 32-row MFMA column blocks per wave
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: numerators stay <= 2^8 between rescales
 
@@ -170,121 +168,56 @@ __device__ __attribute__((always_inline)) inline half4_t read_tr(unsigned addr) 
   return __builtin_bit_cast(half4_t, raw);
 }
 
-// Per-lane state of one wave: 64 query rows as two 32-row column blocks.
+// Per-lane state of one wave (32 query rows = one MFMA column block): the Q^T B operands, dims
+// 16 s + 8 hi + j of the lane's row, x log2(e)/16; the reference max m and running sum l; and -m
+// in all 16 elements, the initial S^T accumulator, so the scores come out of the MFMAs relative
+// to m.
 struct Rows {
-  half8_t q[kNB][16];  // Q^T B operands: dims 16 s + 8 hi + j of the lane's rows, x log2(e)/16
-  float m[kNB], l[kNB];
+  half8_t q[16];
+  float m, l;
+  float16_t negm;
 };
 
-// S^T[key][row] = K Q^T for one tile (32 keys x 64 rows): 16 k-steps over head_dim, each K
-// operand read once and used by both column blocks. kb: the lane's operand address in the tile's
-// slot before the per-step XOR.
-__device__ __attribute__((always_inline)) inline void scores(float16_t (&s)[kNB], const Rows& rw,
-                                                            unsigned kb) {
+__device__ __attribute__((always_inline)) inline float16_t splat16(float x) {
+  float16_t v;
 #pragma unroll
-  for (int nb = 0; nb < kNB; ++nb)
-    s[nb] = float16_t{};
-#pragma unroll
-  for (unsigned st = 0; st < 16; ++st) {
-    const half8_t a = lds_read_b128(kb ^ (32u * st));
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb)
-      s[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, rw.q[nb][st], s[nb], 0, 0, 0);
-  }
+  for (int r = 0; r < 16; ++r)
+    v[r] = x;
+  return v;
 }
 
-// O^T[d][row] += V^T[d][key] P^T[key][row] for one tile; k-slot 8 hi + j of a step holds key
-// 16 step + 4 hi + (j < 4 ? j : j + 4), which is how the S^T accumulator rows lie in the lane, so
-// P^T is the softmax output as is. vb[b][u]: the lane's transpose-read addresses for 32-dim block
-// b (u = 1: rows + 8) in tile slot 0; slot_off moves them to the tile's slot.
-__device__ __attribute__((always_inline)) inline void accumulate(float16_t (&o)[kNB][8],
-                                                                const half8_t (&p)[kNB][2],
-                                                                const unsigned (&vb)[8][2],
-                                                                unsigned slot_off) {
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const unsigned a0 = vb[b][0] + slot_off, a1 = vb[b][1] + slot_off;
-#pragma unroll
-    for (unsigned step = 0; step < 2; ++step) {
-      const half4_t lo = read_tr(a0 + 8192u * step);
-      const half4_t up = read_tr(a1 + 8192u * step);
-      const half8_t a = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-#pragma unroll
-      for (int nb = 0; nb < kNB; ++nb)
-        o[nb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[nb][step], o[nb][b], 0, 0, 0);
-    }
-  }
+// max(a, b, c) in one instruction (the scores are never NaN; no canonicalisation is needed).
+__device__ __attribute__((always_inline)) inline float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 
-// Online softmax of one tile's scores (log2 units) into f16 numerators. kMasked: key k0 + key(r)
-// is visible to the lane's row nb iff it is <= lim[nb]. The reference max moves only when a tile
-// exceeds it by more than the slack; that wave-uniform case returns true after setting `corr`
-// (the factor the accumulators must be scaled by before the next tile is added).
-template <bool kMasked>
-__device__ __attribute__((always_inline)) inline bool softmax(const float16_t (&s)[kNB],
-                                                             Rows& rw, half8_t (&p)[kNB][2],
-                                                             float (&corr)[kNB], unsigned k0,
-                                                             const unsigned (&lim)[kNB],
-                                                             unsigned hi) {
-  float x[kNB][16], mx[kNB];
+// The value of x, opaque to the optimiser: address bases laundered this way stay one register,
+// so the constant parts of each address fold into the LDS instructions' offsets instead of
+// being re-added per access.
+__device__ __attribute__((always_inline)) inline unsigned opaque(unsigned x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// S^T[key][row] = K Q^T for one tile (32 keys x 32 rows): 16 k-steps over head_dim. kb: the
+// lane's operand address in the tile's slot before the per-step XOR.
+__device__ __attribute__((always_inline)) inline float16_t scores(const Rows& rw, unsigned kb) {
+  float16_t s{};
 #pragma unroll
-  for (int nb = 0; nb < kNB; ++nb) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      x[nb][r] = s[nb][r];
-  }
-  if (kMasked) {  // the diagonal tiles only
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
-        x[nb][r] = key <= lim[nb] ? x[nb][r] : -__builtin_inff();
-      }
-  }
-#pragma unroll
-  for (int nb = 0; nb < kNB; ++nb) {
-    float a = fmaxf(fmaxf(x[nb][0], x[nb][1]), x[nb][2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2)
-      a = fmaxf(fmaxf(a, x[nb][r]), x[nb][r + 1]);
-    mx[nb] = fmaxf(a, x[nb][15]);
-  }
-#pragma unroll
-  for (int nb = 0; nb < kNB; ++nb)
-    mx[nb] = cdna4::max_xor32(mx[nb]);  // the other 16 keys of the column are in lane ^ 32
-  bool need = false;
-#pragma unroll
-  for (int nb = 0; nb < kNB; ++nb)
-    need |= mx[nb] > rw.m[nb] + kRescaleSlack;
-  const bool rescale = __builtin_amdgcn_ballot_w64(need) != 0;
-#pragma unroll
-  for (int nb = 0; nb < kNB; ++nb) {
-    const float m_new = rescale ? fmaxf(rw.m[nb], mx[nb]) : rw.m[nb];
-    corr[nb] = __builtin_amdgcn_exp2f(rw.m[nb] - m_new);  // 0 on the first tile (m = -inf)
-    rw.m[nb] = m_new;
-    float ls = 0.0f;
-    float e[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      e[r] = __builtin_amdgcn_exp2f(x[nb][r] - m_new);  // 0 for masked keys
-      ls += e[r];
-    }
-    rw.l[nb] = rw.l[nb] * corr[nb] + ls;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      p[nb][h] = half8_t{static_cast<_Float16>(e[8 * h + 0]), static_cast<_Float16>(e[8 * h + 1]),
-                         static_cast<_Float16>(e[8 * h + 2]), static_cast<_Float16>(e[8 * h + 3]),
-                         static_cast<_Float16>(e[8 * h + 4]), static_cast<_Float16>(e[8 * h + 5]),
-                         static_cast<_Float16>(e[8 * h + 6]), static_cast<_Float16>(e[8 * h + 7])};
-  }
-  return rescale;
+  for (unsigned st = 0; st < 16; ++st)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds_read_b128(kb ^ (32u * st)), rw.q[st], s, 0, 0,
+                                               0);
+  return s;
 }
 
 // o *= c for accumulators that live in AGPRs, element by element in place (read to a VGPR,
 // multiply, write back). Written as assembly so the AGPR -> VGPR copies stay inside the caller's
-// (rarely taken) branch: plain C++ lets the compiler hoist all 128 copies to the loop head.
+// (rarely taken) branch: plain C++ lets the compiler hoist all 128 copies to the loop head. The
+// leading no-ops cover the wait states between an MFMA writing o and a VALU read of it.
 __device__ __attribute__((always_inline)) inline void scale_acc(float16_t (&o)[8], float c) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
   for (int b = 0; b < 8; ++b)
 #pragma unroll
@@ -300,142 +233,223 @@ __device__ __attribute__((always_inline)) inline void scale_acc(float16_t (&o)[8
     }
 }
 
-// One fully visible tile, software-pipelined (one column block per wave): the online softmax
-// of tile ti (scores s, complete) gives P(ti); the scores of tile ti + 1 accumulate into s_next
-// from the K operands at kb (ring slot of tile ti + 1); O += V^T(ti) P(ti) reads V at vb + v_off.
-// The MFMAs are interleaved with the softmax VALU work and the LDS reads run two operands ahead,
-// in a fixed order (scheduling barriers between the groups):
-//   group 1: row max, rescale decision, S steps 0-1;  [rescale of O, rarely]
-//   group 2: S steps 2-9, each with two exponentials and the running sums;
-//   group 3: the 16 P V MFMAs with S steps 10-15 between them.
-// m, l and O are updated in place (O rescaled before P(ti) is added). kMasked: keys k0 + key(r)
-// past the row's causal limit lim (the diagonal tiles) are excluded; kNext: tile ti + 1 exists
-// for this wave (otherwise no S MFMAs are issued).
-template <bool kMasked, bool kNext>
-__device__ __attribute__((always_inline)) inline void tile_step(float16_t& s, float16_t& s_next,
-                                                               Rows& rw, float16_t (&o)[8],
-                                                               unsigned kb,
-                                                               const unsigned (&vb)[8][2],
-                                                               unsigned v_off, unsigned k0,
+// The scores of one tile as the softmax consumes them: S^T values of the lane (keys 8 (r / 4) +
+// 4 hi + r % 4 of the tile, row col) in log2 units relative to the reference max m, with the
+// causal mask applied, and the factor by which O and l were scaled when m moved for this tile.
+struct Pending {
+  float s[16];
+  float corr;
+};
+
+// Scores of a finished S^T accumulator (relative to m) -> Pending: mask (keys past lim, diagonal
+// tiles only), row max over the 32 keys (16 per lane half), and the lazy rescale decision: m
+// moves only when the tile exceeds it by more than the slack, wave-uniformly. The work is split
+// into part(0) .. part(4) so it can sit between MFMAs; after part(4), `moved` says whether m moved
+// (by `delta` >= 0 in the lane's row), and the caller must then finish(): shift the pending
+// scores, reset the accumulator init, and scale O by pend.corr before the tile's P V is added.
+template <bool kMasked>
+struct Decide {
+  float run, delta;
+  bool moved;
+  __device__ __attribute__((always_inline)) inline void part(unsigned i, const float16_t& acc,
+                                                              Pending& pend, Rows& rw, unsigned k0,
+                                                              unsigned lim, unsigned hi) {
+    if (i < 4) {  // read 4 scores, mask, running max
+#pragma unroll
+      for (unsigned j = 0; j < 4; ++j) {
+        const unsigned r = 4 * i + j;
+        float x = acc[r];
+        asm volatile("" : "+v"(x));  // the pending scores live in VGPRs, not in the accumulator
+        if (kMasked) {
+          const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
+          x = key <= lim ? x : -__builtin_inff();
+        }
+        pend.s[r] = x;
+      }
+      const float* v = pend.s + 4 * i;
+      run = i == 0 ? max3(v[0], v[1], v[2]) : max3(run, v[0], v[1]);
+      run = i == 0 ? max3(run, v[3], v[3]) : max3(run, v[2], v[3]);
+    } else if (i == 4) {
+      const float mx = cdna4::max_xor32(run);
+      moved = __builtin_amdgcn_ballot_w64(mx > kRescaleSlack) != 0;
+      delta = moved ? fmaxf(mx, 0.0f) : 0.0f;
+      pend.corr = __builtin_amdgcn_exp2f(-delta);
+      rw.m += delta;
+    }
+  }
+  __device__ __attribute__((always_inline)) inline void finish(Pending& pend, Rows& rw) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      pend.s[r] -= delta;
+    rw.negm = splat16(-rw.m);
+    asm volatile("" : "+a"(rw.negm));  // kept where the MFMA reads its accumulator input
+  }
+};
+
+// The first tile of an item: O and l are still 0, so m is simply the tile's row max.
+template <bool kMasked>
+__device__ __attribute__((always_inline)) inline void first_tile(const float16_t& acc,
+                                                                Pending& pend, Rows& rw,
+                                                                unsigned lim, unsigned hi) {
+  float x[16];
+#pragma unroll
+  for (unsigned r = 0; r < 16; ++r) {
+    x[r] = acc[r];
+    if (kMasked) {
+      const unsigned key = 8 * (r / 4) + 4 * hi + (r % 4);
+      x[r] = key <= lim ? x[r] : -__builtin_inff();
+    }
+  }
+  float run = max3(x[0], x[1], x[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2)
+    run = max3(run, x[r], x[r + 1]);
+  rw.m = cdna4::max_xor32(fmaxf(run, x[15]));  // finite: key 0 is visible to every row
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    pend.s[r] = x[r] - rw.m;
+  pend.corr = 0.0f;
+  rw.negm = splat16(-rw.m);
+  asm volatile("" : "+a"(rw.negm));
+}
+
+// One tile of a wave, software-pipelined: tile ti's softmax numerators (from `cur`, decided in
+// the previous step), O += V^T(ti) P^T(ti), and the scores of tile ti + 1 (kNext), which are
+// decided at the end into `cur` for the next step. Three groups of MFMAs, each with the VALU work
+// that depends only on earlier groups, interleaved one MFMA at a time (scheduling barriers):
+//   A: S(ti + 1) k-steps 0-7; numerators of keys r = 0-7 -> P half 0, their sum;
+//   B: S(ti + 1) k-steps 8-15 alternating with the P V MFMAs of key step 0; numerators r = 8-15;
+//   C: the P V MFMAs of key step 1; scores of tile ti + 1 read, masked (kMaskNext) and decided.
+// If m moved for tile ti + 1, O (now holding every tile <= ti) is rescaled at the end.
+// k-slot 8 hi + j of a P V step holds key 16 step + 4 hi + (j < 4 ? j : j + 4), which is how the
+// S^T accumulator rows lie in the lane, so P^T is the numerators as they are. kb: K operand
+// address in slot 0 and
+// k_off the byte offset of tile ti + 1's slot; vb[c] + v_off: the V^T transpose-read address of
+// 32-dim block c (rows 0-7 of key step 0) in tile ti's slot. Block b + 4 lies 256 bytes above
+// block b and rows 8-15 4096 +- 256 bytes above rows 0-7, so four lane bases serve all 32 reads
+// (the rest are instruction offsets).
+template <bool kMaskNext, bool kNext>
+__device__ __attribute__((always_inline)) inline void tile_step(Pending& cur, Rows& rw,
+                                                               float16_t (&o)[8], unsigned kb,
+                                                               unsigned k_off,
+                                                               const unsigned (&vb)[4],
+                                                               unsigned v_off, unsigned k0_next,
                                                                unsigned lim, unsigned hi) {
-  static_assert(kNB == 1, "the pipelined tile handles one column block");
-  const half8_t(&q)[16] = rw.q[0];
+  const unsigned ks = kb + k_off;  // k_off has no bits below 14: the XORs below commute with it
+  unsigned vt[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    vt[c] = opaque(vb[c] + v_off);
   half8_t ka[16];
+  float16_t s_acc;
   auto kread = [&](unsigned st) __attribute__((always_inline)) {
-    if (kNext)
-      ka[st] = lds_read_b128(kb ^ (32u * st));
+    if (kNext && st < 16)
+      ka[st] = lds_read_b128(ks ^ (32u * st));
   };
   auto smma = [&](unsigned st) __attribute__((always_inline)) {
     if (kNext)
-      s_next = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], q[st],
-                                                      st == 0 ? float16_t{} : s_next, 0, 0, 0);
+      s_acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], rw.q[st],
+                                                     st == 0 ? rw.negm : s_acc, 0, 0, 0);
   };
-  // Group 1.
-  kread(0);
-  kread(1);
-  if (kMasked) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
-      s[r] = key <= lim ? s[r] : -__builtin_inff();
-    }
-  }
-  float a = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-  for (int r = 3; r < 15; r += 2)
-    a = fmaxf(fmaxf(a, s[r]), s[r + 1]);
-  const float mx = cdna4::max_xor32(fmaxf(a, s[15]));
-  const bool rescale = __builtin_amdgcn_ballot_w64(mx > rw.m[0] + kRescaleSlack) != 0;
-  const float m_new = rescale ? fmaxf(rw.m[0], mx) : rw.m[0];
-  const float corr = __builtin_amdgcn_exp2f(rw.m[0] - m_new);
-  rw.m[0] = m_new;
-  kread(2);
-  smma(0);
-  kread(3);
-  smma(1);
-  __builtin_amdgcn_sched_barrier(0);
-  if (rescale)
-    scale_acc(o, corr);
-  // Group 2: numerators of tile ti under S steps 2-9.
-  float e[16], ls = 0.0f;
-#pragma unroll
-  for (unsigned st = 2; st < 10; ++st) {
-    kread(st + 2);
-    smma(st);
-    const unsigned r = 2 * (st - 2);
-    e[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
-    e[r + 1] = __builtin_amdgcn_exp2f(s[r + 1] - m_new);
-    ls += e[r] + e[r + 1];
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  rw.l[0] = rw.l[0] * corr + ls;
-  half8_t p[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    p[h] = half8_t{static_cast<_Float16>(e[8 * h + 0]), static_cast<_Float16>(e[8 * h + 1]),
-                   static_cast<_Float16>(e[8 * h + 2]), static_cast<_Float16>(e[8 * h + 3]),
-                   static_cast<_Float16>(e[8 * h + 4]), static_cast<_Float16>(e[8 * h + 5]),
-                   static_cast<_Float16>(e[8 * h + 6]), static_cast<_Float16>(e[8 * h + 7])};
-  // Group 3: P V, 32-dim block b and key step; V^T operands read four MFMAs ahead.
+  // V^T operands in MFMA order (key step 0 for blocks 0-7, then key step 1), four ahead.
   constexpr unsigned kAhead = 4;
   half4_t vlo[kAhead], vup[kAhead];
   auto vread = [&](unsigned i) __attribute__((always_inline)) {
-    const unsigned b = i / 2, step = i % 2;
-    vlo[i % kAhead] = read_tr(vb[b][0] + v_off + 8192u * step);
-    vup[i % kAhead] = read_tr(vb[b][1] + v_off + 8192u * step);
+    if (i < 16) {
+      const unsigned b = i % 8, step = i / 8;
+      const unsigned at = vt[b % 4] + 256u * (b / 4) + 8192u * step;
+      vlo[i % kAhead] = read_tr(at);
+      vup[i % kAhead] = read_tr(at + (b < 4 ? 4096u + 256u : 4096u - 256u));
+    }
   };
-#pragma unroll
-  for (unsigned i = 0; i < kAhead; ++i)
-    vread(i);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (unsigned i = 0; i < 16; ++i) {
+  half8_t p[2];
+  auto pv = [&](unsigned i) __attribute__((always_inline)) {
     const half4_t lo = vlo[i % kAhead], up = vup[i % kAhead];
     const half8_t av = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-    if (i + kAhead < 16)
-      vread(i + kAhead);
-    o[i / 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, p[i % 2], o[i / 2], 0, 0, 0);
-    if (i % 3 == 0 && 10 + i / 3 < 16) {  // S steps 10-15 after P V MFMAs 0, 3, ..., 15
-      const unsigned st = 10 + i / 3;
-      if (st + 2 < 16)
-        kread(st + 2);
-      smma(st);
+    vread(i + kAhead);
+    o[i % 8] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, p[i / 8], o[i % 8], 0, 0, 0);
+  };
+  // Numerators e(r) = 2^s(r) (s is relative to m) as f16 pairs, one exponential per call
+  // (num(2 j) and num(2 j + 1) make pair j: keys r = 2 j, 2 j + 1); their sum, of the rounded
+  // values the MFMAs use, by dot products with (1, 1).
+  const cdna4::half2_t ones{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  cdna4::half2_t e2[8];
+  float x_even[8];
+  float lsum = 0.0f;
+  auto num = [&](unsigned r) __attribute__((always_inline)) {
+    const float x = __builtin_amdgcn_exp2f(cur.s[r]);
+    if (r % 2 == 0) {
+      x_even[r / 2] = x;
+    } else {
+      e2[r / 2] = cdna4::half2_t{static_cast<_Float16>(x_even[r / 2]), static_cast<_Float16>(x)};
+      lsum = __builtin_amdgcn_fdot2(e2[r / 2], ones, lsum, false);
     }
+  };
+  auto pack = [&](unsigned h) __attribute__((always_inline)) {
+    p[h] = half8_t{e2[4 * h][0],     e2[4 * h][1],     e2[4 * h + 1][0], e2[4 * h + 1][1],
+                   e2[4 * h + 2][0], e2[4 * h + 2][1], e2[4 * h + 3][0], e2[4 * h + 3][1]};
+  };
+
+  // Group A.
+  kread(0);
+  kread(1);
+#pragma unroll
+  for (unsigned st = 0; st < 8; ++st) {
+    kread(st + 2);
+    smma(st);
+    num(st);
+    if (st == 3)
+      vread(0), vread(1);
+    if (st == 7)
+      vread(2), vread(3);
     __builtin_amdgcn_sched_barrier(0);
   }
-}
-
-__device__ __attribute__((always_inline)) inline void rescale_o(float16_t (&o)[kNB][8],
-                                                               const float (&corr)[kNB]) {
+  pack(0);
+  // Group B.
 #pragma unroll
-  for (int nb = 0; nb < kNB; ++nb)
+  for (unsigned j = 0; j < 8; ++j) {
+    kread(j + 10);
+    smma(j + 8);
+    num(8 + j);
+    pv(j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  pack(1);
+  rw.l = rw.l * cur.corr + lsum;
+  // Group C.
+  Decide<kMaskNext> dec;
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        o[nb][b][r] *= corr[nb];
+  for (unsigned j = 0; j < 8; ++j) {
+    pv(8 + j);
+    if (kNext && j >= 1 && j <= 5)
+      dec.part(j - 1, s_acc, cur, rw, k0_next, lim, hi);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (kNext && dec.moved) {
+    dec.finish(cur, rw);
+    scale_acc(o, cur.corr);
+  }
 }
 
 }  // namespace prefill_detail
 
 // Items [first, first + count) (grid-stride). Item -> (KV head, token block) as described at
-// attn_prefill_items. Per workgroup: tokens [32 b, 32 b + 32) x 8 heads of one KV head; wave w
-// owns tokens 32 b + 8 w .. + 8 as two MFMA column blocks of 32 query rows (row n = token offset
+// attn_prefill_items. Per workgroup: tokens [16 b, 16 b + 16) x 8 heads of one KV head; wave w
+// owns tokens 16 b + 4 w .. + 4, the 32 query rows of one MFMA column block (row n = token offset
 // n / 8, head n % 8).
 //
 // K/V tiles of 32 keys stream into a 3-stage LDS ring by direct global->LDS loads; one barrier
-// per tile. Software pipeline per tile i: S^T(i + 1) = K Q^T (32 MFMAs, each K operand feeding
-// both column blocks, Q^T resident as f16 pre-scaled by log2(e)/16), then O^T += V^T P^T(i) (32
-// MFMAs, V^T from ds_read_b64_tr_b16), then the online softmax of tile i + 1 -- independent of
-// the P V MFMAs, so it runs under them. Keys past a row's causal limit are masked only in the
-// (at most two) diagonal tiles of a wave; the gate and 1/l are applied at the store.
+// per tile. Per tile i (tile_step): the numerators of tile i, O^T += V^T P^T(i) (16 MFMAs, V^T
+// from ds_read_b64_tr_b16) and S^T(i + 1) = K Q^T (16 MFMAs, Q^T resident as f16 pre-scaled by
+// log2(e)/16), whose row max and rescale decision close the step. Keys past a row's causal limit
+// are masked only in the diagonal tiles of a wave; the gate and 1/l are applied at the store.
 template <int kBlock>
 __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsigned count) {
   using namespace prefill_detail;
   using attn::kDim;
   static_assert(kBlock == 256, "four waves per prefill workgroup");
   constexpr int kGroup = attn::kQHeads / attn::kKvHeads;
-  constexpr unsigned kWaveTokens = 4 * kNB;
+  constexpr unsigned kWaveTokens = kAttnQBlock / 4;
   __shared__ Shared sh;
   const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -454,17 +468,17 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
   const unsigned kb = lds0 + col * kRowBytes + 16 * hi + 32 * (col & 15u);
   // V^T transpose reads: rows 16 step + vrow (+ 8), chunk 4 b + vchunk, byte vbyte, i.e.
   // (512 vrow + vbyte + 16 (vchunk ^ 2 vrow)) ^ (64 b) [^ 256, + 4096 for rows + 8] + 8192 step.
-  unsigned vb[8][2];  // tile slot 0; + slot * 16 KiB for the others
+  // Bit 8 of the part before the XOR is clear, so blocks 4-7 are blocks 0-3 + 256 and the rows
+  // + 8 are + 4096 -+ 256: vb[c] (block c, rows 0-7, slot 0) is all a lane needs.
+  unsigned vb[4];
   {
     const unsigned g = lane >> 4, j = lane & 15u;
     const unsigned vrow = 4 * (g >> 1) + j / 4, vchunk = 2 * (g & 1u) + (j % 4) / 2;
     const unsigned vbyte = 8 * ((j % 4) & 1u);
     const unsigned base = vrow * kRowBytes + vbyte + 16 * (vchunk ^ (2 * vrow));
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      vb[b][0] = lds0 + kVBase + (base ^ (64u * b));
-      vb[b][1] = lds0 + kVBase + 4096 + (base ^ (64u * b) ^ 256u);
-    }
+    for (int c = 0; c < 4; ++c)
+      vb[c] = lds0 + kVBase + (base ^ (64u * c));
   }
 
   for (unsigned item = first + blockIdx.x; item < first + count; item += gridDim.x) {
@@ -496,50 +510,42 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     if (tiles > 1)
       copy(1);
 
-    // This wave's rows: block nb -> token tq[nb] = tw + 4 nb + col / 8, head kvh * 8 + col % 8.
+    // This wave's rows: token tq = tw + col / 8, head kvh * 8 + col % 8.
     const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
-    unsigned tq[kNB], lim[kNB];
-    bool q_valid[kNB];
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb) {
-      const unsigned raw = tw + 4 * nb + col / kGroup;
-      q_valid[nb] = raw < p.n;
-      tq[nb] = q_valid[nb] ? raw : p.n - 1;
-      lim[nb] = p.pos0 + tq[nb];  // last visible key
-    }
+    const unsigned raw_t = tw + col / kGroup;
+    const bool q_valid = raw_t < p.n;
+    const unsigned tq = q_valid ? raw_t : p.n - 1;
+    const unsigned lim = p.pos0 + tq;  // last visible key
     const bool wave_active = tw < p.n;
-    // Tiles this wave needs, and how many of them every row of the wave sees in full.
+    // Tiles this wave needs, and how many of them every row of the wave sees in full (always
+    // fewer: the last tile of a wave is a diagonal one).
     const unsigned wave_tiles =
         wave_active ? (p.pos0 + min(tw + kWaveTokens - 1, p.n - 1)) / kKeys + 1 : 0;
     const unsigned full_tiles = wave_active ? (p.pos0 + tw + 1) / kKeys : 0;
 
     Rows rw;
-    constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb) {
+    {
+      constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
       const float* src =
-          p.q + (std::size_t{tq[nb]} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
-      const float z = q_valid[nb] ? kScale : 0.0f;
+          p.q + (std::size_t{tq} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
+      const float z = q_valid ? kScale : 0.0f;
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
         const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
         const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
-        rw.q[nb][st] = half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
-                               static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
-                               static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
-                               static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
+        rw.q[st] = half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
+                           static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
+                           static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
+                           static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
       }
-      rw.m[nb] = -__builtin_inff();
-      rw.l[nb] = 0.0f;
+      rw.m = 0.0f;
+      rw.l = 0.0f;
+      rw.negm = float16_t{};
     }
-    float16_t oacc[kNB][8];
+    float16_t oacc[8];
 #pragma unroll
-    for (int nb = 0; nb < kNB; ++nb)
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        oacc[nb][b] = float16_t{};
-    half8_t pb[kNB][2];
-    float corr[kNB];
+    for (int b = 0; b < 8; ++b)
+      oacc[b] = float16_t{};
 
     // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (it is the
     // only copy in flight), every wave's by the barrier, which also says that all waves are done
@@ -555,48 +561,47 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
 
     cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
     __syncthreads();
-    // s: the scores of tile ti at the top of iteration ti (tile 0: computed here).
-    float16_t s[kNB];
-    if (wave_tiles > 0)
-      scores(s, rw, kb);
-    // One pass over the workgroup's tiles in three phases per wave, each a loop with a single
-    // body (the per-wave bounds differ; every wave still runs sync_copy once per tile, in order):
-    // the tiles its rows see in full, then its diagonal tiles (the last one has no successor),
-    // then the tiles it does not need.
-    float16_t s_next;
+    // cur: the decided scores of tile ti at the top of iteration ti (tile 0: here; O is still 0,
+    // so the first decision needs no rescale).
+    Pending cur;
+    if (wave_tiles > 0) {
+      const float16_t s0 = scores(rw, kb);
+      if (full_tiles > 0)
+        first_tile<false>(s0, cur, rw, lim, hi);
+      else
+        first_tile<true>(s0, cur, rw, lim, hi);
+    }
+    // One pass over the workgroup's tiles in phases per wave, each a loop with a single body
+    // (the per-wave bounds differ; every wave still runs sync_copy once per tile, in order):
+    // tiles whose successor the wave's rows see in full, tiles whose successor is diagonal, the
+    // last tile (no successor), then the tiles the wave does not need.
     unsigned ti = 0;
-    for (; ti < full_tiles; ++ti) {
+    for (; ti + 1 < full_tiles; ++ti) {
       sync_copy(ti);
-      tile_step<false, true>(s[0], s_next, rw, oacc[0], kb + ((ti + 1) % kStages) * kTileBytes, vb,
-                             (ti % kStages) * kTileBytes, 0, 0, hi);
-      s[0] = s_next;
+      tile_step<false, true>(cur, rw, oacc, kb, ((ti + 1) % kStages) * kTileBytes, vb,
+                             (ti % kStages) * kTileBytes, (ti + 1) * kKeys, lim, hi);
     }
     for (; ti + 1 < wave_tiles; ++ti) {
       sync_copy(ti);
-      tile_step<true, true>(s[0], s_next, rw, oacc[0], kb + ((ti + 1) % kStages) * kTileBytes, vb,
-                            (ti % kStages) * kTileBytes, ti * kKeys, lim[0], hi);
-      s[0] = s_next;
+      tile_step<true, true>(cur, rw, oacc, kb, ((ti + 1) % kStages) * kTileBytes, vb,
+                            (ti % kStages) * kTileBytes, (ti + 1) * kKeys, lim, hi);
     }
     if (ti < wave_tiles) {
       sync_copy(ti);
-      tile_step<true, false>(s[0], s_next, rw, oacc[0], 0, vb, (ti % kStages) * kTileBytes,
-                             ti * kKeys, lim[0], hi);
+      tile_step<false, false>(cur, rw, oacc, kb, 0, vb, (ti % kStages) * kTileBytes, 0, lim, hi);
       ++ti;
     }
     for (; ti < tiles; ++ti)
       sync_copy(ti);
     __syncthreads();  // the ring is reused by the next item
 
-    // Row totals: each column's keys per tile were split between the lane halves.
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb) {
-      const float l_tot = cdna4::sum_xor32(rw.l[nb]);
-      if (!q_valid[nb])
-        continue;
+    // Row total: each column's keys per tile were split between the lane halves.
+    const float l_tot = cdna4::sum_xor32(rw.l);
+    if (q_valid) {
       const unsigned head = kvh * kGroup + hq;
       const float inv_l = __builtin_amdgcn_rcpf(l_tot);
-      const float* gate = p.qg + std::size_t{tq[nb]} * p.qg_stride + head * 2 * kDim + kDim;
-      float* out = p.core + (std::size_t{tq[nb]} * attn::kQHeads + head) * kDim;
+      const float* gate = p.qg + std::size_t{tq} * p.qg_stride + head * 2 * kDim + kDim;
+      float* out = p.core + (std::size_t{tq} * attn::kQHeads + head) * kDim;
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
 #pragma unroll
@@ -604,10 +609,10 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
           const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
           const float4 gv = *reinterpret_cast<const float4*>(gate + d0);
           float4 o;
-          o.x = oacc[nb][b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.x));
-          o.y = oacc[nb][b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.y));
-          o.z = oacc[nb][b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.z));
-          o.w = oacc[nb][b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.w));
+          o.x = oacc[b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.x));
+          o.y = oacc[b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.y));
+          o.z = oacc[b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.z));
+          o.w = oacc[b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.w));
           *reinterpret_cast<float4*>(out + d0) = o;
         }
       }
