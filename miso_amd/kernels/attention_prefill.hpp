@@ -101,9 +101,11 @@ struct alignas(1024) Shared {
 __device__ inline unsigned swz(unsigned row, unsigned chunk) { return chunk ^ ((row & 15u) << 1); }
 
 // Global -> LDS copy of tile rows [8 w, 8 w + 8) of K and V (one 1 KiB instruction per row pair
-// and tensor). `off[i]` is this lane's byte offset of instruction i inside a tile (row 8 w + 2 i +
-// lane / 32, chunk swz(row, lane % 32)); kt / vt are the tile's first rows (wave-uniform), so the
-// copy needs no per-tile address arithmetic. M0 is saved and restored.
+// and tensor). Instruction i moves tile rows 8 w + 2 i + lane / 32, chunk swz(row, lane % 32), to
+// LDS bytes k_lds / v_lds + 1024 i + 16 lane; its offset field (1024 i) shifts the global and the
+// LDS address alike, so one M0 value serves the four instructions of a tensor and `off[i]` is the
+// lane's byte offset inside the tile minus 1024 i. kt / vt are the tile's first rows
+// (wave-uniform), so the copy needs no per-tile address arithmetic. M0 is saved and restored.
 __device__ __attribute__((always_inline)) inline void copy_tile(const void* kt, const void* vt,
                                                                 const unsigned (&off)[4],
                                                                 unsigned k_lds, unsigned v_lds) {
@@ -113,32 +115,20 @@ __device__ __attribute__((always_inline)) inline void copy_tile(const void* kt, 
       "s_mov_b32 m0, %7\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, %5\n\t"
-      "s_add_u32 m0, %7, 0x400\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, %5\n\t"
-      "s_add_u32 m0, %7, 0x800\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %3, %5\n\t"
-      "s_add_u32 m0, %7, 0xc00\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %4, %5\n\t"
+      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:3072\n\t"
       "s_mov_b32 m0, %8\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, %6\n\t"
-      "s_add_u32 m0, %8, 0x400\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, %6\n\t"
-      "s_add_u32 m0, %8, 0x800\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %3, %6\n\t"
-      "s_add_u32 m0, %8, 0xc00\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %4, %6\n\t"
+      "global_load_lds_dwordx4 %2, %6 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %6 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %6 offset:3072\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(kt), "s"(vt), "s"(k_lds),
         "s"(v_lds)
-      : "memory", "scc");
+      : "memory");
 }
 
 // The same copy for the tile that crosses the end of the keys: rows past last_row are clamped to
@@ -457,12 +447,13 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
   const unsigned blocks = (p.n + kAttnQBlock - 1) / kAttnQBlock;
   const unsigned lds0 = cdna4::lds_offset(sh.kv);
 
-  // Per-lane constant addresses. Copy: instruction i moves rows 8 w + 2 i + lane / 32.
+  // Per-lane constant addresses. Copy: instruction i moves rows 8 w + 2 i + lane / 32 (its
+  // offset field adds the 1024 i).
   unsigned copy_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const unsigned row = 8 * wave + 2 * i + (lane >> 5);
-    copy_off[i] = row * kRowBytes + swz(row, lane & 31u) * 16;
+    copy_off[i] = row * kRowBytes + swz(row, lane & 31u) * 16 - 1024 * i;
   }
   // S^T A operand (key row col, chunk 2 st + hi): (col 512 + 16 hi + 32 (col % 16)) ^ 32 st.
   const unsigned kb = lds0 + col * kRowBytes + 16 * hi + 32 * (col & 15u);
@@ -493,10 +484,18 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * kDim;
     const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * kDim;
     const unsigned tiles = (kv_end + kKeys - 1) / kKeys;
-    auto copy = [&](unsigned ti) __attribute__((always_inline)) {
-      const unsigned st = ti % kStages;
-      const unsigned k_lds = lds0 + st * kTileBytes + wave * 4096;
-      const unsigned v_lds = lds0 + kVBase + st * kTileBytes + wave * 4096;
+    // Ring slots as byte offsets, rotated once per tile: tile ti is in `cur`, ti + 1 in `next`,
+    // ti + 2 goes to `spare`.
+    unsigned slot_cur = 0, slot_next = kTileBytes, slot_spare = 2 * kTileBytes;
+    auto rotate = [&]() __attribute__((always_inline)) {
+      const unsigned t = slot_cur;
+      slot_cur = slot_next;
+      slot_next = slot_spare;
+      slot_spare = t;
+    };
+    auto copy = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
+      const unsigned k_lds = lds0 + slot + wave * 4096;
+      const unsigned v_lds = lds0 + kVBase + slot + wave * 4096;
       if ((ti + 1) * kKeys <= kv_end)
         copy_tile(K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
                   copy_off, k_lds, v_lds);
@@ -506,9 +505,9 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     };
 
     // Start streaming before anything else: tiles 0 and 1.
-    copy(0);
+    copy(0, slot_cur);
     if (tiles > 1)
-      copy(1);
+      copy(1, slot_next);
 
     // This wave's rows: token tq = tw + col / 8, head kvh * 8 + col % 8.
     const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
@@ -555,7 +554,7 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
         cdna4::wait_vmcnt<0>();
         __syncthreads();
         if (ti + 2 < tiles)
-          copy(ti + 2);
+          copy(ti + 2, slot_spare);
       }
     };
 
@@ -576,22 +575,22 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     // tiles whose successor the wave's rows see in full, tiles whose successor is diagonal, the
     // last tile (no successor), then the tiles the wave does not need.
     unsigned ti = 0;
-    for (; ti + 1 < full_tiles; ++ti) {
+    for (; ti + 1 < full_tiles; ++ti, rotate()) {
       sync_copy(ti);
-      tile_step<false, true>(cur, rw, oacc, kb, ((ti + 1) % kStages) * kTileBytes, vb,
-                             (ti % kStages) * kTileBytes, (ti + 1) * kKeys, lim, hi);
+      tile_step<false, true>(cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim,
+                             hi);
     }
-    for (; ti + 1 < wave_tiles; ++ti) {
+    for (; ti + 1 < wave_tiles; ++ti, rotate()) {
       sync_copy(ti);
-      tile_step<true, true>(cur, rw, oacc, kb, ((ti + 1) % kStages) * kTileBytes, vb,
-                            (ti % kStages) * kTileBytes, (ti + 1) * kKeys, lim, hi);
+      tile_step<true, true>(cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim, hi);
     }
     if (ti < wave_tiles) {
       sync_copy(ti);
-      tile_step<false, false>(cur, rw, oacc, kb, 0, vb, (ti % kStages) * kTileBytes, 0, lim, hi);
+      tile_step<false, false>(cur, rw, oacc, kb, 0, vb, slot_cur, 0, lim, hi);
       ++ti;
+      rotate();
     }
-    for (; ti < tiles; ++ti)
+    for (; ti < tiles; ++ti, rotate())
       sync_copy(ti);
     __syncthreads();  // the ring is reused by the next item
 
