@@ -95,39 +95,49 @@ struct alignas(1024) Shared {
   unsigned char kv[2 * kStages * kTileBytes];
 };
 
-// 16-byte chunk c of tile row r lives at chunk position c ^ 2 (r % 16) of that row: the 32 rows
-// read at one chunk (S^T operands) and the transpose reads spread over the banks. The XOR only
-// touches address bits 4-8, so operand addresses are lane bases XOR compile-time constants.
-__device__ inline unsigned swz(unsigned row, unsigned chunk) { return chunk ^ ((row & 15u) << 1); }
+// 16-byte chunk c of tile row r lives at chunk position c ^ s(r) of that row (64 banks of 4 bytes
+// = 16 chunk positions; an XOR, so its own inverse):
+//   K: s(r) = r % 16. The S^T operand read (ds_read_b128) of 16 consecutive lanes takes one chunk
+//      of 16 consecutive rows: 16 distinct positions mod 16, no bank conflict.
+//   V: s(r) = 4 (r % 4) + 16 ((r / 8) % 2). A transpose read (ds_read_b64_tr_b16) of 32 lanes
+//      takes chunks 4 b .. 4 b + 3 of 4 consecutive rows 4 k .. 4 k + 3: positions
+//      4 (b ^ (r % 4)) + chunk % 4, again 16 distinct. Rows r and r + 8 differ only in bit 4 of
+//      the position (byte 256), rows r and r + 16 not at all.
+__device__ inline unsigned swz_k(unsigned row, unsigned chunk) { return chunk ^ (row & 15u); }
+__device__ inline unsigned swz_v(unsigned row, unsigned chunk) {
+  return chunk ^ (4 * (row & 3u) + 16 * ((row >> 3) & 1u));
+}
 
 // Global -> LDS copy of tile rows [8 w, 8 w + 8) of K and V (one 1 KiB instruction per row pair
-// and tensor). Instruction i moves tile rows 8 w + 2 i + lane / 32, chunk swz(row, lane % 32), to
-// LDS bytes k_lds / v_lds + 1024 i + 16 lane; its offset field (1024 i) shifts the global and the
-// LDS address alike, so one M0 value serves the four instructions of a tensor and `off[i]` is the
-// lane's byte offset inside the tile minus 1024 i. kt / vt are the tile's first rows
-// (wave-uniform), so the copy needs no per-tile address arithmetic. M0 is saved and restored.
+// and tensor). Instruction i moves tile rows 8 w + 2 i + lane / 32, chunk swz_k / swz_v(row,
+// lane % 32), to LDS bytes k_lds / v_lds + 1024 i + 16 lane; its offset field (1024 i) shifts the
+// global and the LDS address alike, so one M0 value serves the four instructions of a tensor and
+// `koff[i]` / `voff[i]` are the lane's byte offsets inside the tile minus 1024 i. kt / vt are the
+// tile's first rows (wave-uniform), so the copy needs no per-tile address arithmetic. M0 is saved
+// and restored.
 __device__ __attribute__((always_inline)) inline void copy_tile(const void* kt, const void* vt,
-                                                                const unsigned (&off)[4],
+                                                                const unsigned (&koff)[4],
+                                                                const unsigned (&voff)[4],
                                                                 unsigned k_lds, unsigned v_lds) {
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %7\n\t"
+      "s_mov_b32 m0, %11\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %5\n\t"
-      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
-      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
-      "global_load_lds_dwordx4 %4, %5 offset:3072\n\t"
-      "s_mov_b32 m0, %8\n\t"
+      "global_load_lds_dwordx4 %1, %9\n\t"
+      "global_load_lds_dwordx4 %2, %9 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %9 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %9 offset:3072\n\t"
+      "s_mov_b32 m0, %12\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %6\n\t"
-      "global_load_lds_dwordx4 %2, %6 offset:1024\n\t"
-      "global_load_lds_dwordx4 %3, %6 offset:2048\n\t"
-      "global_load_lds_dwordx4 %4, %6 offset:3072\n\t"
+      "global_load_lds_dwordx4 %5, %10\n\t"
+      "global_load_lds_dwordx4 %6, %10 offset:1024\n\t"
+      "global_load_lds_dwordx4 %7, %10 offset:2048\n\t"
+      "global_load_lds_dwordx4 %8, %10 offset:3072\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(kt), "s"(vt), "s"(k_lds),
-        "s"(v_lds)
+      : "v"(koff[0]), "v"(koff[1]), "v"(koff[2]), "v"(koff[3]), "v"(voff[0]), "v"(voff[1]),
+        "v"(voff[2]), "v"(voff[3]), "s"(kt), "s"(vt), "s"(k_lds), "s"(v_lds)
       : "memory");
 }
 
@@ -142,9 +152,9 @@ __device__ __attribute__((always_inline)) inline void copy_tile_clamped(
     const unsigned row = 2 * m + (lane >> 5);
     unsigned r = k0 + row;
     r = r < last_row ? r : last_row;
-    const std::size_t at = std::size_t{r} * attn::kDim + swz(row, lane & 31u) * 8;
-    cdna4::lds_load16(K + at, k_lds + m * 1024);
-    cdna4::lds_load16(V + at, v_lds + m * 1024);
+    const std::size_t at = std::size_t{r} * attn::kDim;
+    cdna4::lds_load16(K + at + swz_k(row, lane & 31u) * 8, k_lds + m * 1024);
+    cdna4::lds_load16(V + at + swz_v(row, lane & 31u) * 8, v_lds + m * 1024);
   }
 }
 
@@ -449,24 +459,26 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
 
   // Per-lane constant addresses. Copy: instruction i moves rows 8 w + 2 i + lane / 32 (its
   // offset field adds the 1024 i).
-  unsigned copy_off[4];
+  unsigned copy_koff[4], copy_voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const unsigned row = 8 * wave + 2 * i + (lane >> 5);
-    copy_off[i] = row * kRowBytes + swz(row, lane & 31u) * 16 - 1024 * i;
+    copy_koff[i] = row * kRowBytes + swz_k(row, lane & 31u) * 16 - 1024 * i;
+    copy_voff[i] = row * kRowBytes + swz_v(row, lane & 31u) * 16 - 1024 * i;
   }
-  // S^T A operand (key row col, chunk 2 st + hi): (col 512 + 16 hi + 32 (col % 16)) ^ 32 st.
-  const unsigned kb = lds0 + col * kRowBytes + 16 * hi + 32 * (col & 15u);
+  // S^T A operand (key row col, chunk 2 st + hi at position (2 st + hi) ^ (col % 16)):
+  // (col 512 + 16 (hi ^ (col % 16))) ^ 32 st.
+  const unsigned kb = lds0 + col * kRowBytes + 16 * (hi ^ (col & 15u));
   // V^T transpose reads: rows 16 step + vrow (+ 8), chunk 4 b + vchunk, byte vbyte, i.e.
-  // (512 vrow + vbyte + 16 (vchunk ^ 2 vrow)) ^ (64 b) [^ 256, + 4096 for rows + 8] + 8192 step.
-  // Bit 8 of the part before the XOR is clear, so blocks 4-7 are blocks 0-3 + 256 and the rows
-  // + 8 are + 4096 -+ 256: vb[c] (block c, rows 0-7, slot 0) is all a lane needs.
+  // (512 vrow + vbyte + 16 vchunk + 64 (vrow % 4)) ^ (64 b) [^ 256, + 4096 for rows + 8]
+  // + 8192 step. Bit 8 of the part before the XOR is clear, so blocks 4-7 are blocks 0-3 + 256 and
+  // the rows + 8 are + 4096 -+ 256: vb[c] (block c, rows 0-7, slot 0) is all a lane needs.
   unsigned vb[4];
   {
     const unsigned g = lane >> 4, j = lane & 15u;
     const unsigned vrow = 4 * (g >> 1) + j / 4, vchunk = 2 * (g & 1u) + (j % 4) / 2;
     const unsigned vbyte = 8 * ((j % 4) & 1u);
-    const unsigned base = vrow * kRowBytes + vbyte + 16 * (vchunk ^ (2 * vrow));
+    const unsigned base = vrow * kRowBytes + vbyte + 16 * swz_v(vrow, vchunk);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       vb[c] = lds0 + kVBase + (base ^ (64u * c));
@@ -498,7 +510,7 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
       const unsigned v_lds = lds0 + kVBase + slot + wave * 4096;
       if ((ti + 1) * kKeys <= kv_end)
         copy_tile(K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
-                  copy_off, k_lds, v_lds);
+                  copy_koff, copy_voff, k_lds, v_lds);
       else
         copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, k_lds - wave * 4096,
                           v_lds - wave * 4096, wave, lane);
