@@ -593,20 +593,97 @@ namespace decode_detail {
 // dimensions of the same head. The result follows the reference's frozen FP32 order exactly:
 // M = max_c m_c; for c in split order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o);
 // core = o / L / (1 + __expf(-gate)). Split statistics are per head, hence the same for the whole
-// wave: lane c of each 64-split chunk loads m_c, l_c and forms w_c (a max is order-free and w_c
+// wave: lane c of a chunk of splits loads m_c, l_c and forms w_c (a max is order-free and w_c
 // depends only on m_c and M), the wave publishes (w_c, l_c) through LDS, and every lane then runs
-// the ordered FMA chain over the chunk with all 64 o_c loads already in flight. A chunk past the
-// last split is padded with w = 0 and a clamped, finite o: fma(0, x, acc) == acc exactly, so the
-// padding cannot change a bit. Every template variant and the batched path use this routine, so
-// all are bit-identical to one another and to a one-thread-per-dimension serial loop.
+// the ordered FMA chains. A chunk past the last split is padded with w = 0 and a clamped, finite
+// o: fma(0, x, acc) == acc exactly, so the padding cannot change a bit. Every template variant
+// and the batched path use this routine, so all are bit-identical to one another and to a
+// one-thread-per-dimension serial loop.
+//
+// For 16, 64 or 128 splits (the policy's counts at the bench's contexts) all loads of the merge go
+// out at once -- m and l of the lane's splits and the lane's o of every split -- so the merge costs
+// one memory latency plus the two FMA chains; the L chain runs while the o values are in flight.
 struct CombineLds {
-  float w[cdna4::kLanes], l[cdna4::kLanes];
+  float w[2 * cdna4::kLanes], l[2 * cdna4::kLanes];
 };
+
+// Exactly kN == n_splits splits, all in registers (kN = 16, 64 or 128).
+template <unsigned kN>
+__device__ __attribute__((always_inline)) inline float combine_wave_all(
+    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po,
+    unsigned n_splits, float gate, CombineLds& lds) {
+  constexpr unsigned kStride = kGroup;  // partial rows per split
+  constexpr std::size_t kOStride = std::size_t{kStride} * attn::kDim;
+  constexpr unsigned kLanesUsed = kN < cdna4::kLanes ? kN : cdna4::kLanes;
+  constexpr unsigned kPerLane = (kN + cdna4::kLanes - 1) / cdna4::kLanes;
+  const unsigned lane = cdna4::lane_id();
+  float mv[kPerLane], lv[kPerLane];
+#pragma unroll
+  for (unsigned j = 0; j < kPerLane; ++j) {
+    const unsigned c = j * cdna4::kLanes + lane;
+    const unsigned cc = c < n_splits ? c : 0;
+    mv[j] = pm[cc * kStride];
+    lv[j] = pl[cc * kStride];
+  }
+  // o of every split, 8 loads at a time; the scheduling barriers keep each group's address
+  // arithmetic next to its loads instead of 128 addresses live at once.
+  float ov[kN];
+#pragma unroll
+  for (unsigned g = 0; g < kN; g += 8) {
+#pragma unroll
+    for (unsigned r = g; r < g + 8; ++r)
+      ov[r] = po[r * kOStride];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float M = -__builtin_inff();
+#pragma unroll
+  for (unsigned j = 0; j < kPerLane; ++j)
+    if (j * cdna4::kLanes + lane < n_splits)
+      M = fmaxf(M, mv[j]);
+  M = cdna4::wave_allmax(M);
+#pragma unroll
+  for (unsigned j = 0; j < kPerLane; ++j) {
+    const unsigned c = j * cdna4::kLanes + lane;
+    if (lane < kLanesUsed) {
+      lds.w[c] = c < n_splits ? __expf(mv[j] - M) : 0.0f;
+      lds.l[c] = c < n_splits ? lv[j] : 0.0f;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  float L = 0.0f;
+#pragma unroll
+  for (unsigned r = 0; r < kN; r += 4) {
+    const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
+    const float4 l4 = *reinterpret_cast<const float4*>(&lds.l[r]);
+    L = __builtin_fmaf(w4.x, l4.x, L);
+    L = __builtin_fmaf(w4.y, l4.y, L);
+    L = __builtin_fmaf(w4.z, l4.z, L);
+    L = __builtin_fmaf(w4.w, l4.w, L);
+  }
+  float o = 0.0f;
+#pragma unroll
+  for (unsigned r = 0; r < kN; r += 4) {
+    const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
+    o = __builtin_fmaf(w4.x, ov[r], o);
+    o = __builtin_fmaf(w4.y, ov[r + 1], o);
+    o = __builtin_fmaf(w4.z, ov[r + 2], o);
+    o = __builtin_fmaf(w4.w, ov[r + 3], o);
+  }
+  __builtin_amdgcn_wave_barrier();  // a later merge by this wave overwrites the broadcast slots
+  return o / L / (1.0f + __expf(-gate));
+}
 
 __device__ __attribute__((always_inline)) inline float combine_wave(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po,
     unsigned n_splits, float gate, CombineLds& lds) {
-  constexpr unsigned kChunk = cdna4::kLanes, kStride = kGroup;  // partial rows per split
+  if (n_splits == 16)
+    return combine_wave_all<16>(pm, pl, po, n_splits, gate, lds);
+  if (n_splits == 64)
+    return combine_wave_all<64>(pm, pl, po, n_splits, gate, lds);
+  if (n_splits == 128)
+    return combine_wave_all<128>(pm, pl, po, n_splits, gate, lds);
+  // Other split counts: chunks of 64, the loads of one chunk in flight at a time.
+  constexpr unsigned kChunk = cdna4::kLanes, kStride = kGroup;
   constexpr std::size_t kOStride = std::size_t{kStride} * attn::kDim;
   const unsigned lane = cdna4::lane_id();
   float M = -__builtin_inff();
