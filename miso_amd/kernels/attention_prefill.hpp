@@ -613,17 +613,25 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
       const float inv_l = __builtin_amdgcn_rcpf(l_tot);
       const float* gate = p.qg + std::size_t{tq} * p.qg_stride + head * 2 * kDim + kDim;
       float* out = p.core + (std::size_t{tq} * attn::kQHeads + head) * kDim;
+      // Every gate load before the first store: the compiler cannot tell qg from core apart, so
+      // interleaved, each load would wait behind the previous store (32 memory round trips).
+      float4 gv[8][4];
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          gv[b][r4] = *reinterpret_cast<const float4*>(gate + 32 * b + 8 * r4 + 4 * hi);
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
-          const float4 gv = *reinterpret_cast<const float4*>(gate + d0);
+          const float4 g = gv[b][r4];
           float4 o;
-          o.x = oacc[b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.x));
-          o.y = oacc[b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.y));
-          o.z = oacc[b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.z));
-          o.w = oacc[b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-gv.w));
+          o.x = oacc[b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
+          o.y = oacc[b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.y));
+          o.z = oacc[b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.z));
+          o.w = oacc[b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.w));
           *reinterpret_cast<float4*>(out + d0) = o;
         }
       }
