@@ -16,6 +16,12 @@ Also reported:
                 the unmasked (query, key) pairs (1.6493e12 FLOP) vs the 2516.6 TFLOP/s f16 peak.
   cpu_baseline  the FP64 oracle (a C restatement of the reference's host scalar attention) on a
                 bounded sample of the same workload on this host's CPU, rank 0 only.
+  sustained     a pure f16 MFMA loop on random operands over all CUs (libmiso_probe.so): the
+                shader clock the MFMA units hold under such a load and the dense rate it reaches;
+                the prefill is also reported against the peak at that clock.
+  other_configs C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
+                TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table.
+  device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
 Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
 per-launch cost does not throttle a ~10 us step; the kernels are the same ones the C ABI
@@ -56,6 +62,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--no-other", action="store_true", help="skip the C1 / C3 / C5 lines")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 64 MiB device copies (counter calibration for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -102,6 +109,85 @@ def time_replays(torch, g, reps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
+
+def device_state():
+    """A few clock / temperature / power readings from rocm-smi (or amd-smi), best effort."""
+    import subprocess
+    for cmd in (["rocm-smi", "--showtemp", "--showpower", "--showclocks", "--json"],
+                ["amd-smi", "metric", "--json"]):
+        try:
+            res = subprocess.run(cmd, capture_output=True, text=True, timeout=30)
+        except (OSError, subprocess.SubprocessError) as e:
+            last = f"{cmd[0]}: {e}"
+            continue
+        if res.returncode != 0 or not res.stdout.strip():
+            last = f"{cmd[0]}: rc {res.returncode} {res.stderr.strip()[:120]}"
+            continue
+        try:
+            data = json.loads(res.stdout)
+        except ValueError:
+            return {"tool": cmd[0], "raw": res.stdout.strip()[:400]}
+        keep = {}
+
+        def walk(prefix, node):
+            if isinstance(node, dict):
+                for k, v in node.items():
+                    walk(f"{prefix}{k}/", v)
+            elif isinstance(node, list):
+                for i, v in enumerate(node[:4]):
+                    walk(f"{prefix}{i}/", v)
+            elif any(w in prefix.lower() for w in ("sclk", "mclk", "fclk", "temp", "power",
+                                                   "socket", "gfx_clk", "clk")):
+                if len(keep) < 24:
+                    keep[prefix.rstrip("/")] = node
+
+        walk("", data)
+        return {"tool": cmd[0], "readings": keep}
+    return {"error": last}
+
+
+def mfma_sustained(torch):
+    """Shader clock and dense f16 MFMA rate of a pure MFMA loop on random operands, one workgroup
+    per CU (libmiso_probe.so); median of 3 launches."""
+    import ctypes
+    path = ROOT / "miso_amd" / "lib" / "libmiso_probe.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.miso_probe_mfma_clock
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 2048
+    out = torch.empty(blocks * 256, device="cuda")
+    cyc = torch.zeros(blocks, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = fn(out.data_ptr(), cyc.data_ptr(), blocks, iters, stream)
+        if rc != 0:
+            raise RuntimeError(f"miso_probe_mfma_clock failed: {rc}")
+
+    launch()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        launch()
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append((e0.elapsed_time(e1), cyc.double().mean().item()))
+    runs.sort()
+    ms, cycles = runs[1]
+    ghz = cycles / (ms * 1e6)
+    flop = blocks * 4.0 * 16 * iters * 2 * 32 * 32 * 16
+    return {"clock_ghz": round(ghz, 3), "mfma_tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+            "peak_at_clock_tflops": round(blocks * 4096 * ghz * 1e9 / 1e12, 1),
+            "probe": f"{blocks} workgroups x 4 waves, 8 accumulator chains of "
+                     f"v_mfma_f32_32x32x16_f16 on random f16, {16 * iters} MFMAs per wave; "
+                     "cycles from s_memtime, time from HIP events"}
 
 
 def traffic_from_profiles(name):
@@ -187,8 +273,8 @@ def bench_prefill(torch, A, args):
     torch.cuda.synchronize()
     g = graph_of(torch, call, 1)
     time_replays(torch, g, 1)
-    ms, _ = time_replays(torch, g, args.prefill_steps)
-    t = ms / args.prefill_steps
+    runs = sorted(time_replays(torch, g, args.prefill_steps)[0] for _ in range(3))
+    t = runs[1] / args.prefill_steps  # median of 3 timed runs
     pairs = n * pos0 + n * (n + 1) // 2
     flop = 4.0 * H * D * pairs
     tflops = flop / (t * 1e-3) / 1e12
@@ -202,6 +288,75 @@ def bench_prefill(torch, A, args):
         }
     return {"t_ms": t, "flop": flop, "tflops": tflops, "pos0": pos0, "n": n,
             "max_ctx": max_ctx, "host": host}
+
+
+def bench_other(torch, A, args):
+    """C1, C3 and C5 of the survey's configuration table (synthetic N(0,1) inputs)."""
+    import numpy as np
+    out = {}
+    # C1: decode at ctx 512 (1 MiB of K/V: cache-resident, latency-bound).
+    L = 512
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(L)
+    q = torch.randn(H * D, generator=gen, device="cuda")
+    qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
+    k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+    v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+    sc = A.DecodeScratch(args.max_splits)
+    n1 = A.attn_n_splits(L, args.max_splits)
+    core = torch.empty(H * D, device="cuda")
+    g = graph_of(torch, lambda i: A.attn_decode(q, qg, k, v, core, sc, L, L, n1), 6)
+    time_replays(torch, g, 2)
+    ms = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1]
+    t1 = ms / 120
+    out["C1"] = {"workload": "decode, 1 sequence x 1 token, ctx 512 (warm cache)",
+                 "us_per_call": round(t1 * 1e3, 3), "n_splits": n1,
+                 "gbs": round(2048 * L / (t1 * 1e-3) / 1e9, 1)}
+    # C3: causal prefill, 2048 tokens, empty cache.
+    n3 = 2048
+    gen.manual_seed(n3)
+    q = torch.randn(n3 * H * D, generator=gen, device="cuda")
+    qg = torch.randn(n3 * H * 2 * D, generator=gen, device="cuda")
+    k = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
+    v = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
+    core = torch.empty(n3 * H * D, device="cuda")
+    g = graph_of(torch, lambda i: A.attn_prefill(q, qg, k, v, core, 0, n3, n3), 1)
+    time_replays(torch, g, 2)
+    ms = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1]
+    t3 = ms / 20
+    flop3 = 4.0 * H * D * (n3 * (n3 + 1) // 2)
+    out["C3"] = {"workload": "causal prefill, 2048 tokens, empty cache",
+                 "ms_per_call": round(t3, 4), "tflops": round(flop3 / (t3 * 1e-3) / 1e12, 1),
+                 "frac": round(flop3 / (t3 * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    del q, qg, k, v, core
+    # C5: ragged decode, 64 sequences, lengths uniform in [1024, 16384] (numpy, seed 64).
+    lens = np.random.default_rng(64).integers(1024, 16385, 64).astype(np.int64)
+    offs = np.zeros(64, dtype=np.int64)
+    offs[1:] = np.cumsum(lens * KV * D)[:-1]
+    total = int((lens * KV * D).sum())
+    gen.manual_seed(64)
+    qb = torch.randn(64 * H * D, generator=gen, device="cuda")
+    gate = torch.randn(64 * H * D, generator=gen, device="cuda")
+    kc = torch.randn(total, generator=gen, device="cuda").half()
+    vc = torch.randn(total, generator=gen, device="cuda").half()
+    d_offs = torch.from_numpy(offs).cuda()
+    d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
+    scr = A.RaggedScratch(64, int(lens.max()))
+    core = torch.empty(64 * H * D, device="cuda")
+    g = graph_of(torch, lambda i: A.attn_decode_ragged(qb, gate, kc, vc, d_offs, d_lens, core,
+                                                       scr), 1)
+    time_replays(torch, g, 2)
+    ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
+    t5 = ms / 10
+    bytes5 = 2048.0 * float(lens.sum())
+    out["C5"] = {"workload": "ragged decode, 64 sequences x 1 token, lengths U[1024,16384] "
+                             "(numpy seed 64), dense sigmoid gate",
+                 "sum_len": int(lens.sum()), "ms_per_call": round(t5, 4),
+                 "gbs": round(bytes5 / (t5 * 1e-3) / 1e9, 1),
+                 "frac": round(bytes5 / (t5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
+        f"C5 {out['C5']['gbs']} GB/s")
+    return out
 
 
 def cpu_decode_baseline(dec):
@@ -268,6 +423,9 @@ def main():
         copy_calibration(torch)
     dec = bench_decode(torch, A, args)
     pre = None if args.no_prefill else bench_prefill(torch, A, args)
+    sustained = None if args.no_prefill else mfma_sustained(torch)
+    other = None if args.no_other else bench_other(torch, A, args)
+    device = device_state()  # right after the GPU runs, while the clocks are still up
 
     value = dec["kv_bytes"] / (dec["t_step_ms"] * 1e-3) / 1e9
     split_gbs = dec["kv_bytes"] / (dec["t_split_ms"] * 1e-3) / 1e9
@@ -315,6 +473,14 @@ def main():
                          "unit": "TFLOP/s", "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                          "traffic": traffic_from_profiles("prefill_c4")},
         }
+        if sustained is not None:
+            sustained["frac_of_peak_at_clock"] = round(
+                pre["tflops"] / sustained["peak_at_clock_tflops"], 4)
+            sustained["frac_of_probe_rate"] = round(pre["tflops"] / sustained["mfma_tflops"], 4)
+            out["prefill"]["sustained"] = sustained
+    if other is not None:
+        out["other_configs"] = other
+    out["device"] = device
     if not args.no_cpu:
         log("cpu baseline (decode) ...")
         out["cpu_baseline"] = cpu_decode_baseline(dec)

@@ -19,6 +19,9 @@ ROOT = PKG.parent
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libmiso_attn.so"
 SOURCES = [PKG / "csrc" / "miso_attn_capi.hip"]
+# Measurement infrastructure for bench.py (sustained MFMA clock), not part of the C ABI.
+PROBE_LIB = LIB_DIR / "libmiso_probe.so"
+PROBE_SOURCES = [PKG / "csrc" / "mfma_clock_probe.hip"]
 HEADERS = sorted((PKG / "kernels").glob("*.hpp")) + [ROOT / "include" / "miso_attn.h"]
 
 # Packed FP32 VALU forms are disabled for all device code built here.
@@ -43,11 +46,17 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile libmiso_attn.so for gfx950 (always recompiles)."""
+    """Compile libmiso_attn.so (and the bench's libmiso_probe.so) for gfx950 (always recompiles)."""
+    _compile(SOURCES, LIB, verbose)
+    _compile(PROBE_SOURCES, PROBE_LIB, verbose)
+    return LIB
+
+
+def _compile(sources, lib: Path, verbose: bool) -> None:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), *HIP_FLAGS, "-I", str(PKG / "kernels"), "-I", str(ROOT / "include"),
-           *map(str, SOURCES), "-o", str(tmp)]
+           *map(str, sources), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -58,8 +67,7 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
 
 
 if __name__ == "__main__":
