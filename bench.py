@@ -19,6 +19,8 @@ Also reported:
   sustained     a pure f16 MFMA loop on random operands over all CUs (libmiso_probe.so): the
                 shader clock the MFMA units hold under such a load and the dense rate it reaches;
                 the prefill is also reported against the peak at that clock.
+  lds           the LDS time of one prefill tile's K and V operand reads on every CU with no
+                MFMA (libmiso_probe.so), against the 1024 cycles the tile's MFMAs take.
   other_configs C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table.
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
@@ -63,6 +65,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-other", action="store_true", help="skip the C1 / C3 / C5 lines")
+    ap.add_argument("--no-device", action="store_true",
+                    help="skip the rocm-smi / amd-smi readings (implied under a profiler)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 64 MiB device copies (counter calibration for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -188,6 +192,48 @@ def mfma_sustained(torch):
             "probe": f"{blocks} workgroups x 4 waves, 8 accumulator chains of "
                      f"v_mfma_f32_32x32x16_f16 on random f16, {16 * iters} MFMAs per wave; "
                      "cycles from s_memtime, time from HIP events"}
+
+
+def lds_tile_cost(torch):
+    """LDS time of one prefill tile's operand reads (libmiso_probe.so): 4 waves per CU each read a
+    32-key K tile (16 ds_read_b128) and V tile (32 ds_read_b64_tr_b16) in the prefill's layout,
+    no MFMA; shader cycles per tile (median of 3 launches per mode) against the 1024 cycles the
+    tile's MFMAs occupy each SIMD (4 waves x 32 MFMAs x 32 cycles over 4 SIMDs)."""
+    import ctypes
+    path = ROOT / "miso_amd" / "lib" / "libmiso_probe.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.miso_probe_lds_tile
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                   ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 2048
+    out = torch.empty(blocks * 256, device="cuda")
+    cyc = torch.zeros(blocks * 4, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    per_tile = {}
+    for mode in (0, 1, 2):
+        runs = []
+        for _ in range(4):  # the first is a warmup
+            rc = fn(out.data_ptr(), cyc.data_ptr(), blocks, mode, iters, stream)
+            if rc != 0:
+                raise RuntimeError(f"miso_probe_lds_tile failed: {rc}")
+            torch.cuda.synchronize()
+            runs.append(cyc.double().mean().item() / iters)
+        per_tile[mode] = sorted(runs[1:])[1]
+    mfma_cycles = 4 * 32 * 32 / 4
+    kv_bytes = 4 * 16384
+    return {"tile_read_cycles": round(per_tile[0], 1), "k_read_cycles": round(per_tile[1], 1),
+            "v_read_cycles": round(per_tile[2], 1),
+            "k_bytes_per_clk": round(kv_bytes / per_tile[1], 1),
+            "v_bytes_per_clk": round(kv_bytes / per_tile[2], 1),
+            "mfma_cycles_per_tile": mfma_cycles,
+            "mfma_ceiling_from_lds_reads": round(min(1.0, mfma_cycles / per_tile[0]), 4),
+            "probe": f"{blocks} workgroups x 4 waves; per wave and tile 16 KiB of K by "
+                     "ds_read_b128 and 16 KiB of V by ds_read_b64_tr_b16 at the prefill's "
+                     f"swizzled addresses, {iters} tiles; cycles from s_memtime"}
 
 
 def traffic_from_profiles(name):
@@ -424,8 +470,12 @@ def main():
     dec = bench_decode(torch, A, args)
     pre = None if args.no_prefill else bench_prefill(torch, A, args)
     sustained = None if args.no_prefill else mfma_sustained(torch)
+    lds = None if args.no_prefill else lds_tile_cost(torch)
     other = None if args.no_other else bench_other(torch, A, args)
-    device = device_state()  # right after the GPU runs, while the clocks are still up
+    # Right after the GPU runs, while the clocks are still up. Not under a profiler: its preloaded
+    # library would initialise the GPU in the smi tools too, before they exec their interpreter.
+    profiled = "rocprof" in os.environ.get("LD_PRELOAD", "")
+    device = None if (args.no_device or profiled) else device_state()
 
     value = dec["kv_bytes"] / (dec["t_step_ms"] * 1e-3) / 1e9
     split_gbs = dec["kv_bytes"] / (dec["t_split_ms"] * 1e-3) / 1e9
@@ -478,9 +528,12 @@ def main():
                 pre["tflops"] / sustained["peak_at_clock_tflops"], 4)
             sustained["frac_of_probe_rate"] = round(pre["tflops"] / sustained["mfma_tflops"], 4)
             out["prefill"]["sustained"] = sustained
+        if lds is not None:
+            out["prefill"]["lds"] = lds
     if other is not None:
         out["other_configs"] = other
-    out["device"] = device
+    if device is not None:
+        out["device"] = device
     if not args.no_cpu:
         log("cpu baseline (decode) ...")
         out["cpu_baseline"] = cpu_decode_baseline(dec)

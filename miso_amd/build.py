@@ -19,9 +19,10 @@ ROOT = PKG.parent
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libmiso_attn.so"
 SOURCES = [PKG / "csrc" / "miso_attn_capi.hip"]
-# Measurement infrastructure for bench.py (sustained MFMA clock), not part of the C ABI.
+# Measurement infrastructure for bench.py (sustained MFMA clock, LDS read cost of a prefill
+# tile), not part of the C ABI.
 PROBE_LIB = LIB_DIR / "libmiso_probe.so"
-PROBE_SOURCES = [PKG / "csrc" / "mfma_clock_probe.hip"]
+PROBE_SOURCES = [PKG / "csrc" / "mfma_clock_probe.hip", PKG / "csrc" / "lds_tile_probe.hip"]
 HEADERS = sorted((PKG / "kernels").glob("*.hpp")) + [ROOT / "include" / "miso_attn.h"]
 
 # Packed FP32 VALU forms are disabled for all device code built here.
