@@ -22,7 +22,8 @@ Also reported:
   lds           the LDS time of one prefill tile's K and V operand reads on every CU with no
                 MFMA (libmiso_probe.so), against the 1024 cycles the tile's MFMAs take.
   other_configs C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
-                TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table.
+                TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
+                and C5 over a pool of 16-row KV pages (the paged entry point).
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
 Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
@@ -400,8 +401,32 @@ def bench_other(torch, A, args):
                  "sum_len": int(lens.sum()), "ms_per_call": round(t5, 4),
                  "gbs": round(bytes5 / (t5 * 1e-3) / 1e9, 1),
                  "frac": round(bytes5 / (t5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kc, vc
+    # C5 over a KV page pool: the same lengths, 16-row pages in a random order.
+    page = 16
+    npg = (lens + page - 1) // page
+    max_pages = int(npg.max())
+    pool = int(npg.sum())
+    perm = np.random.default_rng(65).permutation(pool).astype(np.int32)
+    table = np.zeros((64, max_pages), np.int32)
+    starts = np.concatenate([[0], np.cumsum(npg)[:-1]])
+    for s_, (st, n_) in enumerate(zip(starts, npg)):
+        table[s_, :n_] = perm[st:st + n_]
+    kp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
+    vp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
+    d_table = torch.from_numpy(table).cuda()
+    g = graph_of(torch, lambda i: A.attn_decode_paged(qb, gate, kp, vp, d_table, page, d_lens,
+                                                      core, scr), 1)
+    time_replays(torch, g, 2)
+    ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
+    t5p = ms / 10
+    out["C5_paged"] = {"workload": "C5 with the K/V in a pool of 16-row pages in a random order "
+                                   "(page table per sequence)",
+                       "page_size": page, "pages": pool, "ms_per_call": round(t5p, 4),
+                       "gbs": round(bytes5 / (t5p * 1e-3) / 1e9, 1),
+                       "frac": round(bytes5 / (t5p * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
-        f"C5 {out['C5']['gbs']} GB/s")
+        f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s")
     return out
 
 

@@ -128,6 +128,22 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
                             const uint32_t* lens, uint32_t batch, uint32_t max_len, float* core,
                             float* part_m, float* part_l, float* part_o, void* stream);
 
+/* Paged batched decode (no reference counterpart; the reference's KV cache is one contiguous
+ * [2][max_ctx][256] f16 buffer per layer, src/engine/attention.hpp:35-41). Same semantics, splits
+ * and partial scratch as miso_attn_decode_ragged (and bit-identical outputs on the same keys), with
+ * the keys in a pool of pages instead of contiguous per-sequence buffers: page g holds
+ * [2 KV heads][page_size][256] f16 at g * 2 * page_size * 256 halves of k_pages / v_pages, and
+ * sequence s's positions [j * page_size, (j + 1) * page_size) are in page
+ * page_table[s * max_pages + j]. page_table and lens are DEVICE arrays (not validated on the host:
+ * every page id of a sequence's first ceil(lens[s] / page_size) entries must lie in the pool).
+ * Rejects batch == 0, max_len == 0, max_pages == 0, page_size not a power of two in [8, 65536],
+ * and max_pages * page_size < max_len. */
+int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_pages,
+                           const uint16_t* v_pages, const int32_t* page_table, uint32_t max_pages,
+                           uint32_t page_size, const uint32_t* lens, uint32_t batch,
+                           uint32_t max_len, float* core, float* part_m, float* part_l,
+                           float* part_o, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -208,3 +208,27 @@ def attn_decode_ragged(q, gate, k_cache, v_cache, kv_offsets, lens, core,
         _ptr(q), _ptr(gate), _ptr(k_cache), _ptr(v_cache), _ptr(kv_offsets), _ptr(lens), batch,
         max_len, _ptr(core), _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o),
         _stream(stream)))
+
+
+def attn_decode_paged(q, gate, k_pages, v_pages, page_table, page_size: int, lens, core,
+                      scratch: RaggedScratch, stream=None) -> None:
+    """Batched decode over a KV page pool: page g holds [2][page_size][256] f16 at
+    g * 2 * page_size * 256 of k_pages / v_pages; sequence s's positions
+    [j * page_size, (j + 1) * page_size) are in page page_table[s, j] (device int32
+    [batch][max_pages]). Same results as attn_decode_ragged on the same keys."""
+    batch, max_len = scratch.batch, scratch.max_len
+    f32 = torch.float32
+    _need(q, "q", f32, batch * Q_HEADS * DIM)
+    _need(gate, "gate", f32, batch * Q_HEADS * DIM)
+    _need(core, "core", f32, batch * Q_HEADS * DIM)
+    _need(lens, "lens", torch.int32, batch)
+    if page_table.dim() != 2 or page_table.shape[0] != batch:
+        raise ValueError("page_table must be [batch][max_pages]")
+    _need(page_table, "page_table", torch.int32, batch * page_table.shape[1])
+    for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
+        if not t.is_cuda or t.dtype not in (torch.float16, torch.int16):
+            raise ValueError(f"{name} must be a float16 device tensor")
+    _lib.check(_lib.load().miso_attn_decode_paged(
+        _ptr(q), _ptr(gate), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        int(page_table.shape[1]), page_size, _ptr(lens), batch, max_len, _ptr(core),
+        _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o), _stream(stream)))

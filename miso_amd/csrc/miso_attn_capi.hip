@@ -231,4 +231,44 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
   return launched("miso_attn_decode_ragged(combine)");
 }
 
+int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_pages,
+                           const uint16_t* v_pages, const int32_t* page_table, uint32_t max_pages,
+                           uint32_t page_size, const uint32_t* lens, uint32_t batch,
+                           uint32_t max_len, float* core, float* part_m, float* part_l,
+                           float* part_o, void* stream) {
+  if (any_bad(q, gate, k_pages, v_pages, core, part_o) || bad_scalars(part_m) ||
+      bad_scalars(part_l) || page_table == nullptr || lens == nullptr)
+    return fail("miso_attn_decode_paged", kBadPtr);
+  if (batch == 0)
+    return fail("miso_attn_decode_paged", "batch must be >= 1");
+  if (max_len == 0)
+    return fail("miso_attn_decode_paged", "max_len must be >= 1");
+  if (max_pages == 0)
+    return fail("miso_attn_decode_paged", "max_pages must be >= 1");
+  if (page_size < 8 || page_size > 65536 || (page_size & (page_size - 1)) != 0)
+    return fail("miso_attn_decode_paged", "page_size must be a power of two in [8, 65536]");
+  if (uint64_t{max_pages} * page_size < max_len)
+    return fail("miso_attn_decode_paged", "max_pages * page_size < max_len");
+  const unsigned s_max = k::attn_ragged_splits(max_len);
+  const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
+  if (items > 0x7FFFFFFFull)
+    return fail("miso_attn_decode_paged", "batch x splits too large for one grid");
+  const k::AttnPagedParams p{q,      as_half(k_pages), as_half(v_pages), page_table,
+                             lens,   part_m,           part_l,           part_o,
+                             batch,  s_max,            max_pages,
+                             static_cast<unsigned>(__builtin_ctz(page_size))};
+  k::attn_paged_split_kernel<256>
+      <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
+  int rc = launched("miso_attn_decode_paged(split)");
+  if (rc != 0)
+    return rc;
+  // The merge reads only the partials, lens, gate and core of the ragged parameters.
+  const k::AttnRaggedParams r{q,      gate,   nullptr, nullptr, nullptr,
+                              lens,   core,   part_m,  part_l,  part_o,
+                              batch,  s_max};
+  const unsigned tiles = batch * k::attn::kQHeads * (k::attn::kDim / 64);
+  k::attn_ragged_combine_kernel<<<tiles, 64, 0, as_stream(stream)>>>(r);
+  return launched("miso_attn_decode_paged(combine)");
+}
+
 }  // extern "C"

@@ -15,6 +15,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "cdna4_wave.hpp"
 
@@ -366,17 +367,34 @@ __device__ __attribute__((always_inline)) inline void process_unit(
   }
 }
 
+// Where the K/V rows of one sequence and KV head lie. LinearRows: row r at K / V + 256 r.
+// PagedRows: rows in pages of 2^log2_page rows; page j of the sequence is page table[j] of the
+// pool, which holds [2 KV heads][2^log2_page][256] per page (head_off selects the KV head). An
+// 8-row unit never crosses a page (units start at multiples of 8, pages hold >= 8 rows).
+struct LinearRows {
+  const attn::half_t* K;
+  const attn::half_t* V;
+};
+struct PagedRows {
+  const attn::half_t* k_pages;
+  const attn::half_t* v_pages;
+  const int32_t* table;     // this sequence's page table
+  unsigned log2_page;       // rows per page = 1 << log2_page, >= 3
+  std::size_t page_halves;  // 2 << log2_page rows of 256 halves: one page of both KV heads
+  std::size_t head_off;     // kvh << log2_page rows of 256 halves
+};
+
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh, written at `base` (=
 // kvh * n_splits + split) in the reference's partial layout. Wave w streams units w, w + W, ...
 // of the span through its R-unit LDS ring (R - 1 units in flight while one is processed); the
 // waves merge through LDS at the end. Every vector-memory load of the kernel is a direct LDS
-// load with an explicit wait. `more` says whether the workgroup runs another item afterwards
-// (its LDS is then reused).
-template <class Shared>
-__device__ __attribute__((always_inline)) inline void split_partial(
-    const float* __restrict__ q, const attn::half_t* K, const attn::half_t* V, unsigned len,
-    AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base,
-    Shared& sh, bool more) {
+// load with an explicit wait, except the paged layout's page-table slice, which is waited for
+// before the first unit is issued. `more` says whether the workgroup runs another item
+// afterwards (its LDS is then reused).
+template <class Shared, class Rows>
+__device__ __attribute__((always_inline)) inline void split_partial_rows(
+    const float* __restrict__ q, const Rows& rows, unsigned len, AttnSpan span, unsigned kvh,
+    float* part_m, float* part_l, float* part_o, std::size_t base, Shared& sh, bool more) {
   constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
   static_assert(kR >= 2 && kR <= 4 && kGroup % kW == 0, "ring depth / wave count");
   const unsigned t = threadIdx.x, lane = t & 63u, c = lane & 31u;
@@ -386,16 +404,44 @@ __device__ __attribute__((always_inline)) inline void split_partial(
   const unsigned first = span.begin + wave * kAttnDecodeUnit;
   const unsigned n_units = first < span.end ? (span.end - first + kStride - 1) / kStride : 0;
   const unsigned ring0 = cdna4::lds_offset(sh.ring[wave][0]);
-  // This lane's address of row pair 0 of unit 0; unit k is kStride rows further.
-  const std::size_t lane_at = std::size_t{first + (lane >> 5)} * attn::kDim + c * 8;
+  std::size_t lane_at = 0;
+  int tab = 0;
+  unsigned page0 = 0;
+  if constexpr (std::is_same_v<Rows, LinearRows>) {
+    // This lane's address of row pair 0 of unit 0; unit k is kStride rows further.
+    lane_at = std::size_t{first + (lane >> 5)} * attn::kDim + c * 8;
+  } else {
+    // The span's pages, one per lane (a span of at most 64 pages; further pages are read from
+    // the table directly).
+    page0 = span.begin >> rows.log2_page;
+    const unsigned npages =
+        span.end > span.begin ? ((span.end - 1) >> rows.log2_page) - page0 + 1 : 0;
+    tab = lane < npages ? rows.table[page0 + lane] : 0;
+    lane_at = std::size_t{lane >> 5} * attn::kDim + c * 8;
+  }
   constexpr std::size_t kUnitStep = std::size_t{kStride} * attn::kDim;
   auto issue = [&](unsigned k) {
     const unsigned u0 = first + k * kStride;
     const unsigned slot = ring0 + (k % kR) * kUnitBytes;
-    if (u0 + kAttnDecodeUnit <= len)  // wave-uniform
-      issue_unit(K + lane_at + k * kUnitStep, V + lane_at + k * kUnitStep, slot);
-    else
-      issue_unit_clamped(K, V, u0, last_row, slot, lane);
+    if constexpr (std::is_same_v<Rows, LinearRows>) {
+      if (u0 + kAttnDecodeUnit <= len)  // wave-uniform
+        issue_unit(rows.K + lane_at + k * kUnitStep, rows.V + lane_at + k * kUnitStep, slot);
+      else
+        issue_unit_clamped(rows.K, rows.V, u0, last_row, slot, lane);
+    } else {
+      const unsigned j = (u0 >> rows.log2_page) - page0;  // wave-uniform
+      const int page = j < 64 ? __builtin_amdgcn_readlane(tab, j) : rows.table[page0 + j];
+      const unsigned in_page = u0 & ((1u << rows.log2_page) - 1u);
+      const std::size_t pg = std::size_t(static_cast<unsigned>(page)) * rows.page_halves +
+                             rows.head_off;
+      if (u0 + kAttnDecodeUnit <= len) {
+        const std::size_t at = pg + std::size_t{in_page} * attn::kDim + lane_at;
+        issue_unit(rows.k_pages + at, rows.v_pages + at, slot);
+      } else {  // the unit holds the last row: same page
+        issue_unit_clamped(rows.k_pages + pg, rows.v_pages + pg, in_page,
+                           in_page + (last_row - u0), slot, lane);
+      }
+    }
   };
 
   // This wave's query heads of the KV head (1 KiB each), then the first kR - 1 units.
@@ -543,6 +589,14 @@ __device__ __attribute__((always_inline)) inline void split_partial(
   }
   if (more)
     __syncthreads();  // LDS is reused by the next item
+}
+
+template <class Shared>
+__device__ __attribute__((always_inline)) inline void split_partial(
+    const float* __restrict__ q, const attn::half_t* K, const attn::half_t* V, unsigned len,
+    AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base,
+    Shared& sh, bool more) {
+  split_partial_rows(q, LinearRows{K, V}, len, span, kvh, part_m, part_l, part_o, base, sh, more);
 }
 
 }  // namespace decode_detail
@@ -827,6 +881,51 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
   p.core[out] = decode_detail::combine_wave(p.part_m + i0, p.part_l + i0,
                                            p.part_o + i0 * attn::kDim + d, n_splits, p.gate[out],
                                            lds);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Paged batched decode (no reference counterpart): the ragged decode over a pool of KV pages.
+// Page id g holds [2 KV heads][page][256] f16 at g * 2 * page * 256 halves of k_pages / v_pages;
+// sequence s's positions [j page, (j + 1) page) are in page page_table[s * max_pages + j]. Same
+// splits, arithmetic and partial layout as the ragged path, so the outputs are bit-identical to
+// it on the same keys; attn_ragged_combine_kernel merges the partials.
+// ------------------------------------------------------------------------------------------------
+
+struct AttnPagedParams {
+  const float* q;                // [batch][16][256] (unscaled)
+  const attn::half_t* k_pages;   // [pages][2][page][256]
+  const attn::half_t* v_pages;
+  const int32_t* page_table;     // [batch][max_pages] (device)
+  const uint32_t* lens;          // [batch] (device)
+  float* part_m;                 // [batch][2][s_max][8]
+  float* part_l;
+  float* part_o;                 // [batch][2][s_max][8][256]
+  unsigned batch, s_max, max_pages, log2_page;
+};
+
+// One workgroup per (sequence, KV head, split slot), as attn_ragged_split_kernel.
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  __shared__ decode_detail::SplitShared sh;
+  const unsigned item = blockIdx.x;
+  const unsigned split = item % p.s_max, kvh = (item / p.s_max) % attn::kKvHeads;
+  const unsigned seq = item / (p.s_max * attn::kKvHeads);
+  if (seq >= p.batch)
+    return;
+  const unsigned len = p.lens[seq];
+  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
+  if (split >= n_splits)
+    return;
+  const decode_detail::PagedRows rows{
+      p.k_pages, p.v_pages, p.page_table + std::size_t{seq} * p.max_pages, p.log2_page,
+      std::size_t{2} * attn::kDim << p.log2_page,
+      std::size_t{kvh} * attn::kDim << p.log2_page};
+  decode_detail::split_partial_rows(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, rows,
+                                    len, attn_split_span(len, n_splits, split), kvh, p.part_m,
+                                    p.part_l, p.part_o,
+                                    (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
+                                    sh, false);
 }
 
 }  // namespace miso::kernels

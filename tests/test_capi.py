@@ -71,6 +71,13 @@ def test_host_validation_rejects_bad_arguments(lib):
              "proj_stride")
     rejected(lib.miso_attn_decode_ragged(P, P, P, P, P, P, 0, 10, P, P, P, P, N), lib, "batch")
     rejected(lib.miso_attn_decode_ragged(P, P, P, P, P, P, 3, 0, P, P, P, P, N), lib, "max_len")
+    paged = lib.miso_attn_decode_paged
+    rejected(paged(P, P, P, P, P, 4, 16, P, 0, 10, P, P, P, P, N), lib, "batch")
+    rejected(paged(P, P, P, P, P, 4, 16, P, 3, 0, P, P, P, P, N), lib, "max_len")
+    rejected(paged(P, P, P, P, P, 0, 16, P, 3, 10, P, P, P, P, N), lib, "max_pages")
+    for bad_page in (0, 4, 12, 131072):
+        rejected(paged(P, P, P, P, P, 4, bad_page, P, 3, 10, P, P, P, P, N), lib, "page_size")
+    rejected(paged(P, P, P, P, P, 4, 16, P, 3, 65, P, P, P, P, N), lib, "max_pages * page_size")
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")
@@ -93,6 +100,11 @@ def test_host_validation_rejects_null_and_misaligned_pointers(lib):
     rejected(lib.miso_attn_split(P, P, P, N, P, P, 5, 10, 1, N), lib, bad)
     rejected(lib.miso_attn_combine(P, P + 2, P, P, P, 4, N), lib, bad)
     rejected(lib.miso_attn_decode_ragged(P, P, P, P, N, P, 3, 10, P, P, P, P, N), lib, bad)
+    for q in (N, P + 4):
+        rejected(lib.miso_attn_decode_paged(P, P, q, P, P, 4, 16, P, 3, 10, P, P, P, P, N), lib,
+                 bad)
+    rejected(lib.miso_attn_decode_paged(P, P, P, P, N, 4, 16, P, 3, 10, P, P, P, P, N), lib, bad)
+    rejected(lib.miso_attn_decode_paged(P, P, P, P, P, 4, 16, N, 3, 10, P, P, P, P, N), lib, bad)
 
 
 def test_python_layer_raises_runtime_error_with_message():
