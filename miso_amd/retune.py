@@ -16,7 +16,9 @@ signature:
   chunk        the attention work of ingesting a P-token prompt (prep_batch + prefill per chunk)
                for several chunk sizes;
   min_tokens   n per-token decode calls (prep + split + combine at lengths L + 1 .. L + n)
-               against one prep_batch + prefill of n tokens, at context L.
+               against one prep_batch + prefill of n tokens, at context L;
+  prefill_map  the prefill kernel alone (TFLOP/s over the unmasked pairs) for chunk sizes n
+               after prefixes pos0: how much of the GPU a chunk of each size fills.
 
 Only the attention kernels are timed: the engine's projections, MoE and DeltaNet layers shift the
 real crossover and chunk optimum, so these are the attention path's side of each trade.
@@ -188,6 +190,29 @@ def sweep_min_tokens(torch, A, ctx, ns, max_splits=128):
     return {"ctx": ctx, "rows": out, "smallest_n_where_prefill_wins": first}
 
 
+def sweep_prefill_map(torch, A, prefixes, sizes):
+    out = []
+    gen = torch.Generator(device="cuda")
+    for pos0 in prefixes:
+        for n in sizes:
+            max_ctx = pos0 + n
+            gen.manual_seed(max_ctx + 7)
+            q = torch.randn(n * H * D, generator=gen, device="cuda")
+            qg = torch.randn(n * H * 2 * D, generator=gen, device="cuda")
+            k = torch.randn(KV * max_ctx * D, generator=gen, device="cuda").half()
+            v = torch.randn(KV * max_ctx * D, generator=gen, device="cuda").half()
+            core = torch.empty(n * H * D, device="cuda")
+            g = _graph(torch, lambda _i: A.attn_prefill(q, qg, k, v, core, pos0, n, max_ctx), 1)
+            t = _time(torch, g, 3)
+            pairs = n * pos0 + n * (n + 1) // 2
+            out.append({"pos0": pos0, "n": n, "workgroups": A.attn_prefill_items(n),
+                        "ms": round(t, 4), "tflops": round(4.0 * H * D * pairs / (t * 1e-3) / 1e12, 1)})
+            print(f"[retune] prefill pos0 {pos0} n {n}: {t:.3f} ms, {out[-1]['tflops']} TFLOP/s",
+                  file=sys.stderr, flush=True)
+            del q, qg, k, v, core, g
+    return out
+
+
 def run(quick=False):
     import torch
     from miso_amd import attention as A
@@ -200,11 +225,14 @@ def run(quick=False):
         contexts = [512, 4096, 32768, 131072]
         prompt, chunks = 8192, [256, 512, 1024, 2048, 4096, 8192]
         ns, ctx = [1, 2, 3, 4, 6, 8, 12, 16], 4096
+    prefixes, sizes = ([0, 4096], [256, 1024]) if quick else \
+        ([0, 8192, 32768], [512, 1024, 2048, 4096, 8192, 16384])
     return {
         "engine_constants": {"kMaxSplits": 60, "kMaxChunk": 512, "kPrefillMinTokens": 8},
         "max_splits": sweep_max_splits(torch, A, contexts),
         "chunk": {"prompt": prompt, "rows": sweep_chunk(torch, A, prompt, chunks)},
         "min_tokens": sweep_min_tokens(torch, A, ctx, ns),
+        "prefill_map": sweep_prefill_map(torch, A, prefixes, sizes),
         "note": "attention kernels only (prep, split, combine, prep_batch, prefill), HIP-event "
                 "time of graph replays, median of 3; synthetic N(0,1) inputs",
     }

@@ -20,3 +20,6 @@ def test_retune_quick_runs():
     assert [r["chunk"] for r in out["chunk"]["rows"]] == [512, 2048]
     assert all(r["ms"] > 0 for r in out["chunk"]["rows"])
     assert [r["n"] for r in out["min_tokens"]["rows"]] == [1, 2, 4]
+    assert [(r["pos0"], r["n"]) for r in out["prefill_map"]] == [(0, 256), (0, 1024),
+                                                                 (4096, 256), (4096, 1024)]
+    assert all(r["tflops"] > 0 for r in out["prefill_map"])
