@@ -144,6 +144,33 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
                            uint32_t max_len, float* core, float* part_m, float* part_l,
                            float* part_o, void* stream);
 
+/* fp8 KV cache (no reference counterpart; the reference's cache is f16 [2][max_ctx][256],
+ * src/engine/attention.hpp:35-41, kernels/attention_decode.hpp:26-27). Row (KV head, position)
+ * is 256 OCP e4m3 codes in k8 / v8 [2][max_ctx][256] (uint8) plus one f32 power-of-two scale in
+ * k_scale / v_scale [2][max_ctx]: value = scale * e4m3(code), scale = 2^(floor(log2 max|x|) - 7)
+ * (rows whose max is below 2^-100 use 2^-107), codes rounded to nearest even, never saturated.
+ * Inputs must be finite. k8 / v8 need 16-byte alignment, the scale arrays 4-byte alignment.
+ *
+ * miso_attn_kv_encode_fp8: rows [pos0, pos0 + n) of both KV heads of an f16 cache -> e4m3 rows
+ * (n == 0 is a no-op). Rejects pos0 + n > max_ctx. */
+int miso_attn_kv_encode_fp8(const uint16_t* k_cache, const uint16_t* v_cache, uint8_t* k8,
+                            uint8_t* v8, float* k_scale, float* v_scale, uint32_t pos0, uint32_t n,
+                            uint32_t max_ctx, void* stream);
+
+/* miso_attn_prep with the token's K / V appended as e4m3 rows at position pos (q output and
+ * arithmetic as miso_attn_prep). Rejects pos >= max_ctx. */
+int miso_attn_prep_fp8(const float* qg, const float* k, const float* v, const float* q_norm,
+                       const float* k_norm, const float* inv_freq, uint8_t* k8, uint8_t* v8,
+                       float* k_scale, float* v_scale, float* q, uint32_t pos, uint32_t max_ctx,
+                       float eps, void* stream);
+
+/* miso_attn_decode over e4m3 rows: split-K partials (same spans and partial layout as
+ * miso_attn_split) then miso_attn_combine. Same scratch sizes and rejections as miso_attn_decode. */
+int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
+                         const float* k_scale, const float* v_scale, float* core, float* part_m,
+                         float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
+                         uint32_t n_splits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

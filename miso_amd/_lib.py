@@ -32,6 +32,11 @@ SIGNATURES = {
     "miso_attn_decode_ragged": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, P, P, P, P, P]),
     "miso_attn_decode_paged": (c_int, [P, P, P, P, P, c_uint32, c_uint32, P, c_uint32, c_uint32,
                                        P, P, P, P, P]),
+    "miso_attn_kv_encode_fp8": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
+    "miso_attn_prep_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_float,
+                                   P]),
+    "miso_attn_decode_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
+                                     P]),
 }
 
 _lib = None

@@ -232,3 +232,77 @@ def attn_decode_paged(q, gate, k_pages, v_pages, page_table, page_size: int, len
         _ptr(q), _ptr(gate), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
         int(page_table.shape[1]), page_size, _ptr(lens), batch, max_len, _ptr(core),
         _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o), _stream(stream)))
+
+
+# ------------------------------------------------------------------------------------------------
+# fp8 KV cache: e4m3 rows (uint8 [2][max_ctx][256]) with one power-of-two f32 scale per row
+# ([2][max_ctx]); value = scale * e4m3(code). Format contract: include/miso_attn.h.
+# ------------------------------------------------------------------------------------------------
+
+class Fp8Cache:
+    """Device buffers of an e4m3 KV cache for max_ctx positions of both KV heads."""
+
+    def __init__(self, max_ctx: int, device="cuda"):
+        self.max_ctx = max_ctx
+        self.k8 = torch.zeros(KV_HEADS * max_ctx * DIM, dtype=torch.uint8, device=device)
+        self.v8 = torch.zeros(KV_HEADS * max_ctx * DIM, dtype=torch.uint8, device=device)
+        self.k_scale = torch.zeros(KV_HEADS * max_ctx, dtype=torch.float32, device=device)
+        self.v_scale = torch.zeros(KV_HEADS * max_ctx, dtype=torch.float32, device=device)
+
+    def buffers(self):
+        return self.k8, self.v8, self.k_scale, self.v_scale
+
+
+def _need_fp8(cache: Fp8Cache) -> None:
+    n = KV_HEADS * cache.max_ctx
+    _need(cache.k8, "k8", torch.uint8, n * DIM)
+    _need(cache.v8, "v8", torch.uint8, n * DIM)
+    _need(cache.k_scale, "k_scale", torch.float32, n)
+    _need(cache.v_scale, "v_scale", torch.float32, n)
+
+
+def attn_kv_encode_fp8(k_cache, v_cache, cache: Fp8Cache, pos0: int, n: int,
+                       stream=None) -> None:
+    """Encode rows [pos0, pos0 + n) of both KV heads of an f16 cache into `cache`."""
+    m = cache.max_ctx
+    _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * m * DIM)
+    _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * m * DIM)
+    _need_fp8(cache)
+    _lib.check(_lib.load().miso_attn_kv_encode_fp8(
+        _ptr(k_cache), _ptr(v_cache), *(_ptr(b) for b in cache.buffers()), pos0, n, m,
+        _stream(stream)))
+
+
+def attn_prep_fp8(qg, k, v, q_norm, k_norm, inv_freq, cache: Fp8Cache, q, pos: int,
+                  eps: float = 1e-6, stream=None) -> None:
+    """attn_prep appending the token's K / V to `cache` as e4m3 rows at position pos."""
+    f32 = torch.float32
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(k, "k", f32, KV_HEADS * DIM)
+    _need(v, "v", f32, KV_HEADS * DIM)
+    for name, t, n in (("q_norm", q_norm, DIM), ("k_norm", k_norm, DIM),
+                       ("inv_freq", inv_freq, 32), ("q", q, Q_HEADS * DIM)):
+        _need(t, name, f32, n)
+    _need_fp8(cache)
+    _lib.check(_lib.load().miso_attn_prep_fp8(
+        _ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(inv_freq),
+        *(_ptr(b) for b in cache.buffers()), _ptr(q), pos, cache.max_ctx, eps, _stream(stream)))
+
+
+def attn_decode_fp8(q, qg, cache: Fp8Cache, core, scratch: DecodeScratch, length: int,
+                    n_splits: Optional[int] = None, stream=None) -> int:
+    """attn_decode over an e4m3 cache: split + combine over keys [0, length)."""
+    if n_splits is None:
+        n_splits = attn_n_splits(length, scratch.max_splits)
+    if n_splits > scratch.max_splits:
+        raise ValueError("n_splits exceeds the scratch capacity")
+    f32 = torch.float32
+    _need(q, "q", f32, Q_HEADS * DIM)
+    _need(qg, "qg", f32, Q_HEADS * 2 * DIM)
+    _need(core, "core", f32, Q_HEADS * DIM)
+    _need_fp8(cache)
+    _lib.check(_lib.load().miso_attn_decode_fp8(
+        _ptr(q), _ptr(qg), *(_ptr(b) for b in cache.buffers()), _ptr(core),
+        _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o), length, cache.max_ctx,
+        n_splits, _stream(stream)))
+    return n_splits

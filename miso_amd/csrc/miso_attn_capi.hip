@@ -10,6 +10,7 @@
 
 #include "../../include/miso_attn.h"
 #include "attention_decode.hpp"
+#include "attention_decode_fp8.hpp"
 #include "attention_prefill.hpp"
 
 namespace k = miso::kernels;
@@ -269,6 +270,59 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
   const unsigned tiles = batch * k::attn::kQHeads * (k::attn::kDim / 64);
   k::attn_ragged_combine_kernel<<<tiles, 64, 0, as_stream(stream)>>>(r);
   return launched("miso_attn_decode_paged(combine)");
+}
+
+int miso_attn_kv_encode_fp8(const uint16_t* k_cache, const uint16_t* v_cache, uint8_t* k8,
+                            uint8_t* v8, float* k_scale, float* v_scale, uint32_t pos0, uint32_t n,
+                            uint32_t max_ctx, void* stream) {
+  if (n == 0)
+    return 0;
+  if (any_bad(k_cache, v_cache, k8, v8) || bad_scalars(k_scale) || bad_scalars(v_scale))
+    return fail("miso_attn_kv_encode_fp8", kBadPtr);
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail("miso_attn_kv_encode_fp8", "rows past max_ctx (pos0 + n > max_ctx)");
+  const k::AttnKvFp8EncodeParams p{as_half(k_cache), as_half(v_cache), k8,  v8,     k_scale,
+                                   v_scale,          pos0,             n,   max_ctx};
+  const unsigned grid = n < 8192u ? n : 8192u;  // 4 rows per workgroup, grid-stride beyond
+  k::attn_kv_fp8_encode_kernel<256><<<grid, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_kv_encode_fp8");
+}
+
+int miso_attn_prep_fp8(const float* qg, const float* kp, const float* v, const float* q_norm,
+                       const float* k_norm, const float* inv_freq, uint8_t* k8, uint8_t* v8,
+                       float* k_scale, float* v_scale, float* q, uint32_t pos, uint32_t max_ctx,
+                       float eps, void* stream) {
+  if (any_bad(qg, kp, v, q_norm, k_norm, inv_freq, k8, v8, q) || bad_scalars(k_scale) ||
+      bad_scalars(v_scale))
+    return fail("miso_attn_prep_fp8", kBadPtr);
+  if (pos >= max_ctx)
+    return fail("miso_attn_prep_fp8", "KV cache is full (pos >= max_ctx)");
+  const k::AttnPrepFp8Params p{qg, kp, v, q_norm, k_norm, inv_freq, k8, v8, k_scale, v_scale,
+                               q,  pos, max_ctx, eps};
+  k::attn_prep_fp8_kernel<256><<<18, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prep_fp8");
+}
+
+int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
+                         const float* k_scale, const float* v_scale, float* core, float* part_m,
+                         float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
+                         uint32_t n_splits, void* stream) {
+  if (any_bad(q, qg, k8, v8, core, part_o) || bad_scalars(k_scale) || bad_scalars(v_scale) ||
+      bad_scalars(part_m) || bad_scalars(part_l))
+    return fail("miso_attn_decode_fp8", kBadPtr);
+  if (len == 0)
+    return fail("miso_attn_decode_fp8", "len must be >= 1");
+  if (len > max_ctx)
+    return fail("miso_attn_decode_fp8", "len exceeds max_ctx");
+  if (n_splits == 0)
+    return fail("miso_attn_decode_fp8", "n_splits must be >= 1");
+  const k::AttnSplitFp8Params p{q,      k8,     v8,     k_scale, v_scale, part_m,
+                                part_l, part_o, len,    max_ctx, n_splits};
+  k::attn_split_fp8_kernel<256><<<dim3(n_splits, 2), 256, 0, as_stream(stream)>>>(p);
+  const int rc = launched("miso_attn_decode_fp8");
+  if (rc != 0)
+    return rc;
+  return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
 }
 
 }  // extern "C"

@@ -52,14 +52,19 @@ struct AttnPrepBatchParams {
   unsigned proj_stride;
 };
 
-// One head of 18 (0..15 query heads, 16..17 KV heads) on a 256-thread workgroup, thread d owning
-// dimension d. The sum of squares is a wave64 butterfly plus a 4-entry LDS exchange; the RoPE
-// partner (d +- 32) is lane ^ 32 of wave 0, read through the lane crossbar, so no LDS staging.
-template <int kBlock>
-__device__ void attn_prep_head(const AttnPrepParams& p, unsigned head) {
+namespace decode_detail {
+
+// Thread d's value of head `head` of 18 (0..15 query heads, 16..17 KV heads) after RMSNorm and
+// NEOX RoPE, on a 256-thread workgroup, thread d owning dimension d. The sum of squares is a
+// wave64 butterfly plus a 4-entry LDS exchange (wave_ss, free again on return); the RoPE partner
+// (d +- 32) is lane ^ 32 of wave 0, read through the lane crossbar, so no LDS staging. P is any
+// params struct with the qg / k / q_norm / k_norm / inv_freq / pos / eps fields of
+// AttnPrepParams.
+template <int kBlock, class P>
+__device__ __attribute__((always_inline)) inline float prep_value(const P& p, unsigned head,
+                                                                  float* wave_ss) {
   using namespace attn;
   static_assert(kBlock == kDim, "one thread per dimension");
-  __shared__ float wave_ss[kBlock / cdna4::kLanes];
   const unsigned d = threadIdx.x;
   const bool is_q = head < static_cast<unsigned>(kQHeads);
   const unsigned kvh = head - kQHeads;
@@ -69,6 +74,7 @@ __device__ void attn_prep_head(const AttnPrepParams& p, unsigned head) {
     wave_ss[d >> 6] = ss_wave;
   __syncthreads();
   const float ss = (wave_ss[0] + wave_ss[1]) + (wave_ss[2] + wave_ss[3]);
+  __syncthreads();  // wave_ss is reused by the next head of a grid-stride loop
   const float r = rsqrtf(ss / kDim + p.eps);
   x = x * r * (is_q ? p.q_norm[d] : p.k_norm[d]);
   if (d < static_cast<unsigned>(kRopeDim)) {  // wave 0 only: uniform for the crossbar read
@@ -78,14 +84,27 @@ __device__ void attn_prep_head(const AttnPrepParams& p, unsigned head) {
     sincosf(static_cast<float>(p.pos) * p.inv_freq[d % kHalf], &s, &c);
     x = d < kHalf ? x * c - partner * s : x * c + partner * s;
   }
-  if (is_q) {
+  return x;
+}
+
+}  // namespace decode_detail
+
+// One head of 18 on a 256-thread workgroup (prep_value), then the store: the query row, or the
+// f16 K and V rows at position pos.
+template <int kBlock>
+__device__ void attn_prep_head(const AttnPrepParams& p, unsigned head) {
+  using namespace attn;
+  __shared__ float wave_ss[kBlock / cdna4::kLanes];
+  const unsigned d = threadIdx.x;
+  const float x = decode_detail::prep_value<kBlock>(p, head, wave_ss);
+  if (head < static_cast<unsigned>(kQHeads)) {
     p.q[head * kDim + d] = x;
   } else {
+    const unsigned kvh = head - kQHeads;
     const std::size_t at = (std::size_t{kvh} * p.max_ctx + p.pos) * kDim + d;
     p.k_cache[at] = static_cast<half_t>(x);
     p.v_cache[at] = static_cast<half_t>(p.v[kvh * kDim + d]);
   }
-  __syncthreads();  // wave_ss is reused by the next head of a grid-stride loop
 }
 
 // Heads [first, first + count) of 18, one workgroup per head (grid-stride).
@@ -259,6 +278,64 @@ __device__ __attribute__((always_inline)) inline float dot2_first(half2_t a, uns
   return r;
 }
 
+// The part of one unit's online softmax that does not depend on the cache format: the
+// reduce-scatter of the lane's 16 partial dot products (see process_unit) to one score per lane
+// (head 4 hq + dc / 4, unit row 4 rq + dc % 4), the span mask, the lazy rescale, and the f16
+// numerators, published to `pbuf` for P V. With kScaled, the score is multiplied by its row's K
+// scale and the published numerator by its row's V scale (the l sum stays unscaled).
+template <bool kScaled>
+__device__ __attribute__((always_inline)) inline void unit_numerators(
+    WaveState& st, const float (&part)[16], unsigned u0, unsigned span_end, float ksc, float vsc,
+    uint32_t (*pbuf)[2][kGroup], unsigned lane) {
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  float r8[8], r4[4], r2[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    r8[j] = part[j] + cdna4::dpp_mov<cdna4::kRowRor8>(part[j ^ 8]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    r4[j] = r8[j] + cdna4::dpp_mov<cdna4::kRowHalfMirror>(r8[j ^ 7]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    r2[j] = r4[j] + cdna4::dpp_mov<cdna4::kQuadXor2>(r4[j ^ 2]);
+  float s = r2[0] + cdna4::dpp_mov<cdna4::kQuadXor1>(r2[1]);
+  if constexpr (kScaled)
+    s *= ksc;
+  const unsigned row = 4 * rq + (dc & 3u);
+  if (u0 + row >= span_end)
+    s = -__builtin_inff();
+  // Head max over its 8 lanes (dc % 4 and rq). Row u0 is always in the span, so every head has
+  // a finite score.
+  float mu = fmaxf(s, cdna4::dpp_mov<cdna4::kQuadXor1>(s));
+  mu = fmaxf(mu, cdna4::dpp_mov<cdna4::kQuadXor2>(mu));
+  mu = cdna4::max_xor16(mu);
+  st.mt = fmaxf(st.mt, mu);
+  if (__builtin_amdgcn_ballot_w64(mu > st.m + kRescaleSlack)) {  // wave-uniform branch
+    const float m_new = fmaxf(st.m, mu);
+    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first unit (m = -inf)
+    st.l *= corr;
+    st.m = m_new;
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+      const float ch =
+          cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), head_lane(h)));
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        st.o[h][e] *= ch;
+    }
+  }
+  const _Float16 p16 = static_cast<_Float16>(__builtin_amdgcn_exp2f(s - st.m));  // 0 if masked
+  st.l += static_cast<float>(p16);  // the sum of exactly the numerators P V uses
+  {
+    const unsigned head = 4 * hq + (dc >> 2);
+    _Float16* ph = reinterpret_cast<_Float16*>(&pbuf[row & 1u][(row >> 1) & 1u][head]);
+    if constexpr (kScaled)
+      ph[row >> 2] = static_cast<_Float16>(static_cast<float>(p16) * vsc);
+    else
+      ph[row >> 2] = p16;
+  }
+}
+
 // One unit (8 rows) of the online softmax.
 //
 // S: the lane's 16 partial dot products (4 heads x 4 rows, 16 of its dimensions each) are laid
@@ -303,47 +380,7 @@ __device__ __attribute__((always_inline)) inline void process_unit(
       part[4 * hh + rr] = acc;
     }
   }
-  float r8[8], r4[4], r2[2];
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    r8[j] = part[j] + cdna4::dpp_mov<cdna4::kRowRor8>(part[j ^ 8]);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    r4[j] = r8[j] + cdna4::dpp_mov<cdna4::kRowHalfMirror>(r8[j ^ 7]);
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    r2[j] = r4[j] + cdna4::dpp_mov<cdna4::kQuadXor2>(r4[j ^ 2]);
-  float s = r2[0] + cdna4::dpp_mov<cdna4::kQuadXor1>(r2[1]);
-  const unsigned row = 4 * rq + (dc & 3u);
-  if (u0 + row >= span_end)
-    s = -__builtin_inff();
-  // Head max over its 8 lanes (dc % 4 and rq). Row u0 is always in the span, so every head has
-  // a finite score.
-  float mu = fmaxf(s, cdna4::dpp_mov<cdna4::kQuadXor1>(s));
-  mu = fmaxf(mu, cdna4::dpp_mov<cdna4::kQuadXor2>(mu));
-  mu = cdna4::max_xor16(mu);
-  st.mt = fmaxf(st.mt, mu);
-  if (__builtin_amdgcn_ballot_w64(mu > st.m + kRescaleSlack)) {  // wave-uniform branch
-    const float m_new = fmaxf(st.m, mu);
-    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first unit (m = -inf)
-    st.l *= corr;
-    st.m = m_new;
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-      const float ch =
-          cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), head_lane(h)));
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        st.o[h][e] *= ch;
-    }
-  }
-  const _Float16 p16 = static_cast<_Float16>(__builtin_amdgcn_exp2f(s - st.m));  // 0 if masked
-  st.l += static_cast<float>(p16);  // the sum of exactly the numerators P V uses
-  {
-    const unsigned head = 4 * hq + (dc >> 2);
-    _Float16* ph = reinterpret_cast<_Float16*>(&pbuf[row & 1u][(row >> 1) & 1u][head]);
-    ph[row >> 2] = p16;
-  }
+  unit_numerators<false>(st, part, u0, span_end, 1.0f, 1.0f, pbuf, lane);
   // P V over this lane's rows 2 i + a, dimensions 8 c .. 8 c + 7.
   const unsigned a = lane >> 5;
 #pragma unroll
@@ -365,6 +402,93 @@ __device__ __attribute__((always_inline)) inline void process_unit(
       for (int e = 0; e < 8; ++e)
         st.o[h][e] = __builtin_amdgcn_fdot2(cdna4::as_half2(pp[h]), pv[e], st.o[h][e], false);
   }
+}
+
+// Cross-wave merge relative to the split's true max M_h = max_w mt_w,h, so the partial is
+// exactly (max, sum exp(s - max), sum exp(s - max) v). Each wave stores its raw accumulators
+// (both row parities) and head statistics, then after one barrier every thread produces two
+// float4 chunks of the partial: o = sum_w exp2(m_w,h - M_h) (o_w,0 + o_w,1). `more` says whether
+// the workgroup runs another item afterwards (its LDS is then reused).
+template <class Shared>
+__device__ __attribute__((always_inline)) inline void write_partial(
+    const WaveState& st, Shared& sh, float* part_m, float* part_l, float* part_o,
+    std::size_t base, bool more) {
+  constexpr int kW = Shared::kWaveCount;
+  const unsigned t = threadIdx.x, lane = t & 63u, c = lane & 31u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  {
+    float l = st.l + cdna4::dpp_mov<cdna4::kQuadXor1>(st.l);
+    l += cdna4::dpp_mov<cdna4::kQuadXor2>(l);  // head total over dc % 4, for this rq
+    const unsigned h = 4 * hq + (dc >> 2);
+    if ((lane & 3u) == 0)
+      sh.stat_l[wave][rq][h] = l;
+    if ((lane & 0x13u) == 0) {  // rq = 0, dc % 4 = 0: one lane per head
+      sh.stat_m[wave][h] = st.m;
+      sh.stat_mt[wave][h] = st.mt;
+    }
+    const unsigned a = lane >> 5;
+#pragma unroll
+    for (int hh = 0; hh < kGroup; ++hh) {
+      float4* dst = reinterpret_cast<float4*>(&sh.merge_o[wave][a][hh][8 * c]);
+      dst[0] = float4{st.o[hh][0], st.o[hh][1], st.o[hh][2], st.o[hh][3]};
+      dst[1] = float4{st.o[hh][4], st.o[hh][5], st.o[hh][6], st.o[hh][7]};
+    }
+  }
+  __syncthreads();
+  {
+    // 8 heads x 256 floats = 512 float4 chunks; thread t makes chunks t + kThreads j (heads
+    // (t + kThreads j) / 64). All LDS reads are issued before any arithmetic (no branches), so
+    // the phase costs one LDS round trip.
+    constexpr unsigned kChunks = kGroup * attn::kDim / 4, kThreads = kW * 64;
+    constexpr unsigned kPer = kChunks / kThreads, kHeadChunks = attn::kDim / 4;
+    static_assert(kChunks % kThreads == 0, "chunks per thread");
+    const float4* src = reinterpret_cast<const float4*>(&sh.merge_o[0][0][0][0]);
+    float4* dst = reinterpret_cast<float4*>(part_o + base * kGroup * attn::kDim);
+    float m[kPer][kW], mt[kPer][kW], lw[kPer][kW];
+    float4 x[kPer][kW][2];
+#pragma unroll
+    for (unsigned j = 0; j < kPer; ++j) {
+      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) {
+        m[j][w] = sh.stat_m[w][h];
+        mt[j][w] = sh.stat_mt[w][h];
+        lw[j][w] = sh.stat_l[w][0][h] + sh.stat_l[w][1][h];
+        x[j][w][0] = src[(w * 2 + 0) * kChunks + i];
+        x[j][w][1] = src[(w * 2 + 1) * kChunks + i];
+      }
+    }
+#pragma unroll
+    for (unsigned j = 0; j < kPer; ++j) {
+      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
+      float M = mt[j][0];
+#pragma unroll
+      for (int w = 1; w < kW; ++w)
+        M = fmaxf(M, mt[j][w]);
+      const bool empty = M == -__builtin_inff();  // no key in the span
+      const float Mc = empty ? 0.0f : M;          // exp2(-inf - 0) = 0 for every wave
+      float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      float L = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) {
+        const float sc = __builtin_amdgcn_exp2f(m[j][w] - Mc);
+        const float4 x0 = x[j][w][0], x1 = x[j][w][1];
+        acc.x = __builtin_fmaf(sc, x0.x + x1.x, acc.x);
+        acc.y = __builtin_fmaf(sc, x0.y + x1.y, acc.y);
+        acc.z = __builtin_fmaf(sc, x0.z + x1.z, acc.z);
+        acc.w = __builtin_fmaf(sc, x0.w + x1.w, acc.w);
+        L = __builtin_fmaf(sc, lw[j][w], L);
+      }
+      dst[i] = acc;
+      if (i % kHeadChunks == 0) {
+        part_m[base * kGroup + h] = M * kLn2;  // -inf stays -inf for an empty span
+        part_l[base * kGroup + h] = L;
+      }
+    }
+  }
+  if (more)
+    __syncthreads();  // LDS is reused by the next item
 }
 
 // Where the K/V rows of one sequence and KV head lie. LinearRows: row r at K / V + 256 r.
@@ -513,82 +637,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_rows(
                  lane);
   }
 
-  // Cross-wave merge relative to the split's true max M_h = max_w mt_w,h, so the partial is
-  // exactly (max, sum exp(s - max), sum exp(s - max) v). Each wave stores its raw accumulators
-  // (both row parities) and head statistics, then after one barrier every thread produces two
-  // float4 chunks of the partial: o = sum_w exp2(m_w,h - M_h) (o_w,0 + o_w,1).
-  {
-    float l = st.l + cdna4::dpp_mov<cdna4::kQuadXor1>(st.l);
-    l += cdna4::dpp_mov<cdna4::kQuadXor2>(l);  // head total over dc % 4, for this rq
-    const unsigned h = 4 * hq + (dc >> 2);
-    if ((lane & 3u) == 0)
-      sh.stat_l[wave][rq][h] = l;
-    if ((lane & 0x13u) == 0) {  // rq = 0, dc % 4 = 0: one lane per head
-      sh.stat_m[wave][h] = st.m;
-      sh.stat_mt[wave][h] = st.mt;
-    }
-    const unsigned a = lane >> 5;
-#pragma unroll
-    for (int hh = 0; hh < kGroup; ++hh) {
-      float4* dst = reinterpret_cast<float4*>(&sh.merge_o[wave][a][hh][8 * c]);
-      dst[0] = float4{st.o[hh][0], st.o[hh][1], st.o[hh][2], st.o[hh][3]};
-      dst[1] = float4{st.o[hh][4], st.o[hh][5], st.o[hh][6], st.o[hh][7]};
-    }
-  }
-  __syncthreads();
-  {
-    // 8 heads x 256 floats = 512 float4 chunks; thread t makes chunks t + kThreads j (heads
-    // (t + kThreads j) / 64). All LDS reads are issued before any arithmetic (no branches), so
-    // the phase costs one LDS round trip.
-    constexpr unsigned kChunks = kGroup * attn::kDim / 4, kThreads = kW * 64;
-    constexpr unsigned kPer = kChunks / kThreads, kHeadChunks = attn::kDim / 4;
-    static_assert(kChunks % kThreads == 0, "chunks per thread");
-    const float4* src = reinterpret_cast<const float4*>(&sh.merge_o[0][0][0][0]);
-    float4* dst = reinterpret_cast<float4*>(part_o + base * kGroup * attn::kDim);
-    float m[kPer][kW], mt[kPer][kW], lw[kPer][kW];
-    float4 x[kPer][kW][2];
-#pragma unroll
-    for (unsigned j = 0; j < kPer; ++j) {
-      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
-#pragma unroll
-      for (int w = 0; w < kW; ++w) {
-        m[j][w] = sh.stat_m[w][h];
-        mt[j][w] = sh.stat_mt[w][h];
-        lw[j][w] = sh.stat_l[w][0][h] + sh.stat_l[w][1][h];
-        x[j][w][0] = src[(w * 2 + 0) * kChunks + i];
-        x[j][w][1] = src[(w * 2 + 1) * kChunks + i];
-      }
-    }
-#pragma unroll
-    for (unsigned j = 0; j < kPer; ++j) {
-      const unsigned i = t + kThreads * j, h = i / kHeadChunks;
-      float M = mt[j][0];
-#pragma unroll
-      for (int w = 1; w < kW; ++w)
-        M = fmaxf(M, mt[j][w]);
-      const bool empty = M == -__builtin_inff();  // no key in the span
-      const float Mc = empty ? 0.0f : M;          // exp2(-inf - 0) = 0 for every wave
-      float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      float L = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kW; ++w) {
-        const float sc = __builtin_amdgcn_exp2f(m[j][w] - Mc);
-        const float4 x0 = x[j][w][0], x1 = x[j][w][1];
-        acc.x = __builtin_fmaf(sc, x0.x + x1.x, acc.x);
-        acc.y = __builtin_fmaf(sc, x0.y + x1.y, acc.y);
-        acc.z = __builtin_fmaf(sc, x0.z + x1.z, acc.z);
-        acc.w = __builtin_fmaf(sc, x0.w + x1.w, acc.w);
-        L = __builtin_fmaf(sc, lw[j][w], L);
-      }
-      dst[i] = acc;
-      if (i % kHeadChunks == 0) {
-        part_m[base * kGroup + h] = M * kLn2;  // -inf stays -inf for an empty span
-        part_l[base * kGroup + h] = L;
-      }
-    }
-  }
-  if (more)
-    __syncthreads();  // LDS is reused by the next item
+  write_partial(st, sh, part_m, part_l, part_o, base, more);
 }
 
 template <class Shared>

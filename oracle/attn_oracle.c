@@ -25,6 +25,11 @@
  *   - oracle_ref_n_splits: the reference split-count policy, kernels/attention_decode.hpp:92-115.
  *   - oracle_ragged_f64:   oracle_decode_f64 per sequence with a dense [B][16][256] gate
  *                          (no reference function: the reference is batch-1).
+ *   - oracle_e4m3_value / oracle_e4m3_encode / oracle_fp8_encode_rows / oracle_decode_fp8_f64:
+ *                          the e4m3 KV-row format of miso_amd/kernels/attention_decode_fp8.hpp
+ *                          and oracle_decode_f64 over its dequantized rows (no reference
+ *                          function: the reference's cache is f16). The encoder is a search
+ *                          for the nearest code, not the kernels' bit arithmetic.
  *
  * Inputs come from a portable generator (splitmix64-seeded xoshiro256**, Box-Muller normals,
  * round-to-nearest-even binary16), so GPU tests and this oracle see bit-identical inputs on any
@@ -481,4 +486,108 @@ uint32_t oracle_ref_n_splits(uint32_t len, uint32_t max_splits) {
     }
   }
   return n;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* e4m3 KV rows (no reference counterpart: the reference's cache is f16,                       */
+/* src/engine/attention.hpp:35-41). Restates the format documented in                          */
+/* miso_amd/kernels/attention_decode_fp8.hpp: value = scale * e4m3(code), OCP e4m3 (bias 7,    */
+/* subnormal step 2^-9, max 448), scale = 2^(E - 7) with E = floor(log2 max|x|) (>= -100).     */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Value of an e4m3 code from its fields (0x7F / 0xFF are NaN). */
+double oracle_e4m3_value(uint8_t c) {
+  const int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+  if (e == 15 && m == 7) return NAN;
+  const double v = e ? ldexp(1.0 + m / 8.0, e - 7) : ldexp(m / 8.0, -6);
+  return s ? -v : v;
+}
+
+/* Round-to-nearest-even e4m3 code of y, |y| < 256, by search: the representable magnitude
+ * nearest to |y|, ties to the even code (the one with a clear lowest mantissa bit). */
+uint8_t oracle_e4m3_encode(float y) {
+  const double a = fabs((double)y);
+  int best = 0;
+  double best_err = INFINITY;
+  for (int c = 0; c <= 0x78; ++c) {
+    const double err = fabs(oracle_e4m3_value((uint8_t)c) - a);
+    if (err < best_err || (err == best_err && (c & 1) == 0)) best = c, best_err = err;
+  }
+  return (uint8_t)(best | (signbit(y) ? 0x80 : 0));
+}
+
+/* Rows of 256 floats -> codes and power-of-two scales. */
+void oracle_fp8_encode_rows(const float* x, size_t rows, uint8_t* codes, float* scales) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * KD;
+    float amax = 0;
+    for (int d = 0; d < KD; ++d)
+      if (fabsf(xr[d]) > amax) amax = fabsf(xr[d]);
+    int e = -100;
+    if (amax > 0) {
+      int ex;
+      frexpf(amax, &ex); /* amax = f 2^ex, f in [0.5, 1): floor(log2 amax) = ex - 1 */
+      if (ex - 1 > e) e = ex - 1;
+    }
+    const float inv = ldexpf(1.0f, 7 - e);
+    for (int d = 0; d < KD; ++d) codes[r * KD + d] = oracle_e4m3_encode(xr[d] * inv);
+    scales[r] = ldexpf(1.0f, e - 7);
+  }
+}
+
+/* attend_row over e4m3 rows: K / V row j is scale[j] * e4m3(code[j][.]), in double. */
+static void attend_row_fp8(const float* q, const float* gate, const uint8_t* K, const uint8_t* V,
+                           const float* ks, const float* vs, size_t seen, double* s,
+                           double* out) {
+  double lut[256];
+  for (int c = 0; c < 256; ++c) lut[c] = oracle_e4m3_value((uint8_t)c);
+  double mx = -1e300;
+  for (size_t j = 0; j < seen; ++j) {
+    const uint8_t* kr = K + j * KD;
+    double d = 0;
+    for (int e = 0; e < KD; ++e) d += (double)q[e] * lut[kr[e]];
+    s[j] = d * (double)ks[j] / 16.0;
+    if (s[j] > mx) mx = s[j];
+  }
+  double l = 0;
+  for (size_t j = 0; j < seen; ++j) {
+    s[j] = exp(s[j] - mx);
+    l += s[j];
+  }
+  double o[KD];
+  for (int e = 0; e < KD; ++e) o[e] = 0;
+  for (size_t j = 0; j < seen; ++j) {
+    const uint8_t* vr = V + j * KD;
+    const double pj = s[j] * (double)vs[j];
+    for (int e = 0; e < KD; ++e) o[e] += pj * lut[vr[e]];
+  }
+  for (int e = 0; e < KD; ++e) out[e] = o[e] / l / (1.0 + exp(-(double)gate[e]));
+}
+
+typedef struct {
+  const float* q;
+  const float* qg;
+  const uint8_t* k8;
+  const uint8_t* v8;
+  const float* ks;
+  const float* vs;
+  size_t len, max_ctx;
+  double* out;
+} decode_fp8_ctx_t;
+
+static void decode_fp8_row(void* p, size_t h) {
+  decode_fp8_ctx_t* c = (decode_fp8_ctx_t*)p;
+  const size_t kvh = h / KGROUP, base = kvh * c->max_ctx;
+  double* s = (double*)malloc(sizeof(double) * (c->len ? c->len : 1));
+  attend_row_fp8(c->q + h * KD, c->qg + h * 2 * KD + KD, c->k8 + base * KD, c->v8 + base * KD,
+                 c->ks + base, c->vs + base, c->len, s, c->out + h * KD);
+  free(s);
+}
+
+/* oracle_decode_f64 over e4m3 rows: k8 / v8 [2][max_ctx][256], ks / vs [2][max_ctx]. */
+void oracle_decode_fp8_f64(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
+                           const float* ks, const float* vs, uint32_t len, uint32_t max_ctx,
+                           double* out, int threads) {
+  decode_fp8_ctx_t c = {q, qg, k8, v8, ks, vs, len, max_ctx, out};
+  parallel_rows(decode_fp8_row, &c, KQ, threads);
 }

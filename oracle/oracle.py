@@ -56,6 +56,10 @@ def lib() -> ctypes.CDLL:
             "oracle_inv_freq": (None, [c_float, V]),
             "oracle_prep_f64": (None, [V, V, V, V, V, V, c_uint32, c_float, V, V, V]),
             "oracle_ref_n_splits": (c_uint32, [c_uint32, c_uint32]),
+            "oracle_e4m3_value": (c_double, [ctypes.c_uint8]),
+            "oracle_e4m3_encode": (ctypes.c_uint8, [c_float]),
+            "oracle_fp8_encode_rows": (None, [V, ctypes.c_size_t, V, V]),
+            "oracle_decode_fp8_f64": (None, [V, V, V, V, V, V, c_uint32, c_uint32, V, c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -188,6 +192,51 @@ def decode_f64(q, qg, k, v, length: int, max_ctx: int, threads: int = 0) -> np.n
     out = np.empty((Q_HEADS, DIM), dtype=np.float64)
     lib().oracle_decode_f64(_ptr(q), _ptr(qg), _ptr(k), _ptr(v), length, max_ctx, _ptr(out),
                             threads or default_threads())
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# e4m3 KV rows (the format of miso_amd/kernels/attention_decode_fp8.hpp; no reference counterpart)
+# ------------------------------------------------------------------------------------------------
+
+def e4m3_table() -> np.ndarray:
+    """Value of each of the 256 e4m3 codes (NaN for 0x7F / 0xFF)."""
+    return np.array([lib().oracle_e4m3_value(c) for c in range(256)], dtype=np.float64)
+
+
+def e4m3_encode(y: float) -> int:
+    """Nearest e4m3 code of y (|y| < 256), ties to even, found by search."""
+    return int(lib().oracle_e4m3_encode(float(y)))
+
+
+def fp8_encode_rows(x) -> tuple[np.ndarray, np.ndarray]:
+    """Rows of 256 floats -> (codes uint8 [rows, 256], power-of-two scales float32 [rows])."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, DIM)
+    codes = np.empty(x.shape, dtype=np.uint8)
+    scales = np.empty(x.shape[0], dtype=np.float32)
+    lib().oracle_fp8_encode_rows(_ptr(x), x.shape[0], _ptr(codes), _ptr(scales))
+    return codes, scales
+
+
+def fp8_dequant(codes, scales) -> np.ndarray:
+    """value = scale * e4m3(code), in float64, shape of codes."""
+    codes = np.asarray(codes, np.uint8)
+    return e4m3_table()[codes] * np.asarray(scales, np.float64).reshape(
+        codes.shape[:-1] + (1,))
+
+
+def decode_fp8_f64(q, qg, k8, v8, ks, vs, length: int, max_ctx: int,
+                   threads: int = 0) -> np.ndarray:
+    """decode_f64 over e4m3 rows: k8 / v8 [2][max_ctx][256] uint8, ks / vs [2][max_ctx]."""
+    q = np.ascontiguousarray(q, np.float32)
+    qg = np.ascontiguousarray(qg, np.float32)
+    k8 = np.ascontiguousarray(k8, np.uint8)
+    v8 = np.ascontiguousarray(v8, np.uint8)
+    ks = np.ascontiguousarray(ks, np.float32)
+    vs = np.ascontiguousarray(vs, np.float32)
+    out = np.empty((Q_HEADS, DIM), dtype=np.float64)
+    lib().oracle_decode_fp8_f64(_ptr(q), _ptr(qg), _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs),
+                                length, max_ctx, _ptr(out), threads or default_threads())
     return out
 
 

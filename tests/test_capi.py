@@ -78,6 +78,12 @@ def test_host_validation_rejects_bad_arguments(lib):
     for bad_page in (0, 4, 12, 131072):
         rejected(paged(P, P, P, P, P, 4, bad_page, P, 3, 10, P, P, P, P, N), lib, "page_size")
     rejected(paged(P, P, P, P, P, 4, 16, P, 3, 65, P, P, P, P, N), lib, "max_pages * page_size")
+    enc, prep8, dec8 = lib.miso_attn_kv_encode_fp8, lib.miso_attn_prep_fp8, lib.miso_attn_decode_fp8
+    rejected(enc(P, P, P, P, P, P, 8, 3, 10, N), lib, "max_ctx")
+    rejected(prep8(P, P, P, P, P, P, P, P, P, P, P, 10, 10, 1e-6, N), lib, "full")
+    rejected(dec8(P, P, P, P, P, P, P, P, P, P, 0, 10, 4, N), lib, "len must be")
+    rejected(dec8(P, P, P, P, P, P, P, P, P, P, 11, 10, 4, N), lib, "exceeds max_ctx")
+    rejected(dec8(P, P, P, P, P, P, P, P, P, P, 5, 10, 0, N), lib, "n_splits")
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")
@@ -105,6 +111,19 @@ def test_host_validation_rejects_null_and_misaligned_pointers(lib):
                  bad)
     rejected(lib.miso_attn_decode_paged(P, P, P, P, N, 4, 16, P, 3, 10, P, P, P, P, N), lib, bad)
     rejected(lib.miso_attn_decode_paged(P, P, P, P, P, 4, 16, N, 3, 10, P, P, P, P, N), lib, bad)
+    # fp8 cache: codes need 16-byte alignment, the per-row scales 4-byte alignment
+    for q in (N, P + 4):
+        rejected(lib.miso_attn_kv_encode_fp8(P, P, q, P, P, P, 0, 3, 10, N), lib, bad)
+        rejected(lib.miso_attn_prep_fp8(P, P, P, P, P, P, P, q, P, P, P, 1, 10, 1e-6, N), lib,
+                 bad)
+        rejected(lib.miso_attn_decode_fp8(P, P, q, P, P, P, P, P, P, P, 5, 10, 4, N), lib, bad)
+    for s_bad in (N, P + 2):
+        rejected(lib.miso_attn_kv_encode_fp8(P, P, P, P, s_bad, P, 0, 3, 10, N), lib, bad)
+        rejected(lib.miso_attn_prep_fp8(P, P, P, P, P, P, P, P, P, s_bad, P, 1, 10, 1e-6, N),
+                 lib, bad)
+        rejected(lib.miso_attn_decode_fp8(P, P, P, P, s_bad, P, P, P, P, P, 5, 10, 4, N), lib,
+                 bad)
+    assert lib.miso_attn_kv_encode_fp8(N, N, N, N, N, N, 0, 0, 10, N) == 0  # n == 0: no-op
 
 
 def test_python_layer_raises_runtime_error_with_message():

@@ -1,0 +1,193 @@
+"""fp8 (e4m3 rows) KV cache on MI355X, through the C ABI, against the oracle.
+
+  * encode: codes and scales bit-identical to the oracle's nearest-code encoder;
+  * decode: split + combine over e4m3 rows against oracle_decode_fp8_f64 on the same codes and
+    scales, gate |got - ref| <= 2e-3 + 1e-2 |ref| (the kernel's own arithmetic: f16 query,
+    f16 numerators, f32 sums), over the reference's boundary lengths, the C2 size, every code
+    value, and with NaN codes past len (a read past the cache would show);
+  * prep: the q output bit-identical to attn_prep's, V codes bit-identical to the oracle's, K
+    within half a code step of the oracle's normalised, rotated row;
+  * the format's own error against the f16 cache (reported, bounded loosely): it is a property
+    of e4m3 storage, not of the kernels.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import report, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+H, KV, D = 16, 2, 256
+CANARY = -9123.5
+
+
+def encode_host(O, k16, v16, max_ctx):
+    kf = O.f16_to_f32(k16).reshape(KV * max_ctx, D)
+    vf = O.f16_to_f32(v16).reshape(KV * max_ctx, D)
+    return O.fp8_encode_rows(kf) + O.fp8_encode_rows(vf)  # k8, ks, v8, vs
+
+
+def upload(attn, torch, k8, ks, v8, vs, max_ctx):
+    c = attn.Fp8Cache(max_ctx)
+    c.k8.copy_(torch.from_numpy(k8.reshape(-1)))
+    c.v8.copy_(torch.from_numpy(v8.reshape(-1)))
+    c.k_scale.copy_(torch.from_numpy(ks.reshape(-1)))
+    c.v_scale.copy_(torch.from_numpy(vs.reshape(-1)))
+    return c
+
+
+def run_decode_fp8(attn, torch, q, qg, cache, length, max_splits, n_splits=None):
+    core = torch.full((H * D,), CANARY, dtype=torch.float32, device="cuda")
+    sc = attn.DecodeScratch(max_splits)
+    n = attn.attn_decode_fp8(to_dev(torch, q), to_dev(torch, qg), cache, core, sc, length,
+                             n_splits)
+    torch.cuda.synchronize()
+    out = to_host(core).reshape(H, D)
+    assert not (out == CANARY).any(), "unwritten outputs"
+    return out, n
+
+
+def test_encode_kernel_bit_identical(O, attn, torch_mod):
+    torch = torch_mod
+    max_ctx, pos0, n = 300, 37, 250
+    d = O.decode_inputs(41, max_ctx, max_ctx)
+    k16 = d["k"].reshape(KV, max_ctx, D).copy()
+    v16 = d["v"].reshape(KV, max_ctx, D).copy()
+    k16[0, 40] = 0                                       # zero row
+    k16[1, 41] = O.f32_to_f16(np.full(D, 6e-8, np.float32))   # f16 subnormals
+    v16[0, 42] = O.f32_to_f16(np.linspace(-65504, 65504, D).astype(np.float32))  # f16 extremes
+    mids = (O.e4m3_table()[0x38:0x40] + O.e4m3_table()[0x39:0x41]) / 2  # exact ties at scale 1
+    v16[1, 43] = O.f32_to_f16(np.resize(mids * (2.0 ** -7) * 128, D).astype(np.float32))
+    kc, vc = to_dev(torch, k16.reshape(-1)), to_dev(torch, v16.reshape(-1))
+    cache = attn.Fp8Cache(max_ctx)
+    cache.k8.fill_(0xAB)
+    cache.k_scale.fill_(-1.0)
+    attn.attn_kv_encode_fp8(kc, vc, cache, pos0, n)
+    torch.cuda.synchronize()
+    k8, ks, v8, vs = encode_host(O, k16.reshape(-1), v16.reshape(-1), max_ctx)
+    rows = np.zeros((KV, max_ctx), bool)
+    rows[:, pos0:pos0 + n] = True
+    rows = rows.reshape(-1)
+    gk8 = to_host(cache.k8).reshape(KV * max_ctx, D)
+    gks = to_host(cache.k_scale)
+    assert np.array_equal(gk8[rows], k8[rows]) and np.array_equal(gks[rows], ks[rows])
+    assert np.array_equal(to_host(cache.v8).reshape(-1, D)[rows], v8[rows])
+    assert np.array_equal(to_host(cache.v_scale)[rows], vs[rows])
+    assert (gk8[~rows] == 0xAB).all() and (gks[~rows] == -1.0).all()  # nothing else written
+
+
+@pytest.mark.parametrize("length", [1, 15, 16, 17, 63, 64, 65, 257, 1000, 4101])
+def test_decode_fp8_boundaries(O, attn, torch_mod, length):
+    torch = torch_mod
+    max_ctx = length + 21
+    d = O.decode_inputs(length, length, max_ctx, q_scale=2.0)
+    k8, ks, v8, vs = encode_host(O, d["k"], d["v"], max_ctx)
+    # rows past len hold NaN codes and NaN scales: any read of them would poison the output
+    for a in (k8, v8):
+        a.reshape(KV, max_ctx, D)[:, length:] = 0x7F
+    for a in (ks, vs):
+        a.reshape(KV, max_ctx)[:, length:] = np.nan
+    cache = upload(attn, torch, k8, ks, v8, vs, max_ctx)
+    ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs, length, max_ctx)
+    for cap in (60, 128):
+        got, n = run_decode_fp8(attn, torch, d["q"], d["qg"], cache, length, cap)
+        st = O.compare(got, ref)
+        report(f"fp8 decode len={length} splits={n}", st)
+        assert st["ok"], st
+
+
+def test_decode_fp8_c2_and_format_error(O, attn, torch_mod):
+    """C2 (32768 keys, q/K/V N(0,1) from seed = len): parity with the oracle on the e4m3 rows,
+    independence of the split count, and the format's error against the f16 cache."""
+    torch = torch_mod
+    L = 32768
+    d = O.decode_inputs(L, L, L, q_scale=1.0)
+    k8, ks, v8, vs = encode_host(O, d["k"], d["v"], L)
+    cache = upload(attn, torch, k8, ks, v8, vs, L)
+    ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs, L, L)
+    outs = []
+    for n in (128, 1, 7):
+        got, _ = run_decode_fp8(attn, torch, d["q"], d["qg"], cache, L, 128, n)
+        st = O.compare(got, ref)
+        report(f"fp8 decode C2 splits={n}", st)
+        assert st["ok"], st
+        outs.append(got)
+    for o in outs[1:]:
+        assert O.compare(o, outs[0].astype(np.float64))["ok"]
+    ref16 = O.decode_f64(d["q"], d["qg"], d["k"], d["v"], L, L)
+    st = O.compare(outs[0], ref16)
+    report("fp8 format vs f16 cache, C2", st)
+    assert st["rel_l2"] < 0.05, st
+
+
+def test_decode_fp8_every_code(O, attn, torch_mod):
+    """Random bytes over every finite code (both signs, subnormals, 448) with random
+    power-of-two row scales: each code's widening to f16 and both scale paths are exercised."""
+    torch = torch_mod
+    L = max_ctx = 2048
+    rng = np.random.default_rng(17)
+    finite = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+    k8 = rng.choice(finite, size=(KV * L, D)).astype(np.uint8)
+    v8 = rng.choice(finite, size=(KV * L, D)).astype(np.uint8)
+    ks = (2.0 ** rng.integers(-11, -8, KV * L)).astype(np.float32)
+    vs = (2.0 ** rng.integers(-9, -3, KV * L)).astype(np.float32)
+    d = O.decode_inputs(3, L, L, q_scale=1.0)
+    cache = upload(attn, torch, k8, ks, v8, vs, max_ctx)
+    ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs, L, max_ctx)
+    got, n = run_decode_fp8(attn, torch, d["q"], d["qg"], cache, L, 128)
+    st = O.compare(got, ref)
+    report(f"fp8 decode every code splits={n}", st)
+    assert st["ok"], st
+
+
+def test_prep_fp8_and_engine_sequence(O, attn, torch_mod):
+    """prep_fp8 at several positions: q equals attn_prep's bit for bit, V codes equal the
+    oracle's, K within half a code step of the oracle's row; then decode over the cache the
+    appends built, against the oracle on the same codes."""
+    torch = torch_mod
+    PROJ, EPS = 9216, 1e-6
+    rng = np.random.default_rng(77)
+    q_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    k_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    inv = O.inv_freq(10_000_000.0)
+    w = [to_dev(torch, a) for a in (q_norm, k_norm, inv)]
+    max_ctx, P = 700, 640
+    d = O.decode_inputs(7, P, max_ctx)
+    k8, ks, v8, vs = encode_host(O, d["k"], d["v"], max_ctx)
+    cache = upload(attn, torch, k8, ks, v8, vs, max_ctx)  # positions >= P are overwritten below
+    kc16 = torch.zeros(KV * max_ctx * D, dtype=torch.float16, device="cuda")
+    vc16 = torch.zeros_like(kc16)
+    q8 = torch.empty(H * D, device="cuda")
+    q16 = torch.empty(H * D, device="cuda")
+    out = torch.empty(H * D, device="cuda")
+    sc = attn.DecodeScratch(128)
+    for i in range(12):
+        pos = P + i
+        proj = O.normal(900 + pos, PROJ)
+        dp = to_dev(torch, proj)
+        attn.attn_prep_fp8(dp[:8192], dp[8192:8704], dp[8704:], *w, cache, q8, pos, EPS)
+        attn.attn_prep(dp[:8192], dp[8192:8704], dp[8704:], *w, kc16, vc16, q16, pos, max_ctx,
+                       EPS)
+        attn.attn_decode_fp8(q8, dp[:8192], cache, out, sc, pos + 1)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(q8), to_host(q16))
+        _, k_ref, _ = O.prep_f64(proj[:8192], proj[8192:8704], proj[8704:], q_norm, k_norm, inv,
+                                 pos, EPS)
+        g8 = to_host(cache.k8).reshape(KV, max_ctx, D)[:, pos]
+        gs = to_host(cache.k_scale).reshape(KV, max_ctx)[:, pos]
+        gv8 = to_host(cache.v8).reshape(KV, max_ctx, D)[:, pos]
+        gvs = to_host(cache.v_scale).reshape(KV, max_ctx)[:, pos]
+        v_codes, v_scales = O.fp8_encode_rows(proj[8704:].reshape(KV, D))
+        assert np.array_equal(gv8, v_codes) and np.array_equal(gvs, v_scales)
+        kx = O.f16_to_f32(k_ref).astype(np.float64)  # the oracle's row, f16-rounded
+        deq = O.fp8_dequant(g8, gs)
+        assert np.all(np.abs(deq - kx) <= np.abs(kx) * (2.0 ** -4 + 2.0 ** -10)
+                      + gs[:, None] * 2.0 ** -9 + 1e-6)
+        kh, vh = to_host(cache.k8), to_host(cache.v8)
+        ref = O.decode_fp8_f64(to_host(q8), proj[:8192], kh, vh, to_host(cache.k_scale),
+                               to_host(cache.v_scale), pos + 1, max_ctx)
+        st = O.compare(to_host(out).reshape(H, D), ref)
+        report(f"fp8 engine decode len={pos + 1}", st)
+        assert st["ok"], st
