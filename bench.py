@@ -23,7 +23,8 @@ Also reported:
                 MFMA (libmiso_probe.so), against the 1024 cycles the tile's MFMAs take.
   other_configs C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
-                and C5 over a pool of 16-row KV pages (the paged entry point).
+                and C5 over a pool of 16-row KV pages (the paged entry point); C2 over an fp8
+                (e4m3 rows) KV cache: us per decode step and GB/s of codes + row scales.
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
 Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
@@ -425,8 +426,39 @@ def bench_other(torch, A, args):
                        "page_size": page, "pages": pool, "ms_per_call": round(t5p, 4),
                        "gbs": round(bytes5 / (t5p * 1e-3) / 1e9, 1),
                        "frac": round(bytes5 / (t5p * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kp, vp
+    # C2 over an fp8 (e4m3 rows) cache: the same context and buffer rotation as the C2 line,
+    # each cache encoded on the GPU from an N(0,1) f16 cache.
+    L, R = args.ctx, args.buffers
+    gen.manual_seed(L + 1)
+    q = torch.randn(H * D, generator=gen, device="cuda")
+    qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
+    caches8 = []
+    for _ in range(R):
+        k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+        v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+        c8 = A.Fp8Cache(L)
+        A.attn_kv_encode_fp8(k, v, c8, 0, L)
+        caches8.append(c8)
+    del k, v
+    sc = A.DecodeScratch(args.max_splits)
+    n8 = A.attn_n_splits(L, args.max_splits)
+    core = torch.empty(H * D, device="cuda")
+    g = graph_of(torch, lambda i: A.attn_decode_fp8(q, qg, caches8[i % R], core, sc, L, n8), R)
+    time_replays(torch, g, 2)
+    reps = max(1, (args.steps + R - 1) // R)
+    ms = sorted(time_replays(torch, g, reps)[0] for _ in range(3))[1]
+    t8 = ms / (reps * R)
+    bytes8 = 2.0 * KV * L * (D + 4)  # codes and row scales of K and V
+    out["C2_fp8"] = {"workload": f"C2 (decode, 1 sequence x 1 token, ctx {L}) over an e4m3-row "
+                                 "KV cache (1-byte codes + one f32 scale per row)",
+                     "us_per_step": round(t8 * 1e3, 2), "n_splits": n8,
+                     "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
+                     "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del caches8
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
-        f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s")
+        f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
+        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step")
     return out
 
 

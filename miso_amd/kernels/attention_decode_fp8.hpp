@@ -196,11 +196,15 @@ namespace decode_detail {
 // 256 r -- the f16 unit's 8 KiB slot -- and 64 scales (K rows 0-15, V rows 0-15, then a copy).
 constexpr unsigned kFp8UnitRows = 16;
 
-struct SplitFp8Shared {
-  static constexpr int kWaveCount = kWaves, kRingUnits = kRing;
-  SplitShared base;
-  float scale[kWaves][kRing][64];
+constexpr int kFp8Ring = 2;  // units per wave's LDS ring: kFp8Ring - 1 in flight under one
+
+template <int R>
+struct SplitFp8SharedT {
+  static constexpr int kWaveCount = kWaves, kRingUnits = R;
+  SplitSharedT<kWaves, R> base;
+  float scale[kWaves][R][64];
 };
+using SplitFp8Shared = SplitFp8SharedT<kFp8Ring>;
 
 // Global -> LDS copy of one e4m3 unit: 4 row quads of K and of V (1 KiB each: row u0 + 4 i +
 // lane / 16, bytes 16 (lane % 16)), then one 4-byte load per lane of the scales. `kw` / `vw` are
@@ -359,13 +363,15 @@ __device__ __attribute__((always_inline)) inline void process_unit_fp8(
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh over e4m3 rows (K8 / V8 /
 // KS / VS: the KV head's bases), written at `base` in the reference's partial layout. The same
 // schedule as split_partial_rows with 16-row units: wave w streams units starting at rows
-// span.begin + 16 w, + 64, ... through its 2-unit LDS ring; rows past the span are masked and
+// span.begin + 16 w, + 64, ... through its kRingUnits-unit LDS ring; rows past the span are masked and
 // rows past len - 1 are never read.
+template <class Shared>
 __device__ __attribute__((always_inline)) inline void split_partial_fp8(
     const float* __restrict__ q, const uint8_t* K8, const uint8_t* V8, const float* KS,
     const float* VS, unsigned len, AttnSpan span, unsigned kvh, float* part_m, float* part_l,
-    float* part_o, std::size_t base, SplitFp8Shared& sh, bool more) {
-  constexpr int kW = kWaves, kR = kRing;
+    float* part_o, std::size_t base, Shared& sh, bool more) {
+  constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
+  static_assert(kR >= 2 && kR <= 4 && kW == kWaves, "ring depth / wave count");
   const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned last_row = len - 1;
