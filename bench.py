@@ -25,6 +25,7 @@ Also reported:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
                 and C5 over a pool of 16-row KV pages (the paged entry point); C2 over an fp8
                 (e4m3 rows) KV cache: us per decode step and GB/s of codes + row scales.
+                F4_q4k_gemv: the Q4_K GEMV at the attention's projection shapes (us, GB/s).
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
 Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
@@ -456,9 +457,35 @@ def bench_other(torch, A, args):
                      "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
                      "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del caches8
+    # Q4_K GEMV of the attention's projections (row f4), f16 activations as the engine: weights
+    # rotated over >= 512 MB of copies so they stream from HBM as a model's layers do.
+    gemv = {}
+    for name, k, n in (("attn_q", 2048, 8192), ("attn_k", 2048, 512), ("attn_output", 4096, 2048)):
+        wbytes = n * k // 256 * 144
+        copies = max(2, -(-(512 << 20) // wbytes))
+        wq = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device="cuda", generator=gen)
+        # finite f16 d / dmin in every block (bytes 0..3)
+        blk = wq.view(copies, -1, 144)
+        blk[:, :, 0:4] = torch.tensor([0x1F, 0x1E, 0x0F, 0x1A], dtype=torch.uint8, device="cuda")
+        xg = torch.randn(k, generator=gen, device="cuda")
+        yg = torch.empty(n, device="cuda")
+        g = graph_of(torch, lambda i: A.q4k_gemv(wq[i % copies], xg, yg, n, k), copies)
+        time_replays(torch, g, 1)
+        ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
+        t = ms / (3 * copies)
+        gemv[name] = {"k": k, "n_rows": n, "weight_bytes": wbytes, "us_per_call": round(t * 1e3, 2),
+                      "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                      "frac": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "weight_copies_rotated": copies}
+        del wq, blk
+    out["F4_q4k_gemv"] = {"workload": "Q4_K r1 GEMV y = W x with f16 activations at the engine's "
+                                      "Q4_K attention projections (synthetic blocks, HBM-resident "
+                                      "weights)", **gemv}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
-        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step")
+        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
+        + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
+                    for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict)))
     return out
 
 

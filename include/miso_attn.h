@@ -171,6 +171,16 @@ int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, con
                          float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                          uint32_t n_splits, void* stream);
 
+/* Q4_K GEMV y = W x (row f4: the attention's Q4_K projections attn_q, attn_k, attn_output). Replaces
+ * the launches of q4k_gemv_kernel<ActFormat, K, 256, R> in gemv() (src/engine/weights.hip:248-275,
+ * kernels/q4k_gemv.hpp:196-239). w: n_rows rows of k / 256 Q4_K blocks in the r1 layout
+ * (src/repack.hpp:14-19; 144 bytes per block, 16-byte aligned), x: k floats (16-byte aligned),
+ * y: n_rows floats. act_format 1 converts x to f16 (the engine's choice), 0 to per-32 absmax
+ * int8. n_rows == 0 is a no-op. Rejects k other than 2048, 4096, 8192 and other act_format
+ * values. */
+int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
+                       int act_format, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

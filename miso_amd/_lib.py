@@ -37,6 +37,7 @@ SIGNATURES = {
                                    P]),
     "miso_attn_decode_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                      P]),
+    "miso_attn_q4k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, c_int, P]),
 }
 
 _lib = None

@@ -306,3 +306,18 @@ def attn_decode_fp8(q, qg, cache: Fp8Cache, core, scratch: DecodeScratch, length
         _ptr(scratch.part_m), _ptr(scratch.part_l), _ptr(scratch.part_o), length, cache.max_ctx,
         n_splits, _stream(stream)))
     return n_splits
+
+
+# ------------------------------------------------------------------------------------------------
+# Q4_K GEMV of the attention's projections (weights: rows of Q4_K r1 blocks, 144 bytes per 256)
+# ------------------------------------------------------------------------------------------------
+
+def q4k_gemv(w, x, y, n_rows: int, k: int, act: str = "fp16", stream=None) -> None:
+    """y[:n_rows] = W x for Q4_K r1 rows w (uint8 device tensor, n_rows * k / 256 * 144 bytes)."""
+    if act not in ("fp16", "int8"):
+        raise ValueError("act must be 'fp16' or 'int8'")
+    _need(w, "w", torch.uint8, n_rows * k // 256 * 144)
+    _need(x, "x", torch.float32, k)
+    _need(y, "y", torch.float32, n_rows)
+    _lib.check(_lib.load().miso_attn_q4k_gemv(_ptr(w), _ptr(x), _ptr(y), n_rows, k,
+                                              1 if act == "fp16" else 0, _stream(stream)))

@@ -12,6 +12,7 @@
 #include "attention_decode.hpp"
 #include "attention_decode_fp8.hpp"
 #include "attention_prefill.hpp"
+#include "q4k_gemv.hpp"
 
 namespace k = miso::kernels;
 using k::attn::half_t;
@@ -33,6 +34,27 @@ int launched(const char* fn) {
     return 0;
   g_last_error = std::string(fn) + ": " + hipGetErrorName(err) + " (" + hipGetErrorString(err) + ")";
   return static_cast<int>(err);
+}
+
+// Q4_K GEMV launch shapes, from a sweep of workgroup size x rows per wave step at the engine's
+// Q4_K projections (f16 activations, HBM-resident weights): up to 1024 rows, one-wave workgroups
+// and one row per step (attn_k, 512 rows: 2.50 us against 3.62 us with 4-wave workgroups and 4
+// rows); more rows, 4-wave workgroups and K / 512 rows per step (attn_q 8192 x 2048: 5.35 us,
+// attn_output 2048 x 4096: 4.25 us). One step per wave up to 8192 workgroups (grid-stride beyond).
+template <k::ActFormat A, unsigned K, int kBlock, int kRows>
+void launch_q4k_shape(const k::Q4kGemvParams& p, hipStream_t stream) {
+  const unsigned per_wg = (kBlock / 64) * kRows;
+  unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
+  grid = grid < 8192u ? grid : 8192u;
+  k::q4k_gemv_kernel<A, K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
+}
+
+template <k::ActFormat A, unsigned K>
+void launch_q4k(const k::Q4kGemvParams& p, hipStream_t stream) {
+  if (p.n_rows <= 1024)
+    launch_q4k_shape<A, K, 64, 1>(p, stream);
+  else
+    launch_q4k_shape<A, K, 256, (K == 2048 ? 4 : K == 4096 ? 2 : 1)>(p, stream);
 }
 
 template <bool kPrepared, int kPipeline>
@@ -323,6 +345,30 @@ int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, con
   if (rc != 0)
     return rc;
   return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
+}
+
+int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
+                       int act_format, void* stream) {
+  if (n_rows == 0)
+    return 0;
+  if (any_bad(w, x) || bad_scalars(y))
+    return fail("miso_attn_q4k_gemv", kBadPtr);
+  if (k != 2048 && k != 4096 && k != 8192)
+    return fail("miso_attn_q4k_gemv", "k must be 2048, 4096 or 8192");
+  if (act_format != 0 && act_format != 1)
+    return fail("miso_attn_q4k_gemv", "act_format must be 0 (int8) or 1 (fp16)");
+  const k::Q4kGemvParams p{w, x, y, n_rows};
+  const hipStream_t st = as_stream(stream);
+  if (act_format == 1) {
+    if (k == 2048) launch_q4k<k::ActFormat::Fp16, 2048>(p, st);
+    else if (k == 4096) launch_q4k<k::ActFormat::Fp16, 4096>(p, st);
+    else launch_q4k<k::ActFormat::Fp16, 8192>(p, st);
+  } else {
+    if (k == 2048) launch_q4k<k::ActFormat::Int8, 2048>(p, st);
+    else if (k == 4096) launch_q4k<k::ActFormat::Int8, 4096>(p, st);
+    else launch_q4k<k::ActFormat::Int8, 8192>(p, st);
+  }
+  return launched("miso_attn_q4k_gemv");
 }
 
 }  // extern "C"

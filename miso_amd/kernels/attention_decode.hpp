@@ -351,7 +351,6 @@ __device__ __attribute__((always_inline)) inline void process_unit(
     WaveState& st, const unsigned char* slot, const unsigned (&koff)[4],
     const half2_t (&qh)[4][8], unsigned u0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
     unsigned lane) {
-  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
   // All of the unit's K and V reads first, so their LDS latency overlaps.
   uint4 kr[4][2], vr[4];
 #pragma unroll

@@ -30,6 +30,10 @@
  *                          and oracle_decode_f64 over its dequantized rows (no reference
  *                          function: the reference's cache is f16). The encoder is a search
  *                          for the nearest code, not the kernels' bit arithmetic.
+ *   - oracle_q4k_scale_min / oracle_q4k_dequant: GGUF Q4_K, src/dequant.cpp:45-61,80-84.
+ *   - oracle_q4k_repack_r1: the r1 layout of the GPU GEMV, src/repack.cpp:9-25.
+ *   - oracle_q4k_gemv_f64: y = W x in double over the dequantized rows, the reference of
+ *                          tests/test_q4k_gemv.hip:80-90.
  *
  * Inputs come from a portable generator (splitmix64-seeded xoshiro256**, Box-Muller normals,
  * round-to-nearest-even binary16), so GPU tests and this oracle see bit-identical inputs on any
@@ -590,4 +594,76 @@ void oracle_decode_fp8_f64(const float* q, const float* qg, const uint8_t* k8, c
                            double* out, int threads) {
   decode_fp8_ctx_t c = {q, qg, k8, v8, ks, vs, len, max_ctx, out};
   parallel_rows(decode_fp8_row, &c, KQ, threads);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Q4_K weights of the attention's projections (row f4: attn_q / attn_k / attn_output).       */
+/* GGUF Q4_K block (144 bytes): f16 d, f16 dmin, 12 bytes of packed 6-bit (scale, min) pairs  */
+/* for 8 sub-blocks of 32, 128 bytes of nibbles (sub-block 2g: low nibbles of bytes 32g..+31, */
+/* 2g + 1: their high nibbles). w = d sc q - dmin m.                                            */
+/* ------------------------------------------------------------------------------------------ */
+
+static float f16_at(const uint8_t* p) { return oracle_f16_to_f32((uint16_t)(p[0] | p[1] << 8)); }
+
+/* 6-bit scale and min of sub-block j, src/dequant.cpp:80-84. */
+void oracle_q4k_scale_min(const uint8_t* block, int j, uint8_t* sc, uint8_t* m) {
+  const uint8_t* s = block + 4;
+  if (j < 4) {
+    *sc = s[j] & 63;
+    *m = s[j + 4] & 63;
+  } else {
+    *sc = (uint8_t)((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4));
+    *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+  }
+}
+
+/* Dequantize n_blocks GGUF Q4_K blocks to 256 floats each, in f32 as src/dequant.cpp:45-61
+ * (dj = d sc, mj = dmin m, y = dj q - mj). ds (optional): d sc of each element's sub-block. */
+void oracle_q4k_dequant(const uint8_t* blocks, size_t n_blocks, float* out, float* ds) {
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t* blk = blocks + b * 144;
+    const float d = f16_at(blk), dmin = f16_at(blk + 2);
+    for (int j = 0; j < 8; ++j) {
+      uint8_t sc, m;
+      oracle_q4k_scale_min(blk, j, &sc, &m);
+      const float dj = d * (float)sc, mj = dmin * (float)m;
+      const uint8_t* q = blk + 16 + 32 * (j / 2);
+      for (int l = 0; l < 32; ++l) {
+        const int v = (q[l] >> (4 * (j % 2))) & 15;
+        out[b * 256 + 32 * j + l] = dj * (float)v - mj;
+        if (ds) ds[b * 256 + 32 * j + l] = dj;
+      }
+    }
+  }
+}
+
+/* GGUF -> r1 (src/repack.cpp:9-25): bytes 4..15 become, per nibble group g, the 24-bit
+ * little-endian value sc[2g] | m[2g] << 6 | sc[2g+1] << 12 | m[2g+1] << 18 at byte 4 + 3 g. */
+void oracle_q4k_repack_r1(const uint8_t* src, size_t n_blocks, uint8_t* dst) {
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t* s = src + b * 144;
+    uint8_t* d = dst + b * 144;
+    memcpy(d, s, 144);
+    for (int g = 0; g < 4; ++g) {
+      uint8_t sc0, m0, sc1, m1;
+      oracle_q4k_scale_min(s, 2 * g, &sc0, &m0);
+      oracle_q4k_scale_min(s, 2 * g + 1, &sc1, &m1);
+      const uint32_t v = (uint32_t)sc0 | (uint32_t)m0 << 6 | (uint32_t)sc1 << 12 | (uint32_t)m1 << 18;
+      for (int i = 0; i < 3; ++i) d[4 + 3 * g + i] = (uint8_t)(v >> (8 * i));
+    }
+  }
+}
+
+/* y = W x in double over the f32-dequantized GGUF rows (n_rows rows of k / 256 blocks), as the
+ * reference's GEMV tests form their reference (tests/test_q4k_gemv.hip:80-90). */
+void oracle_q4k_gemv_f64(const uint8_t* blocks, const float* x, uint32_t n_rows, uint32_t k,
+                         double* y) {
+  float* w = (float*)malloc(sizeof(float) * k);
+  for (uint32_t r = 0; r < n_rows; ++r) {
+    oracle_q4k_dequant(blocks + (size_t)r * (k / 256) * 144, k / 256, w, NULL);
+    double acc = 0;
+    for (uint32_t i = 0; i < k; ++i) acc += (double)w[i] * (double)x[i];
+    y[r] = acc;
+  }
+  free(w);
 }

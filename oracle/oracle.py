@@ -60,6 +60,9 @@ def lib() -> ctypes.CDLL:
             "oracle_e4m3_encode": (ctypes.c_uint8, [c_float]),
             "oracle_fp8_encode_rows": (None, [V, ctypes.c_size_t, V, V]),
             "oracle_decode_fp8_f64": (None, [V, V, V, V, V, V, c_uint32, c_uint32, V, c_int]),
+            "oracle_q4k_dequant": (None, [V, ctypes.c_size_t, V, V]),
+            "oracle_q4k_repack_r1": (None, [V, ctypes.c_size_t, V]),
+            "oracle_q4k_gemv_f64": (None, [V, V, c_uint32, c_uint32, V]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -238,6 +241,55 @@ def decode_fp8_f64(q, qg, k8, v8, ks, vs, length: int, max_ctx: int,
     lib().oracle_decode_fp8_f64(_ptr(q), _ptr(qg), _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs),
                                 length, max_ctx, _ptr(out), threads or default_threads())
     return out
+
+
+# ------------------------------------------------------------------------------------------------
+# Q4_K projection weights (GGUF blocks of 144 bytes per 256 weights)
+# ------------------------------------------------------------------------------------------------
+
+def q4k_dequant(blocks) -> tuple[np.ndarray, np.ndarray]:
+    """GGUF Q4_K blocks -> (f32 weights, d * sc of each weight's sub-block)."""
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    nb = blocks.size // 144
+    w = np.empty(nb * 256, np.float32)
+    ds = np.empty(nb * 256, np.float32)
+    lib().oracle_q4k_dequant(_ptr(blocks), nb, _ptr(w), _ptr(ds))
+    return w, ds
+
+
+def q4k_repack_r1(blocks) -> np.ndarray:
+    """GGUF Q4_K blocks -> the r1 layout the GPU GEMV reads."""
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    out = np.empty_like(blocks)
+    lib().oracle_q4k_repack_r1(_ptr(blocks), blocks.size // 144, _ptr(out))
+    return out
+
+
+def q4k_gemv_f64(blocks, x, n_rows: int, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(n_rows, np.float64)
+    lib().oracle_q4k_gemv_f64(_ptr(blocks), _ptr(x), n_rows, k, _ptr(y))
+    return y
+
+
+def q4k_error_bound(w, ds, x, act: str) -> np.ndarray:
+    """Per-row bound on |y_gpu - W x| for f32 dequantized rows w [n][k], the same rule as
+    tests/test_q4k_gemv.hip:60-90: activation conversion error (fp16: 2^-11 |x| + 2^-25; int8:
+    half a step of the per-32 absmax / 127 grid) times |W|, the fp16 nibble chain term
+    2^-20 * 15 * d sc |x|, and K * 2^-23 * sum |W x| of f32 accumulation."""
+    w = np.asarray(w, np.float64)
+    x64 = np.asarray(x, np.float64)
+    k = x64.size
+    if act == "fp16":
+        e = np.abs(x64) * 2.0 ** -11 + 2.0 ** -25
+    else:
+        amax = np.abs(x64).reshape(-1, 32).max(axis=1)
+        e = np.repeat(0.5 * amax / 127.0, 32)
+    bound = np.abs(w) @ e + k * 2.0 ** -23 * (np.abs(w) @ np.abs(x64))
+    if act == "fp16":
+        bound += 2.0 ** -20 * 15.0 * (np.asarray(ds, np.float64).reshape(w.shape) @ np.abs(x64))
+    return bound
 
 
 def prefill_f64(q, qg, qg_stride: int, k, v, pos0: int, max_ctx: int, tokens,

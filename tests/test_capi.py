@@ -84,6 +84,11 @@ def test_host_validation_rejects_bad_arguments(lib):
     rejected(dec8(P, P, P, P, P, P, P, P, P, P, 0, 10, 4, N), lib, "len must be")
     rejected(dec8(P, P, P, P, P, P, P, P, P, P, 11, 10, 4, N), lib, "exceeds max_ctx")
     rejected(dec8(P, P, P, P, P, P, P, P, P, P, 5, 10, 0, N), lib, "n_splits")
+    q4k = lib.miso_attn_q4k_gemv
+    for bad_k in (0, 256, 1024, 3072, 16384):
+        rejected(q4k(P, P, P, 8, bad_k, 1, N), lib, "k must be")
+    rejected(q4k(P, P, P, 8, 2048, 2, N), lib, "act_format")
+    assert q4k(N, N, N, 0, 7, 9, N) == 0  # n_rows == 0: no-op
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")
@@ -124,6 +129,10 @@ def test_host_validation_rejects_null_and_misaligned_pointers(lib):
         rejected(lib.miso_attn_decode_fp8(P, P, P, P, s_bad, P, P, P, P, P, 5, 10, 4, N), lib,
                  bad)
     assert lib.miso_attn_kv_encode_fp8(N, N, N, N, N, N, 0, 0, 10, N) == 0  # n == 0: no-op
+    for q in (N, P + 4):
+        rejected(lib.miso_attn_q4k_gemv(q, P, P, 8, 2048, 1, N), lib, bad)
+        rejected(lib.miso_attn_q4k_gemv(P, q, P, 8, 2048, 1, N), lib, bad)
+    rejected(lib.miso_attn_q4k_gemv(P, P, P + 2, 8, 2048, 1, N), lib, bad)
 
 
 def test_python_layer_raises_runtime_error_with_message():
