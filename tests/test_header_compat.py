@@ -1,9 +1,10 @@
 """Drop-in check of the C++ header API (CPU, compile-only): the reference's own callers of the
 attention kernels -- src/engine/attention.hip, tests/test_attn_splitk.hip and
-bench/attention/*.hip -- compile UNCHANGED for gfx950 with this repository's
-miso_amd/kernels ahead of the reference's kernels/ on the include path, and the preprocessor
-really picks this repository's attention headers (while the reference's own rmsnorm.hpp and
-wave.hpp stay reachable in the same translation unit without clashes).
+bench/attention/*.hip -- and of the Q4_K GEMV -- tests/test_q4k_gemv.hip -- compile UNCHANGED
+for gfx950 with this repository's miso_amd/kernels ahead of the reference's kernels/ on the
+include path, and the preprocessor really picks this repository's headers (while the
+reference's own rmsnorm.hpp and wave.hpp stay reachable in the same translation unit without
+clashes).
 
 Runs only where the reference tree and hipcc exist (this container); nothing is copied, objects
 go to a temporary directory.
@@ -20,13 +21,15 @@ ROOT = Path(__file__).resolve().parent.parent
 REF = Path("/root/reference")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
-# (caller, includes the attention kernel headers itself)
+# (caller, the header of ours it includes itself, or None if only through engine headers)
 CALLERS = [
-    ("src/engine/attention.hip", True),
-    ("tests/test_attn_splitk.hip", True),
-    ("bench/attention/bench_combine.hip", True),
-    ("bench/attention/bench_attention.hip", False),  # only through engine/attention.hpp
+    ("src/engine/attention.hip", "attention_decode.hpp"),
+    ("tests/test_attn_splitk.hip", "attention_decode.hpp"),
+    ("bench/attention/bench_combine.hip", "attention_decode.hpp"),
+    ("bench/attention/bench_attention.hip", None),  # only through engine/attention.hpp
+    ("tests/test_q4k_gemv.hip", "q4k_gemv.hpp"),
 ]
+OURS = ("attention_decode.hpp", "attention_prefill.hpp", "q4k_gemv.hpp")
 
 pytestmark = pytest.mark.skipif(not (REF / "kernels").is_dir() or not Path(HIPCC).exists(),
                                 reason="reference tree or hipcc not available")
@@ -41,14 +44,15 @@ def test_reference_caller_compiles_against_our_headers(caller, direct, tmp_path)
            "-I", str(ROOT / "miso_amd" / "kernels"),
            "-I", str(REF / "kernels"), "-I", str(REF / "src"),
            "-isystem", str(REF / "third_party"),
-           '-DMISO_ORNITH_GGUF="/nonexistent.gguf"']
+           '-DMISO_ORNITH_GGUF="/nonexistent.gguf"', '-DMISO_FIXTURE_DIR="/nonexistent"',
+           '-DMISO_GOLDEN_DIR="/nonexistent"']
     res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert res.returncode == 0, res.stderr[-4000:]
     included = [l.lstrip(". ").strip() for l in res.stderr.splitlines() if l.startswith(".")]
     ours = str(ROOT / "miso_amd" / "kernels")
-    for name in ("attention_decode.hpp", "attention_prefill.hpp"):
+    for name in OURS:
         hits = [p for p in included if p.endswith("/" + name)]
-        if hits:  # every resolution of the attention headers is ours
+        if hits:  # every resolution of these headers is ours
             assert all(Path(p).resolve().as_posix().startswith(ours) for p in hits), hits
     if direct:
-        assert any(p.endswith("/attention_decode.hpp") for p in included)
+        assert any(p.endswith("/" + direct) for p in included)
