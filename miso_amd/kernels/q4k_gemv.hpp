@@ -5,7 +5,10 @@
 // engine's model). Source-compatible with miso's kernels/q4k_gemv.hpp: ActFormat, Q4kGemvParams,
 // q4k_gemv_op<A, K, kBlock, kRows>(params, first, count, logical_block, logical_grid) and
 // q4k_gemv_kernel<A, K, kBlock, kRows> keep their names, fields and template parameters, so
-// src/engine/weights.hip and tests/test_q4k_gemv.hip compile unchanged. The body is new.
+// tests/test_q4k_gemv.hip compiles unchanged against it. (src/engine/weights.hip also includes the
+// reference's kernels/qgemm.hpp, which includes the reference's q4k_gemv.hpp from its own
+// directory; this header replaces that one only together with a qgemm.hpp, not provided here.)
+// The body is new.
 //
 // Weights are Q4_K "r1" blocks (src/repack.hpp:14-19): the 144-byte GGUF block with bytes 4..15
 // holding, per nibble group g (sub-blocks 2g, 2g + 1, whose nibbles share bytes 16 + 32g ..
