@@ -25,7 +25,8 @@ Also reported:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
                 and C5 over a pool of 16-row KV pages (the paged entry point); C2 over an fp8
                 (e4m3 rows) KV cache: us per decode step and GB/s of codes + row scales.
-                F4_q4k_gemv: the Q4_K GEMV at the attention's projection shapes (us, GB/s).
+                F4_q4k_gemv / F4_q6k_gemv: the Q4_K and Q6_K GEMVs at the attention's projection
+                shapes (us, GB/s of weights).
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
 Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
@@ -481,11 +482,34 @@ def bench_other(torch, A, args):
     out["F4_q4k_gemv"] = {"workload": "Q4_K r1 GEMV y = W x with f16 activations at the engine's "
                                       "Q4_K attention projections (synthetic blocks, HBM-resident "
                                       "weights)", **gemv}
+    # attn_v is Q6_K (2048 -> 512).
+    k, n = 2048, 512
+    wbytes = n * A.q6k_row_bytes(k)
+    copies = max(2, -(-(512 << 20) // wbytes))
+    wq = torch.randint(0, 256, (copies, n, A.q6k_row_bytes(k)), dtype=torch.uint8, device="cuda",
+                       generator=gen)
+    wq[:, :, k // 256 * 208:] = 0  # d = 0 halves (finite) and the row padding
+    wq[:, :, k // 256 * 208 + 1::2] = 0x1A  # d = 0.0029.. as f16 high bytes (finite)
+    wq = wq.reshape(copies, -1)
+    xg = torch.randn(k, generator=gen, device="cuda")
+    yg = torch.empty(n, device="cuda")
+    g = graph_of(torch, lambda i: A.q6k_gemv(wq[i % copies], xg, yg, n, k), copies)
+    time_replays(torch, g, 1)
+    ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
+    t = ms / (3 * copies)
+    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v (synthetic blocks, "
+                                      "HBM-resident weights)",
+                          "attn_v": {"k": k, "n_rows": n, "weight_bytes": wbytes,
+                                     "us_per_call": round(t * 1e3, 2),
+                                     "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                                     "weight_copies_rotated": copies}}
+    del wq
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
         + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
-                    for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict)))
+                    for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
+        + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us")
     return out
 
 

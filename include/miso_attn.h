@@ -181,6 +181,14 @@ int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, con
 int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
                        int act_format, void* stream);
 
+/* Q6_K GEMV y = W x with f16 activations (row f4: the attention's attn_v projection). Replaces the
+ * launches of q6k_gemv_kernel<K, 256, R> in gemv() (src/engine/weights.hip:270-279,
+ * kernels/q6k_gemv.hpp:85-131). w: n_rows Q6_K r1 rows (src/repack.hpp:25-28; k / 256 x 210
+ * bytes rounded up to 16 per row, 16-byte aligned), x: k floats (16-byte aligned), y: n_rows
+ * floats. n_rows == 0 is a no-op. Rejects k other than 2048, 4096, 8192. */
+int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

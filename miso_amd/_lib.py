@@ -38,6 +38,7 @@ SIGNATURES = {
     "miso_attn_decode_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                      P]),
     "miso_attn_q4k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, c_int, P]),
+    "miso_attn_q6k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, P]),
 }
 
 _lib = None

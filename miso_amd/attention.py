@@ -321,3 +321,17 @@ def q4k_gemv(w, x, y, n_rows: int, k: int, act: str = "fp16", stream=None) -> No
     _need(y, "y", torch.float32, n_rows)
     _lib.check(_lib.load().miso_attn_q4k_gemv(_ptr(w), _ptr(x), _ptr(y), n_rows, k,
                                               1 if act == "fp16" else 0, _stream(stream)))
+
+
+def q6k_row_bytes(k: int) -> int:
+    """Bytes of one Q6_K r1 row of k weights (210 per 256, rounded up to 16)."""
+    return (k // 256 * 210 + 15) // 16 * 16
+
+
+def q6k_gemv(w, x, y, n_rows: int, k: int, stream=None) -> None:
+    """y[:n_rows] = W x for Q6_K r1 rows w (uint8 device tensor), f16 activations."""
+    _need(w, "w", torch.uint8, n_rows * q6k_row_bytes(k))
+    _need(x, "x", torch.float32, k)
+    _need(y, "y", torch.float32, n_rows)
+    _lib.check(_lib.load().miso_attn_q6k_gemv(_ptr(w), _ptr(x), _ptr(y), n_rows, k,
+                                              _stream(stream)))

@@ -13,6 +13,7 @@
 #include "attention_decode_fp8.hpp"
 #include "attention_prefill.hpp"
 #include "q4k_gemv.hpp"
+#include "q6k_gemv.hpp"
 
 namespace k = miso::kernels;
 using k::attn::half_t;
@@ -55,6 +56,23 @@ void launch_q4k(const k::Q4kGemvParams& p, hipStream_t stream) {
     launch_q4k_shape<A, K, 64, 1>(p, stream);
   else
     launch_q4k_shape<A, K, 256, (K == 2048 ? 4 : K == 4096 ? 2 : 1)>(p, stream);
+}
+
+// Q6_K GEMV launch, the same shape rule as the Q4_K one.
+template <unsigned K, int kBlock, int kRows>
+void launch_q6k_shape(const k::Q6kGemvParams& p, hipStream_t stream) {
+  const unsigned per_wg = (kBlock / 64) * kRows;
+  unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
+  grid = grid < 8192u ? grid : 8192u;
+  k::q6k_gemv_kernel<K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
+}
+
+template <unsigned K>
+void launch_q6k(const k::Q6kGemvParams& p, hipStream_t stream) {
+  if (p.n_rows <= 1024)
+    launch_q6k_shape<K, 64, 1>(p, stream);
+  else
+    launch_q6k_shape<K, 256, (K == 2048 ? 4 : K == 4096 ? 2 : 1)>(p, stream);
 }
 
 template <bool kPrepared, int kPipeline>
@@ -369,6 +387,22 @@ int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
     else launch_q4k<k::ActFormat::Int8, 8192>(p, st);
   }
   return launched("miso_attn_q4k_gemv");
+}
+
+int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
+                       void* stream) {
+  if (n_rows == 0)
+    return 0;
+  if (any_bad(w, x) || bad_scalars(y))
+    return fail("miso_attn_q6k_gemv", kBadPtr);
+  if (k != 2048 && k != 4096 && k != 8192)
+    return fail("miso_attn_q6k_gemv", "k must be 2048, 4096 or 8192");
+  const k::Q6kGemvParams p{w, x, y, n_rows};
+  const hipStream_t st = as_stream(stream);
+  if (k == 2048) launch_q6k<2048>(p, st);
+  else if (k == 4096) launch_q6k<4096>(p, st);
+  else launch_q6k<8192>(p, st);
+  return launched("miso_attn_q6k_gemv");
 }
 
 }  // extern "C"

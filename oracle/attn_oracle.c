@@ -34,6 +34,8 @@
  *   - oracle_q4k_repack_r1: the r1 layout of the GPU GEMV, src/repack.cpp:9-25.
  *   - oracle_q4k_gemv_f64: y = W x in double over the dequantized rows, the reference of
  *                          tests/test_q4k_gemv.hip:80-90.
+ *   - oracle_q6k_dequant / oracle_q6k_repack_r1 / oracle_q6k_gemv_f64: the same for Q6_K,
+ *                          src/dequant.cpp:63-75, src/repack.cpp:53-74.
  *
  * Inputs come from a portable generator (splitmix64-seeded xoshiro256**, Box-Muller normals,
  * round-to-nearest-even binary16), so GPU tests and this oracle see bit-identical inputs on any
@@ -661,6 +663,54 @@ void oracle_q4k_gemv_f64(const uint8_t* blocks, const float* x, uint32_t n_rows,
   float* w = (float*)malloc(sizeof(float) * k);
   for (uint32_t r = 0; r < n_rows; ++r) {
     oracle_q4k_dequant(blocks + (size_t)r * (k / 256) * 144, k / 256, w, NULL);
+    double acc = 0;
+    for (uint32_t i = 0; i < k; ++i) acc += (double)w[i] * (double)x[i];
+    y[r] = acc;
+  }
+  free(w);
+}
+
+/* Q6_K (attn_v). GGUF block (210 bytes): ql[128], qh[64], int8 scales[16], f16 d;
+ * element e: q = (ql[64 (e/128) + e%64] >> 4 ((e%128)/64) & 15) | (qh[32 (e/128) + e%32] >>
+ * 2 ((e%128)/32) & 3) << 4, y = (d sc[e/16]) (q - 32) in f32 (src/dequant.cpp:63-75). */
+void oracle_q6k_dequant(const uint8_t* blocks, size_t n_blocks, float* out) {
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t* ql = blocks + b * 210;
+    const uint8_t* qh = ql + 128;
+    const int8_t* sc = (const int8_t*)(ql + 192);
+    const float d = f16_at(ql + 208);
+    for (int e = 0; e < 256; ++e) {
+      const int h = e / 128, r = e % 128;
+      const int lo = (ql[h * 64 + r % 64] >> (4 * (r / 64))) & 15;
+      const int hi = (qh[h * 32 + r % 32] >> (2 * (r / 32))) & 3;
+      const float ds = d * (float)sc[e / 16];
+      out[b * 256 + e] = ds * (float)((lo | hi << 4) - 32);
+    }
+  }
+}
+
+/* GGUF rows -> r1 rows (src/repack.cpp:53-74): per row [ql nb x 128][qh nb x 64][scales nb x 16]
+ * [d nb x 2], zero-padded to a multiple of 16 bytes. */
+void oracle_q6k_repack_r1(const uint8_t* src, uint32_t n_rows, uint32_t k, uint8_t* dst) {
+  const size_t nb = k / 256, src_row = nb * 210, dst_row = (nb * 210 + 15) / 16 * 16;
+  for (uint32_t r = 0; r < n_rows; ++r) {
+    uint8_t* o = dst + r * dst_row;
+    memset(o, 0, dst_row);
+    for (size_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = src + r * src_row + b * 210;
+      memcpy(o + b * 128, blk, 128);
+      memcpy(o + nb * 128 + b * 64, blk + 128, 64);
+      memcpy(o + nb * 192 + b * 16, blk + 192, 16);
+      memcpy(o + nb * 208 + b * 2, blk + 208, 2);
+    }
+  }
+}
+
+void oracle_q6k_gemv_f64(const uint8_t* blocks, const float* x, uint32_t n_rows, uint32_t k,
+                         double* y) {
+  float* w = (float*)malloc(sizeof(float) * k);
+  for (uint32_t r = 0; r < n_rows; ++r) {
+    oracle_q6k_dequant(blocks + (size_t)r * (k / 256) * 210, k / 256, w);
     double acc = 0;
     for (uint32_t i = 0; i < k; ++i) acc += (double)w[i] * (double)x[i];
     y[r] = acc;

@@ -63,6 +63,9 @@ def lib() -> ctypes.CDLL:
             "oracle_q4k_dequant": (None, [V, ctypes.c_size_t, V, V]),
             "oracle_q4k_repack_r1": (None, [V, ctypes.c_size_t, V]),
             "oracle_q4k_gemv_f64": (None, [V, V, c_uint32, c_uint32, V]),
+            "oracle_q6k_dequant": (None, [V, ctypes.c_size_t, V]),
+            "oracle_q6k_repack_r1": (None, [V, c_uint32, c_uint32, V]),
+            "oracle_q6k_gemv_f64": (None, [V, V, c_uint32, c_uint32, V]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -270,6 +273,29 @@ def q4k_gemv_f64(blocks, x, n_rows: int, k: int) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty(n_rows, np.float64)
     lib().oracle_q4k_gemv_f64(_ptr(blocks), _ptr(x), n_rows, k, _ptr(y))
+    return y
+
+
+def q6k_dequant(blocks) -> np.ndarray:
+    """GGUF Q6_K blocks (210 bytes per 256 weights) -> f32 weights."""
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    w = np.empty(blocks.size // 210 * 256, np.float32)
+    lib().oracle_q6k_dequant(_ptr(blocks), blocks.size // 210, _ptr(w))
+    return w
+
+
+def q6k_repack_r1(blocks, n_rows: int, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    out = np.empty(n_rows * ((k // 256 * 210 + 15) // 16 * 16), np.uint8)
+    lib().oracle_q6k_repack_r1(_ptr(blocks), n_rows, k, _ptr(out))
+    return out
+
+
+def q6k_gemv_f64(blocks, x, n_rows: int, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(n_rows, np.float64)
+    lib().oracle_q6k_gemv_f64(_ptr(blocks), _ptr(x), n_rows, k, _ptr(y))
     return y
 
 

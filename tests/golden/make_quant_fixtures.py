@@ -1,9 +1,10 @@
-"""Writes tests/golden/q4k_tiny.npz from the reference's own test fixtures (data only):
-tests/fixtures/tiny.gguf's Q4_K tensor "q4_k" (its raw GGUF blocks) and tests/fixtures/tiny.q4_k.f32
-(the same tensor dequantized by the reference, the file its tests compare against). Run in a
-container that holds the reference tree:
+"""Writes tests/golden/q4k_tiny.npz and tests/golden/q6k_tiny.npz from the reference's own test
+fixtures (data only): tests/fixtures/tiny.gguf's Q4_K tensor "q4_k" and Q6_K tensor "q6_k" (their
+raw GGUF blocks) and tests/fixtures/tiny.q4_k.f32 / tiny.q6_k.f32 (the same tensors dequantized
+by the reference, the files its tests compare against). Run in a container that holds the
+reference tree:
 
-    python tests/golden/make_q4k_fixture.py [/path/to/reference]
+    python tests/golden/make_quant_fixtures.py [/path/to/reference]
 
 The GGUF container is parsed here (header, key/value pairs, tensor infos, aligned data section);
 no reference code is imported or run.
@@ -80,15 +81,17 @@ def gguf_tensors(path: Path):
 
 def main(ref: Path) -> None:
     fx = ref / "tests" / "fixtures"
-    t, dims, raw = gguf_tensors(fx / "tiny.gguf")["q4_k"]
-    assert t == 12, t  # GGML_TYPE_Q4_K
-    expect = np.fromfile(fx / "tiny.q4_k.f32", dtype="<f4")
-    k, n = int(dims[0]), int(np.prod(dims[1:]))
-    assert expect.size == k * n and len(raw) == k * n // 256 * 144
-    out = Path(__file__).resolve().parent / "q4k_tiny.npz"
-    np.savez_compressed(out, blocks=np.frombuffer(raw, np.uint8), dequant=expect,
-                        k=np.int64(k), n=np.int64(n))
-    print(f"{out}: K={k} N={n}, {len(raw)} bytes of Q4_K blocks")
+    tensors = gguf_tensors(fx / "tiny.gguf")
+    for name, ggml_type, block_bytes in (("q4_k", 12, 144), ("q6_k", 14, 210)):
+        t, dims, raw = tensors[name]
+        assert t == ggml_type, (name, t)
+        expect = np.fromfile(fx / f"tiny.{name}.f32", dtype="<f4")
+        k, n = int(dims[0]), int(np.prod(dims[1:]))
+        assert expect.size == k * n and len(raw) == k * n // 256 * block_bytes
+        out = Path(__file__).resolve().parent / f"{name.replace('_', '')}_tiny.npz"
+        np.savez_compressed(out, blocks=np.frombuffer(raw, np.uint8), dequant=expect,
+                            k=np.int64(k), n=np.int64(n))
+        print(f"{out}: K={k} N={n}, {len(raw)} bytes of {name} blocks")
 
 
 if __name__ == "__main__":

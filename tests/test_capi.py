@@ -89,6 +89,9 @@ def test_host_validation_rejects_bad_arguments(lib):
         rejected(q4k(P, P, P, 8, bad_k, 1, N), lib, "k must be")
     rejected(q4k(P, P, P, 8, 2048, 2, N), lib, "act_format")
     assert q4k(N, N, N, 0, 7, 9, N) == 0  # n_rows == 0: no-op
+    for bad_k in (0, 256, 3072):
+        rejected(lib.miso_attn_q6k_gemv(P, P, P, 8, bad_k, N), lib, "k must be")
+    assert lib.miso_attn_q6k_gemv(N, N, N, 0, 7, N) == 0
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")
@@ -133,6 +136,8 @@ def test_host_validation_rejects_null_and_misaligned_pointers(lib):
         rejected(lib.miso_attn_q4k_gemv(q, P, P, 8, 2048, 1, N), lib, bad)
         rejected(lib.miso_attn_q4k_gemv(P, q, P, 8, 2048, 1, N), lib, bad)
     rejected(lib.miso_attn_q4k_gemv(P, P, P + 2, 8, 2048, 1, N), lib, bad)
+    for q in (N, P + 4):
+        rejected(lib.miso_attn_q6k_gemv(q, P, P, 8, 2048, N), lib, bad)
 
 
 def test_python_layer_raises_runtime_error_with_message():

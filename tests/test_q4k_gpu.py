@@ -1,5 +1,5 @@
-"""Q4_K GEMV (row f4) on MI355X through the C ABI, against the oracle's float64 product over the
-reference-dequantized rows, with the per-row error bound of the reference's own test
+"""Q4_K and Q6_K GEMVs (row f4) on MI355X through the C ABI, against the oracle's float64 product
+over the reference-dequantized rows, with the per-row error bound of the reference's own test
 (tests/test_q4k_gemv.hip:60-113; oracle.q4k_error_bound): |y - W x| <= sum |W| e(x) +
 K 2^-23 sum |W x| (+ the fp16 nibble-chain term). Cases: the reference's fixture (real model
 blocks, K = 8192, N = 2), the engine's attention projections (attn_q 2048 -> 8192, attn_k
@@ -81,3 +81,58 @@ def test_cancelling_activation(O, attn, torch_mod):
     x[1::2] = np.abs(x[1::2])
     for act in ("fp16", "int8"):
         check(O, attn, torch_mod, blocks, x, n, k, act, "cancel")
+
+
+# ------------------------------------------------------------------------------------------------
+# Q6_K (attn_v): the same bound with d sc replaced by d |sc| and codes q - 32 (|q - 32| <= 32):
+# activation error times |W|, K 2^-23 sum |W x| of accumulation, and the f16 chain term
+# 2^-20 * 63 * d |sc| |x| (codes up to 63 accumulate in 16-element chains before scaling).
+# ------------------------------------------------------------------------------------------------
+
+Q6K_GOLDEN = Path(__file__).resolve().parent / "golden" / "q6k_tiny.npz"
+
+
+def random_q6k_blocks(rng, n_rows, k):
+    nb = n_rows * k // 256
+    b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    d = (rng.random(nb) * 0.004 + 1e-4).astype(np.float16)
+    b[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
+def q6k_check(O, attn, torch, blocks, x, n, k, name):
+    r1 = O.q6k_repack_r1(blocks, n, k)
+    y = torch.full((n + 64,), CANARY, dtype=torch.float32, device="cuda")
+    attn.q6k_gemv(to_dev(torch, r1), to_dev(torch, x.astype(np.float32)), y, n, k)
+    torch.cuda.synchronize()
+    out = to_host(y)
+    assert (out[n:] == CANARY).all(), "write past n_rows"
+    got = out[:n].astype(np.float64)
+    ref = O.q6k_gemv_f64(blocks, x, n, k)
+    w = O.q6k_dequant(blocks).reshape(n, k).astype(np.float64)
+    nb = k // 256
+    blk = blocks.reshape(n * nb, 210)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float64).reshape(-1)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float64)
+    dsc = np.repeat(np.abs(d[:, None] * sc), 16, axis=1).reshape(n, k)
+    x64 = x.astype(np.float64)
+    e = np.abs(x64) * 2.0 ** -11 + 2.0 ** -25
+    bound = (np.abs(w) @ e + k * 2.0 ** -23 * (np.abs(w) @ np.abs(x64))
+             + 2.0 ** -20 * 63.0 * (dsc @ np.abs(x64)))
+    ratio = np.abs(got - ref) / bound
+    print(f"[q6k {name}] N={n} K={k} max err/bound {ratio.max():.3f}", flush=True)
+    assert np.isfinite(got).all() and (ratio <= 1.0).all(), int(ratio.argmax())
+
+
+def test_q6k_reference_fixture(O, attn, torch_mod):
+    g = np.load(Q6K_GOLDEN)
+    k, n = int(g["k"]), int(g["n"])
+    x = np.random.default_rng(9).standard_normal(k).astype(np.float32) * 1.5
+    q6k_check(O, attn, torch_mod, g["blocks"], x, n, k, "fixture")
+
+
+@pytest.mark.parametrize("k,n", [(2048, 512), (2048, 8192), (4096, 1001), (8192, 37)])
+def test_q6k_shapes(O, attn, torch_mod, k, n):
+    rng = np.random.default_rng(3 * k + n)
+    q6k_check(O, attn, torch_mod, random_q6k_blocks(rng, n, k),
+              rng.standard_normal(k).astype(np.float32), n, k, "random")

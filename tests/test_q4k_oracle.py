@@ -1,6 +1,7 @@
-"""CPU pins of the oracle's Q4_K functions (oracle/attn_oracle.c: oracle_q4k_*), which restate the
-reference's GGUF Q4_K dequantization (src/dequant.cpp:45-61,80-84), its r1 repack
-(src/repack.cpp:9-25) and its GEMV reference (tests/test_q4k_gemv.hip:80-90):
+"""CPU pins of the oracle's Q4_K and Q6_K functions (oracle/attn_oracle.c: oracle_q4k_*,
+oracle_q6k_*), which restate the reference's GGUF dequantization (src/dequant.cpp:45-75,80-84),
+its r1 repacks (src/repack.cpp:9-25,53-74) and its GEMV reference (tests/test_q4k_gemv.hip:80-90);
+Q6_K below the Q4_K tests, with the same kinds of pins:
 
   * dequant: bit-identical to the reference's own dequantized fixture (tests/fixtures/
     tiny.q4_k.f32, K = 8192, N = 2, real model blocks; tests/golden/q4k_tiny.npz);
@@ -92,5 +93,42 @@ def test_gemv_equals_float64_product():
     x = np.random.default_rng(7).standard_normal(k).astype(np.float32) * 1.5
     w, _ = O.q4k_dequant(g["blocks"])
     y = O.q4k_gemv_f64(g["blocks"], x, n, k)
+    np.testing.assert_allclose(y, w.reshape(n, k).astype(np.float64) @ x.astype(np.float64),
+                               rtol=1e-12)
+
+
+Q6K_GOLDEN = Path(__file__).resolve().parent / "golden" / "q6k_tiny.npz"
+
+
+def test_q6k_dequant_matches_reference_fixture():
+    """oracle_q6k_dequant (src/dequant.cpp:63-75) against the reference's dequantized fixture
+    tests/fixtures/tiny.q6_k.f32 (K = 4096, N = 4)."""
+    g = np.load(Q6K_GOLDEN)
+    w = O.q6k_dequant(g["blocks"])
+    assert np.array_equal(w.view(np.uint32), g["dequant"].astype(np.float32).view(np.uint32))
+
+
+def test_q6k_repack_r1_sections():
+    """r1 rows: per row the ql, qh, scale and d sections of its blocks in order, then zeros."""
+    g = np.load(Q6K_GOLDEN)
+    k, n = int(g["k"]), int(g["n"])
+    nb = k // 256
+    src = g["blocks"].reshape(n, nb, 210)
+    r1 = O.q6k_repack_r1(g["blocks"], n, k).reshape(n, -1)
+    assert r1.shape[1] == (nb * 210 + 15) // 16 * 16
+    for r in range(n):
+        assert np.array_equal(r1[r, :nb * 128], src[r, :, :128].reshape(-1))
+        assert np.array_equal(r1[r, nb * 128:nb * 192], src[r, :, 128:192].reshape(-1))
+        assert np.array_equal(r1[r, nb * 192:nb * 208], src[r, :, 192:208].reshape(-1))
+        assert np.array_equal(r1[r, nb * 208:nb * 210], src[r, :, 208:210].reshape(-1))
+        assert not r1[r, nb * 210:].any()
+
+
+def test_q6k_gemv_equals_float64_product():
+    g = np.load(Q6K_GOLDEN)
+    k, n = int(g["k"]), int(g["n"])
+    x = np.random.default_rng(8).standard_normal(k).astype(np.float32)
+    w = O.q6k_dequant(g["blocks"])
+    y = O.q6k_gemv_f64(g["blocks"], x, n, k)
     np.testing.assert_allclose(y, w.reshape(n, k).astype(np.float64) @ x.astype(np.float64),
                                rtol=1e-12)
