@@ -503,13 +503,35 @@ def bench_other(torch, A, args):
                                      "us_per_call": round(t * 1e3, 2),
                                      "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
                                      "weight_copies_rotated": copies}}
-    del wq
+    # attn_q + attn_v in one launch (the engine's gemv_pair), same weights sizes.
+    w4b = 8192 * 2048 // 256 * 144
+    w6b = 512 * A.q6k_row_bytes(2048)
+    copies = max(2, -(-(512 << 20) // (w4b + w6b)))
+    w4 = torch.randint(0, 256, (copies, w4b), dtype=torch.uint8, device="cuda", generator=gen)
+    w4.view(copies, -1, 144)[:, :, 0:4] = torch.tensor([0x1F, 0x1E, 0x0F, 0x1A], dtype=torch.uint8,
+                                                        device="cuda")
+    w6 = torch.randint(0, 256, (copies, 512, A.q6k_row_bytes(2048)), dtype=torch.uint8,
+                       device="cuda", generator=gen)
+    w6[:, :, 8 * 208:] = 0
+    w6[:, :, 8 * 208 + 1::2] = 0x1A
+    w6 = w6.reshape(copies, -1)
+    y4, y6 = torch.empty(8192, device="cuda"), torch.empty(512, device="cuda")
+    g = graph_of(torch, lambda i: A.q4k_q6k_gemv_pair(w4[i % copies], 8192, y4, w6[i % copies], 512,
+                                                      y6, xg), copies)
+    time_replays(torch, g, 1)
+    ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
+    t = ms / (3 * copies)
+    out["F4_q6k_gemv"]["attn_q_plus_attn_v_pair"] = {
+        "us_per_call": round(t * 1e3, 2), "weight_bytes": w4b + w6b,
+        "gbs": round((w4b + w6b) / (t * 1e-3) / 1e9, 1), "weight_copies_rotated": copies}
+    del w4, w6
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
         + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
                     for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
-        + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us")
+        + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "
+        f"{out['F4_q6k_gemv']['attn_q_plus_attn_v_pair']['us_per_call']} us")
     return out
 
 

@@ -189,6 +189,14 @@ int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
 int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,
                        void* stream);
 
+/* The attention's q (Q4_K, f16 activations) and v (Q6_K) projections of one activation vector in
+ * one launch, K = 2048. Replaces the mixed_gemv_kernel launch of gemv_pair()
+ * (src/engine/weights.hip:286-307, kernels/mixed_gemv.hpp:12-30). w4: n4 Q4_K r1 rows -> y4;
+ * w6: n6 Q6_K r1 rows -> y6; x: 2048 floats. Outputs are bit-identical to miso_attn_q4k_gemv
+ * (act_format 1) and miso_attn_q6k_gemv on the same rows. Rejects n4 == 0 or n6 == 0. */
+int miso_attn_q4k_q6k_gemv_pair(const uint8_t* w4, uint32_t n4, float* y4, const uint8_t* w6,
+                                uint32_t n6, float* y6, const float* x, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

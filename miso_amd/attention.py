@@ -335,3 +335,16 @@ def q6k_gemv(w, x, y, n_rows: int, k: int, stream=None) -> None:
     _need(y, "y", torch.float32, n_rows)
     _lib.check(_lib.load().miso_attn_q6k_gemv(_ptr(w), _ptr(x), _ptr(y), n_rows, k,
                                               _stream(stream)))
+
+
+def q4k_q6k_gemv_pair(w4, n4: int, y4, w6, n6: int, y6, x, stream=None) -> None:
+    """The attention's q (Q4_K, f16 activations) and v (Q6_K) projections of x (2048 floats) in
+    one launch; bit-identical to q4k_gemv(..., act="fp16") and q6k_gemv on the same rows."""
+    k = 2048
+    _need(w4, "w4", torch.uint8, n4 * k // 256 * 144)
+    _need(w6, "w6", torch.uint8, n6 * q6k_row_bytes(k))
+    _need(x, "x", torch.float32, k)
+    _need(y4, "y4", torch.float32, n4)
+    _need(y6, "y6", torch.float32, n6)
+    _lib.check(_lib.load().miso_attn_q4k_q6k_gemv_pair(_ptr(w4), n4, _ptr(y4), _ptr(w6), n6,
+                                                       _ptr(y6), _ptr(x), _stream(stream)))

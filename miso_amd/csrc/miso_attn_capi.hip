@@ -14,6 +14,7 @@
 #include "attention_prefill.hpp"
 #include "q4k_gemv.hpp"
 #include "q6k_gemv.hpp"
+#include "mixed_gemv.hpp"
 
 namespace k = miso::kernels;
 using k::attn::half_t;
@@ -403,6 +404,22 @@ int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
   else if (k == 4096) launch_q6k<4096>(p, st);
   else launch_q6k<8192>(p, st);
   return launched("miso_attn_q6k_gemv");
+}
+
+int miso_attn_q4k_q6k_gemv_pair(const uint8_t* w4, uint32_t n4, float* y4, const uint8_t* w6,
+                                uint32_t n6, float* y6, const float* x, void* stream) {
+  if (any_bad(w4, w6, x) || bad_scalars(y4) || bad_scalars(y6))
+    return fail("miso_attn_q4k_q6k_gemv_pair", kBadPtr);
+  if (n4 == 0 || n6 == 0)
+    return fail("miso_attn_q4k_q6k_gemv_pair", "both row counts must be >= 1");
+  // Logical grids sized for the attention's attn_q (8192 rows, 16 per Q4_K workgroup) and attn_v
+  // (512 rows, 4 per Q6_K workgroup); other row counts grid-stride.
+  constexpr unsigned kQ6Grid = 128, kQ4Grid = 512;
+  const k::Q6kGemvParams p6{w6, x, y6, n6};
+  const k::Q4kGemvParams p4{w4, x, y4, n4};
+  k::mixed_gemv_kernel<1, kQ6Grid, kQ4Grid, 256>
+      <<<kQ6Grid + kQ4Grid, 256, 0, as_stream(stream)>>>(p6, p4);
+  return launched("miso_attn_q4k_q6k_gemv_pair");
 }
 
 }  // extern "C"

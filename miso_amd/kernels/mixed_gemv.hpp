@@ -1,0 +1,41 @@
+#pragma once
+
+// Two independent projections of one activation vector in one launch: a Q6_K GEMV (attn_v) and a
+// Q4_K GEMV with f16 activations (attn_q), K = 2048 -- the engine's gemv_pair
+// (src/engine/weights.hip:286-307). Same names and template parameters as miso's
+// kernels/mixed_gemv.hpp: mixed_gemv_op / mixed_gemv_kernel<Q6Rows, Q6Grid, Q4Grid, kBlock>; each
+// operator keeps its own logical grid (Q6Grid / Q4Grid workgroups) and its own per-row arithmetic,
+// so its outputs are bit-identical to its separate launch. The body is new.
+//
+// Workgroup order: stripes of one workgroup of the smaller logical grid followed by
+// (larger / smaller) of the larger, so both kinds are in flight across the whole launch and each
+// hides the other's memory latency.
+
+#include "q4k_gemv.hpp"
+#include "q6k_gemv.hpp"
+
+namespace miso::kernels {
+
+template <int Q6Rows, unsigned Q6Grid, unsigned Q4Grid, int kBlock = 256>
+__device__ void mixed_gemv_op(const Q6kGemvParams& q6, const Q4kGemvParams& q4) {
+  static_assert(Q6Grid > 0 && Q4Grid > 0, "both operators need workgroups");
+  constexpr bool kQ6Larger = Q6Grid >= Q4Grid;
+  constexpr unsigned kLarge = kQ6Larger ? Q6Grid : Q4Grid, kSmall = kQ6Larger ? Q4Grid : Q6Grid;
+  static_assert(kLarge % kSmall == 0, "the larger logical grid is a multiple of the smaller");
+  constexpr unsigned kPer = kLarge / kSmall, kStripe = kPer + 1;
+  const unsigned stripe = blockIdx.x / kStripe, pos = blockIdx.x % kStripe;
+  const bool small = pos == 0;  // uniform across the workgroup
+  const unsigned logical = small ? stripe : stripe * kPer + pos - 1;
+  if (small == kQ6Larger)  // this workgroup runs the Q4_K operator
+    q4k_gemv_op<ActFormat::Fp16, 2048, kBlock, 4>(q4, 0, q4.n_rows, logical, Q4Grid);
+  else
+    q6k_gemv_op<2048, kBlock, Q6Rows>(q6, 0, q6.n_rows, logical, Q6Grid);
+}
+
+// Grid: Q6Grid + Q4Grid workgroups of kBlock threads.
+template <int Q6Rows, unsigned Q6Grid, unsigned Q4Grid, int kBlock = 256>
+__global__ void __launch_bounds__(kBlock) mixed_gemv_kernel(Q6kGemvParams q6, Q4kGemvParams q4) {
+  mixed_gemv_op<Q6Rows, Q6Grid, Q4Grid, kBlock>(q6, q4);
+}
+
+}  // namespace miso::kernels

@@ -92,6 +92,10 @@ def test_host_validation_rejects_bad_arguments(lib):
     for bad_k in (0, 256, 3072):
         rejected(lib.miso_attn_q6k_gemv(P, P, P, 8, bad_k, N), lib, "k must be")
     assert lib.miso_attn_q6k_gemv(N, N, N, 0, 7, N) == 0
+    pair = lib.miso_attn_q4k_q6k_gemv_pair
+    rejected(pair(P, 0, P, P, 5, P, P, N), lib, "row counts")
+    rejected(pair(P, 5, P, P, 0, P, P, N), lib, "row counts")
+    rejected(pair(P + 4, 5, P, P, 5, P, P, N), lib, "NULL or not 16-byte aligned")
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")

@@ -29,8 +29,10 @@ CALLERS = [
     ("bench/attention/bench_attention.hip", None),  # only through engine/attention.hpp
     ("tests/test_q4k_gemv.hip", "q4k_gemv.hpp"),
     ("tests/test_q6k_gemv.hip", "q6k_gemv.hpp"),
+    ("tests/test_gemv_dispatch.hip", "mixed_gemv.hpp"),
 ]
-OURS = ("attention_decode.hpp", "attention_prefill.hpp", "q4k_gemv.hpp", "q6k_gemv.hpp")
+OURS = ("attention_decode.hpp", "attention_prefill.hpp", "q4k_gemv.hpp", "q6k_gemv.hpp",
+        "mixed_gemv.hpp")
 
 pytestmark = pytest.mark.skipif(not (REF / "kernels").is_dir() or not Path(HIPCC).exists(),
                                 reason="reference tree or hipcc not available")

@@ -136,3 +136,27 @@ def test_q6k_shapes(O, attn, torch_mod, k, n):
     rng = np.random.default_rng(3 * k + n)
     q6k_check(O, attn, torch_mod, random_q6k_blocks(rng, n, k),
               rng.standard_normal(k).astype(np.float32), n, k, "random")
+
+
+@pytest.mark.parametrize("n4,n6", [(8192, 512), (1001, 37), (16, 3000)])
+def test_pair_matches_separate_launches(O, attn, torch_mod, n4, n6):
+    """One mixed launch (attn_q Q4_K + attn_v Q6_K, K = 2048) equals the two separate launches
+    bit for bit, and both outputs stay inside their oracle bounds (checked by the separate
+    tests on the same kernels)."""
+    torch = torch_mod
+    k = 2048
+    rng = np.random.default_rng(n4 + 7 * n6)
+    b4, b6 = random_blocks(rng, n4, k), random_q6k_blocks(rng, n6, k)
+    x = to_dev(torch, rng.standard_normal(k).astype(np.float32))
+    w4, w6 = to_dev(torch, O.q4k_repack_r1(b4)), to_dev(torch, O.q6k_repack_r1(b6, n6, k))
+    y4 = torch.full((n4 + 64,), CANARY, device="cuda")
+    y6 = torch.full((n6 + 64,), CANARY, device="cuda")
+    s4, s6 = torch.empty(n4, device="cuda"), torch.empty(n6, device="cuda")
+    attn.q4k_q6k_gemv_pair(w4, n4, y4, w6, n6, y6, x)
+    attn.q4k_gemv(w4, x, s4, n4, k, "fp16")
+    attn.q6k_gemv(w6, x, s6, n6, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y4[:n4], s4) and torch.equal(y6[:n6], s6)
+    assert (to_host(y4)[n4:] == CANARY).all() and (to_host(y6)[n6:] == CANARY).all()
+    ref = O.q4k_gemv_f64(b4, to_host(x), n4, k)
+    assert np.abs(to_host(s4) - ref).max() <= 1e-3 * np.abs(ref).max() + 1e-3
