@@ -340,6 +340,27 @@ def bench_prefill(torch, A, args):
             "max_ctx": max_ctx, "host": host}
 
 
+def synthetic_q4k(torch, gen, copies, n, k):
+    """copies x n rows of random Q4_K r1 blocks (uint8 [copies][n k / 256 x 144]) whose f16 d and
+    dmin (bytes 0..3 of each block) are finite: d = 0.00598, dmin = 0.00296."""
+    w = torch.randint(0, 256, (copies, n * k // 256 * 144), dtype=torch.uint8, device="cuda",
+                      generator=gen)
+    w.view(copies, -1, 144)[:, :, 0:4] = torch.tensor([0x1F, 0x1E, 0x0F, 0x1A], dtype=torch.uint8,
+                                                      device="cuda")
+    return w
+
+
+def synthetic_q6k(torch, gen, copies, n, k):
+    """copies x n random Q6_K r1 rows ([ql][qh][scales][d][padding] per row) with every d finite
+    (0x1A00 = 0.00293) and the padding zero."""
+    nb = k // 256
+    row = (nb * 210 + 15) // 16 * 16
+    w = torch.randint(0, 256, (copies, n, row), dtype=torch.uint8, device="cuda", generator=gen)
+    w[:, :, nb * 208:] = 0
+    w[:, :, nb * 208 + 1:nb * 210:2] = 0x1A  # the high byte of each f16 d
+    return w.reshape(copies, -1)
+
+
 def bench_other(torch, A, args):
     """C1, C3 and C5 of the survey's configuration table (synthetic N(0,1) inputs)."""
     import numpy as np
@@ -458,73 +479,55 @@ def bench_other(torch, A, args):
                      "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
                      "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del caches8
-    # Q4_K GEMV of the attention's projections (row f4), f16 activations as the engine: weights
-    # rotated over >= 512 MB of copies so they stream from HBM as a model's layers do.
+    # The projection GEMVs (row f4), f16 activations as the engine; weights rotated over >= 512 MB
+    # of copies so they stream from HBM as a model's layers do.
+    def rotated(nbytes):
+        return max(2, -(-(512 << 20) // nbytes))
+
+    def timed(fn, copies):
+        g = graph_of(torch, fn, copies)
+        time_replays(torch, g, 1)
+        return sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / (3 * copies)
+
+    def line(wbytes, t, copies, **extra):
+        return {**extra, "weight_bytes": wbytes, "us_per_call": round(t * 1e3, 2),
+                "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                "frac": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "weight_copies_rotated": copies}
+
+    x2048 = torch.randn(2048, generator=gen, device="cuda")
+    x4096 = torch.randn(4096, generator=gen, device="cuda")
     gemv = {}
     for name, k, n in (("attn_q", 2048, 8192), ("attn_k", 2048, 512), ("attn_output", 4096, 2048)):
         wbytes = n * k // 256 * 144
-        copies = max(2, -(-(512 << 20) // wbytes))
-        wq = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device="cuda", generator=gen)
-        # finite f16 d / dmin in every block (bytes 0..3)
-        blk = wq.view(copies, -1, 144)
-        blk[:, :, 0:4] = torch.tensor([0x1F, 0x1E, 0x0F, 0x1A], dtype=torch.uint8, device="cuda")
-        xg = torch.randn(k, generator=gen, device="cuda")
+        copies = rotated(wbytes)
+        wq = synthetic_q4k(torch, gen, copies, n, k)
         yg = torch.empty(n, device="cuda")
-        g = graph_of(torch, lambda i: A.q4k_gemv(wq[i % copies], xg, yg, n, k), copies)
-        time_replays(torch, g, 1)
-        ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
-        t = ms / (3 * copies)
-        gemv[name] = {"k": k, "n_rows": n, "weight_bytes": wbytes, "us_per_call": round(t * 1e3, 2),
-                      "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
-                      "frac": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                      "weight_copies_rotated": copies}
-        del wq, blk
+        xg = x2048 if k == 2048 else x4096
+        t = timed(lambda i: A.q4k_gemv(wq[i % copies], xg, yg, n, k), copies)
+        gemv[name] = line(wbytes, t, copies, k=k, n_rows=n)
+        del wq
     out["F4_q4k_gemv"] = {"workload": "Q4_K r1 GEMV y = W x with f16 activations at the engine's "
                                       "Q4_K attention projections (synthetic blocks, HBM-resident "
                                       "weights)", **gemv}
-    # attn_v is Q6_K (2048 -> 512).
-    k, n = 2048, 512
-    wbytes = n * A.q6k_row_bytes(k)
-    copies = max(2, -(-(512 << 20) // wbytes))
-    wq = torch.randint(0, 256, (copies, n, A.q6k_row_bytes(k)), dtype=torch.uint8, device="cuda",
-                       generator=gen)
-    wq[:, :, k // 256 * 208:] = 0  # d = 0 halves (finite) and the row padding
-    wq[:, :, k // 256 * 208 + 1::2] = 0x1A  # d = 0.0029.. as f16 high bytes (finite)
-    wq = wq.reshape(copies, -1)
-    xg = torch.randn(k, generator=gen, device="cuda")
-    yg = torch.empty(n, device="cuda")
-    g = graph_of(torch, lambda i: A.q6k_gemv(wq[i % copies], xg, yg, n, k), copies)
-    time_replays(torch, g, 1)
-    ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
-    t = ms / (3 * copies)
-    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v (synthetic blocks, "
-                                      "HBM-resident weights)",
-                          "attn_v": {"k": k, "n_rows": n, "weight_bytes": wbytes,
-                                     "us_per_call": round(t * 1e3, 2),
-                                     "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
-                                     "weight_copies_rotated": copies}}
-    # attn_q + attn_v in one launch (the engine's gemv_pair), same weights sizes.
-    w4b = 8192 * 2048 // 256 * 144
-    w6b = 512 * A.q6k_row_bytes(2048)
-    copies = max(2, -(-(512 << 20) // (w4b + w6b)))
-    w4 = torch.randint(0, 256, (copies, w4b), dtype=torch.uint8, device="cuda", generator=gen)
-    w4.view(copies, -1, 144)[:, :, 0:4] = torch.tensor([0x1F, 0x1E, 0x0F, 0x1A], dtype=torch.uint8,
-                                                        device="cuda")
-    w6 = torch.randint(0, 256, (copies, 512, A.q6k_row_bytes(2048)), dtype=torch.uint8,
-                       device="cuda", generator=gen)
-    w6[:, :, 8 * 208:] = 0
-    w6[:, :, 8 * 208 + 1::2] = 0x1A
-    w6 = w6.reshape(copies, -1)
-    y4, y6 = torch.empty(8192, device="cuda"), torch.empty(512, device="cuda")
-    g = graph_of(torch, lambda i: A.q4k_q6k_gemv_pair(w4[i % copies], 8192, y4, w6[i % copies], 512,
-                                                      y6, xg), copies)
-    time_replays(torch, g, 1)
-    ms = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1]
-    t = ms / (3 * copies)
-    out["F4_q6k_gemv"]["attn_q_plus_attn_v_pair"] = {
-        "us_per_call": round(t * 1e3, 2), "weight_bytes": w4b + w6b,
-        "gbs": round((w4b + w6b) / (t * 1e-3) / 1e9, 1), "weight_copies_rotated": copies}
+    # attn_v is Q6_K (2048 -> 512); the engine's gemv_pair runs it with attn_q in one launch.
+    w6b, w4b = 512 * A.q6k_row_bytes(2048), 8192 * 2048 // 256 * 144
+    copies = rotated(w6b)
+    w6 = synthetic_q6k(torch, gen, copies, 512, 2048)
+    y6 = torch.empty(512, device="cuda")
+    t6 = timed(lambda i: A.q6k_gemv(w6[i % copies], x2048, y6, 512, 2048), copies)
+    del w6
+    copies_p = rotated(w4b + w6b)
+    w4 = synthetic_q4k(torch, gen, copies_p, 8192, 2048)
+    w6 = synthetic_q6k(torch, gen, copies_p, 512, 2048)
+    y4 = torch.empty(8192, device="cuda")
+    tp = timed(lambda i: A.q4k_q6k_gemv_pair(w4[i % copies_p], 8192, y4, w6[i % copies_p], 512, y6,
+                                             x2048), copies_p)
     del w4, w6
+    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired with "
+                                      "attn_q in one launch (synthetic blocks, HBM-resident weights)",
+                          "attn_v": line(w6b, t6, copies, k=2048, n_rows=512),
+                          "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p)}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
