@@ -240,6 +240,9 @@ def decode_fp8_f64(q, qg, k8, v8, ks, vs, length: int, max_ctx: int,
     v8 = np.ascontiguousarray(v8, np.uint8)
     ks = np.ascontiguousarray(ks, np.float32)
     vs = np.ascontiguousarray(vs, np.float32)
+    rows = KV_HEADS * max_ctx
+    if min(k8.size, v8.size) < rows * DIM or min(ks.size, vs.size) < rows or length > max_ctx:
+        raise ValueError("e4m3 rows / scales smaller than [2][max_ctx] (or length > max_ctx)")
     out = np.empty((Q_HEADS, DIM), dtype=np.float64)
     lib().oracle_decode_fp8_f64(_ptr(q), _ptr(qg), _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs),
                                 length, max_ctx, _ptr(out), threads or default_threads())

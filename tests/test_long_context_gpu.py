@@ -65,3 +65,23 @@ def test_ragged_sequence_far_past_max_len(O, attn, torch_mod):
     st = O.compare(got, ref)
     report("ragged far past max_len", st)
     assert st["ok"], st
+
+
+def test_decode_fp8_full_262k_cache(O, attn, torch_mod):
+    """The fp8 (e4m3 rows) decode over a whole 262,144-token cache, encoded on the GPU from the
+    f16 cache, against the oracle on the same codes and scales."""
+    length = 262144
+    d = O.decode_inputs(33, length, length, q_scale=1.0)
+    torch = torch_mod
+    cache = attn.Fp8Cache(length)
+    attn.attn_kv_encode_fp8(to_dev(torch, d["k"]), to_dev(torch, d["v"]), cache, 0, length)
+    core = torch.full((H * D,), -9123.5, device="cuda")
+    attn.attn_decode_fp8(to_dev(torch, d["q"]), to_dev(torch, d["qg"]), cache, core,
+                         attn.DecodeScratch(128), length)
+    torch.cuda.synchronize()
+    got = to_host(core).reshape(H, D)
+    k8, v8, ks, vs = (to_host(t) for t in cache.buffers())
+    ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs, length, length)
+    st = O.compare(got, ref)
+    report(f"fp8 decode len={length}", st)
+    assert st["ok"], st
