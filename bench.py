@@ -523,18 +523,25 @@ def bench_other(torch, A, args):
     y4 = torch.empty(8192, device="cuda")
     tp = timed(lambda i: A.q4k_q6k_gemv_pair(w4[i % copies_p], 8192, y4, w6[i % copies_p], 512, y6,
                                              x2048), copies_p)
-    del w4, w6
+    wk = synthetic_q4k(torch, gen, copies_p, 512, 2048)
+    yk = torch.empty(512, device="cuda")
+    tq = timed(lambda i: A.qkv_gemv(w4[i % copies_p], 8192, y4, wk[i % copies_p], 512, yk,
+                                    w6[i % copies_p], 512, y6, x2048), copies_p)
+    del w4, w6, wk
     out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired with "
                                       "attn_q in one launch (synthetic blocks, HBM-resident weights)",
                           "attn_v": line(w6b, t6, copies, k=2048, n_rows=512),
-                          "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p)}
+                          "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p),
+                          "attn_q_k_v_one_launch": line(w4b + w6b + 512 * 2048 // 256 * 144, tq,
+                                                        copies_p)}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
         + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
                     for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
         + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "
-        f"{out['F4_q6k_gemv']['attn_q_plus_attn_v_pair']['us_per_call']} us")
+        f"{out['F4_q6k_gemv']['attn_q_plus_attn_v_pair']['us_per_call']} us, q+k+v "
+        f"{out['F4_q6k_gemv']['attn_q_k_v_one_launch']['us_per_call']} us")
     return out
 
 

@@ -197,6 +197,15 @@ int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
 int miso_attn_q4k_q6k_gemv_pair(const uint8_t* w4, uint32_t n4, float* y4, const uint8_t* w6,
                                 uint32_t n6, float* y6, const float* x, void* stream);
 
+/* The attention's three input projections of one activation vector in one launch, K = 2048 (no
+ * reference counterpart: the engine issues gemv_pair(q, v) then gemv(k),
+ * src/engine/attention.hip:87-93). wq: nq Q4_K r1 rows -> yq, wk: nk Q4_K r1 rows -> yk (f16
+ * activations), wv: nv Q6_K r1 rows -> yv; x: 2048 floats. Outputs are bit-identical to
+ * miso_attn_q4k_gemv (act_format 1) and miso_attn_q6k_gemv. Rejects any row count of 0. */
+int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t* wk, uint32_t nk,
+                       float* yk, const uint8_t* wv, uint32_t nv, float* yv, const float* x,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,7 @@ SIGNATURES = {
     "miso_attn_q4k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, c_int, P]),
     "miso_attn_q6k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, P]),
     "miso_attn_q4k_q6k_gemv_pair": (c_int, [P, c_uint32, P, P, c_uint32, P, P, P]),
+    "miso_attn_qkv_gemv": (c_int, [P, c_uint32, P, P, c_uint32, P, P, c_uint32, P, P, P]),
 }
 
 _lib = None

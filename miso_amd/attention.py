@@ -348,3 +348,17 @@ def q4k_q6k_gemv_pair(w4, n4: int, y4, w6, n6: int, y6, x, stream=None) -> None:
     _need(y6, "y6", torch.float32, n6)
     _lib.check(_lib.load().miso_attn_q4k_q6k_gemv_pair(_ptr(w4), n4, _ptr(y4), _ptr(w6), n6,
                                                        _ptr(y6), _ptr(x), _stream(stream)))
+
+
+def qkv_gemv(wq, nq: int, yq, wk, nk: int, yk, wv, nv: int, yv, x, stream=None) -> None:
+    """q and k (Q4_K, f16 activations) and v (Q6_K) projections of x (2048 floats) in one launch;
+    bit-identical to the separate q4k_gemv / q6k_gemv calls."""
+    k = 2048
+    _need(wq, "wq", torch.uint8, nq * k // 256 * 144)
+    _need(wk, "wk", torch.uint8, nk * k // 256 * 144)
+    _need(wv, "wv", torch.uint8, nv * q6k_row_bytes(k))
+    _need(x, "x", torch.float32, k)
+    for name, t, n in (("yq", yq, nq), ("yk", yk, nk), ("yv", yv, nv)):
+        _need(t, name, torch.float32, n)
+    _lib.check(_lib.load().miso_attn_qkv_gemv(_ptr(wq), nq, _ptr(yq), _ptr(wk), nk, _ptr(yk),
+                                              _ptr(wv), nv, _ptr(yv), _ptr(x), _stream(stream)))

@@ -422,4 +422,20 @@ int miso_attn_q4k_q6k_gemv_pair(const uint8_t* w4, uint32_t n4, float* y4, const
   return launched("miso_attn_q4k_q6k_gemv_pair");
 }
 
+int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t* wk, uint32_t nk,
+                       float* yk, const uint8_t* wv, uint32_t nv, float* yv, const float* x,
+                       void* stream) {
+  if (any_bad(wq, wk, wv, x) || bad_scalars(yq) || bad_scalars(yk) || bad_scalars(yv))
+    return fail("miso_attn_qkv_gemv", kBadPtr);
+  if (nq == 0 || nk == 0 || nv == 0)
+    return fail("miso_attn_qkv_gemv", "all three row counts must be >= 1");
+  // Logical grids sized for attn_q (8192 rows) and attn_k (512 rows), 16 rows per Q4_K
+  // workgroup, and attn_v (512 rows), 4 per Q6_K workgroup; other row counts grid-stride.
+  constexpr unsigned kQ = 512, kK = 32, kV = 128;
+  const k::Q4kGemvParams pq{wq, x, yq, nq}, pk{wk, x, yk, nk};
+  const k::Q6kGemvParams pv{wv, x, yv, nv};
+  k::qkv_gemv_kernel<kQ, kK, kV, 256><<<kQ + kK + kV, 256, 0, as_stream(stream)>>>(pq, pk, pv);
+  return launched("miso_attn_qkv_gemv");
+}
+
 }  // extern "C"

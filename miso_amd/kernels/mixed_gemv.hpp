@@ -38,4 +38,22 @@ __global__ void __launch_bounds__(kBlock) mixed_gemv_kernel(Q6kGemvParams q6, Q4
   mixed_gemv_op<Q6Rows, Q6Grid, Q4Grid, kBlock>(q6, q4);
 }
 
+// The attention's three input projections of one activation vector (K = 2048) in one launch: q
+// and k (Q4_K, f16 activations) and v (Q6_K). No reference counterpart: the engine issues
+// gemv_pair(q, v) then gemv(k) (src/engine/attention.hip:87-93). Workgroups [0, kQGrid) run q,
+// the next kKGrid run k, the rest v, each operator on its own logical grid with its separate
+// launch's per-row arithmetic (outputs bit-identical to the separate launches). All of them are
+// resident at once at the engine's sizes, so contiguous ranges overlap fully.
+template <unsigned kQGrid, unsigned kKGrid, unsigned kVGrid, int kBlock = 256>
+__global__ void __launch_bounds__(kBlock) qkv_gemv_kernel(Q4kGemvParams q, Q4kGemvParams k,
+                                                          Q6kGemvParams v) {
+  const unsigned b = blockIdx.x;
+  if (b < kQGrid)
+    q4k_gemv_op<ActFormat::Fp16, 2048, kBlock, 4>(q, 0, q.n_rows, b, kQGrid);
+  else if (b < kQGrid + kKGrid)
+    q4k_gemv_op<ActFormat::Fp16, 2048, kBlock, 4>(k, 0, k.n_rows, b - kQGrid, kKGrid);
+  else
+    q6k_gemv_op<2048, kBlock, 1>(v, 0, v.n_rows, b - kQGrid - kKGrid, kVGrid);
+}
+
 }  // namespace miso::kernels

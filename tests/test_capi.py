@@ -96,6 +96,10 @@ def test_host_validation_rejects_bad_arguments(lib):
     rejected(pair(P, 0, P, P, 5, P, P, N), lib, "row counts")
     rejected(pair(P, 5, P, P, 0, P, P, N), lib, "row counts")
     rejected(pair(P + 4, 5, P, P, 5, P, P, N), lib, "NULL or not 16-byte aligned")
+    qkv = lib.miso_attn_qkv_gemv
+    for nq, nk, nv in ((0, 5, 5), (5, 0, 5), (5, 5, 0)):
+        rejected(qkv(P, nq, P, P, nk, P, P, nv, P, P, N), lib, "row counts")
+    rejected(qkv(P, 5, P, P, 5, P, P + 4, 5, P, P, N), lib, "NULL or not 16-byte aligned")
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")

@@ -160,3 +160,25 @@ def test_pair_matches_separate_launches(O, attn, torch_mod, n4, n6):
     assert (to_host(y4)[n4:] == CANARY).all() and (to_host(y6)[n6:] == CANARY).all()
     ref = O.q4k_gemv_f64(b4, to_host(x), n4, k)
     assert np.abs(to_host(s4) - ref).max() <= 1e-3 * np.abs(ref).max() + 1e-3
+
+
+@pytest.mark.parametrize("nq,nk,nv", [(8192, 512, 512), (100, 3000, 7)])
+def test_qkv_one_launch_matches_separate(O, attn, torch_mod, nq, nk, nv):
+    """q, k (Q4_K) and v (Q6_K) in one launch equal the three separate launches bit for bit."""
+    torch = torch_mod
+    k = 2048
+    rng = np.random.default_rng(nq + 3 * nk + 5 * nv)
+    bq, bk, bv = random_blocks(rng, nq, k), random_blocks(rng, nk, k), random_q6k_blocks(rng, nv, k)
+    x = to_dev(torch, rng.standard_normal(k).astype(np.float32))
+    wq, wk = to_dev(torch, O.q4k_repack_r1(bq)), to_dev(torch, O.q4k_repack_r1(bk))
+    wv = to_dev(torch, O.q6k_repack_r1(bv, nv, k))
+    ys = [torch.full((n + 64,), CANARY, device="cuda") for n in (nq, nk, nv)]
+    ss = [torch.empty(n, device="cuda") for n in (nq, nk, nv)]
+    attn.qkv_gemv(wq, nq, ys[0], wk, nk, ys[1], wv, nv, ys[2], x)
+    attn.q4k_gemv(wq, x, ss[0], nq, k, "fp16")
+    attn.q4k_gemv(wk, x, ss[1], nk, k, "fp16")
+    attn.q6k_gemv(wv, x, ss[2], nv, k)
+    torch.cuda.synchronize()
+    for y, s_, n in zip(ys, ss, (nq, nk, nv)):
+        assert torch.equal(y[:n], s_)
+        assert (to_host(y)[n:] == CANARY).all()
