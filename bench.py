@@ -528,8 +528,9 @@ def bench_other(torch, A, args):
     tq = timed(lambda i: A.qkv_gemv(w4[i % copies_p], 8192, y4, wk[i % copies_p], 512, yk,
                                     w6[i % copies_p], 512, y6, x2048), copies_p)
     del w4, w6, wk
-    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired with "
-                                      "attn_q in one launch (synthetic blocks, HBM-resident weights)",
+    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired "
+                                      "with attn_q in one launch (synthetic blocks, HBM-resident "
+                                      "weights)",
                           "attn_v": line(w6b, t6, copies, k=2048, n_rows=512),
                           "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p),
                           "attn_q_k_v_one_launch": line(w4b + w6b + 512 * 2048 // 256 * 144, tq,

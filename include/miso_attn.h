@@ -165,14 +165,15 @@ int miso_attn_prep_fp8(const float* qg, const float* k, const float* v, const fl
                        float eps, void* stream);
 
 /* miso_attn_decode over e4m3 rows: split-K partials (same spans and partial layout as
- * miso_attn_split) then miso_attn_combine. Same scratch sizes and rejections as miso_attn_decode. */
+ * miso_attn_split) then miso_attn_combine. Same scratch sizes and rejections as
+ * miso_attn_decode. */
 int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
                          const float* k_scale, const float* v_scale, float* core, float* part_m,
                          float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                          uint32_t n_splits, void* stream);
 
-/* Q4_K GEMV y = W x (row f4: the attention's Q4_K projections attn_q, attn_k, attn_output). Replaces
- * the launches of q4k_gemv_kernel<ActFormat, K, 256, R> in gemv() (src/engine/weights.hip:248-275,
+/* Q4_K GEMV y = W x (the attention's Q4_K projections attn_q, attn_k, attn_output). Replaces the
+ * launches of q4k_gemv_kernel<ActFormat, K, 256, R> in gemv() (src/engine/weights.hip:248-275,
  * kernels/q4k_gemv.hpp:196-239). w: n_rows rows of k / 256 Q4_K blocks in the r1 layout
  * (src/repack.hpp:14-19; 144 bytes per block, 16-byte aligned), x: k floats (16-byte aligned),
  * y: n_rows floats. act_format 1 converts x to f16 (the engine's choice), 0 to per-32 absmax

@@ -363,8 +363,8 @@ __device__ __attribute__((always_inline)) inline void process_unit_fp8(
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh over e4m3 rows (K8 / V8 /
 // KS / VS: the KV head's bases), written at `base` in the reference's partial layout. The same
 // schedule as split_partial_rows with 16-row units: wave w streams units starting at rows
-// span.begin + 16 w, + 64, ... through its kRingUnits-unit LDS ring; rows past the span are masked and
-// rows past len - 1 are never read.
+// span.begin + 16 w, + 64, ... through its kRingUnits-unit LDS ring; rows past the span are
+// masked and rows past len - 1 are never read.
 template <class Shared>
 __device__ __attribute__((always_inline)) inline void split_partial_fp8(
     const float* __restrict__ q, const uint8_t* K8, const uint8_t* V8, const float* KS,

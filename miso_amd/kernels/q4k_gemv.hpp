@@ -90,6 +90,15 @@ __device__ __attribute__((always_inline)) inline const float* chunk_x(const floa
   return x + 256 * (c >> 3) + 64 * ((c >> 1) & 3u) + 16 * (c & 1u);
 }
 
+__device__ __attribute__((always_inline)) inline half2_t pair(float a, float b) {
+  return half2_t{static_cast<_Float16>(a), static_cast<_Float16>(b)};
+}
+
+// Lane ^ 1's value (DPP quad permutation [1, 0, 3, 2]).
+__device__ __attribute__((always_inline)) inline float swap_pair(float v) {
+  return cdna4::as_float(__builtin_amdgcn_mov_dpp(cdna4::as_uint(v), 0xB1, 0xF, 0xF, false));
+}
+
 template <ActFormat A>
 __device__ inline ChunkX<A> convert_chunk(const float* x, unsigned c) {
   float lo[16], hi[16];
@@ -101,10 +110,10 @@ __device__ inline ChunkX<A> convert_chunk(const float* x, unsigned c) {
     s.sum_hi = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s.lo_ev[i] = half2_t{static_cast<_Float16>(lo[4 * i]), static_cast<_Float16>(lo[4 * i + 2])};
-      s.lo_od[i] = half2_t{static_cast<_Float16>(lo[4 * i + 1]), static_cast<_Float16>(lo[4 * i + 3])};
-      s.hi_ev[i] = half2_t{static_cast<_Float16>(hi[4 * i]), static_cast<_Float16>(hi[4 * i + 2])};
-      s.hi_od[i] = half2_t{static_cast<_Float16>(hi[4 * i + 1]), static_cast<_Float16>(hi[4 * i + 3])};
+      s.lo_ev[i] = pair(lo[4 * i], lo[4 * i + 2]);
+      s.lo_od[i] = pair(lo[4 * i + 1], lo[4 * i + 3]);
+      s.hi_ev[i] = pair(hi[4 * i], hi[4 * i + 2]);
+      s.hi_od[i] = pair(hi[4 * i + 1], hi[4 * i + 3]);
       s.sum_lo += (static_cast<float>(s.lo_ev[i][0]) + static_cast<float>(s.lo_ev[i][1])) +
                   (static_cast<float>(s.lo_od[i][0]) + static_cast<float>(s.lo_od[i][1]));
       s.sum_hi += (static_cast<float>(s.hi_ev[i][0]) + static_cast<float>(s.hi_ev[i][1])) +
@@ -118,8 +127,8 @@ __device__ inline ChunkX<A> convert_chunk(const float* x, unsigned c) {
       m_lo = fmaxf(m_lo, __builtin_fabsf(lo[i]));
       m_hi = fmaxf(m_hi, __builtin_fabsf(hi[i]));
     }
-    m_lo = fmaxf(m_lo, cdna4::as_float(__builtin_amdgcn_mov_dpp(cdna4::as_uint(m_lo), 0xB1, 0xF, 0xF, false)));
-    m_hi = fmaxf(m_hi, cdna4::as_float(__builtin_amdgcn_mov_dpp(cdna4::as_uint(m_hi), 0xB1, 0xF, 0xF, false)));
+    m_lo = fmaxf(m_lo, swap_pair(m_lo));
+    m_hi = fmaxf(m_hi, swap_pair(m_hi));
     s.step_lo = m_lo / 127.0f;
     s.step_hi = m_hi / 127.0f;
     const float inv_lo = m_lo > 0.0f ? 127.0f / m_lo : 0.0f;

@@ -47,8 +47,8 @@ __device__ inline Half16 half16(const float* x) {
   r.sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    r.ev[i] = half2_t{static_cast<_Float16>(v[4 * i]), static_cast<_Float16>(v[4 * i + 2])};
-    r.od[i] = half2_t{static_cast<_Float16>(v[4 * i + 1]), static_cast<_Float16>(v[4 * i + 3])};
+    r.ev[i] = q4k_gemv_detail::pair(v[4 * i], v[4 * i + 2]);
+    r.od[i] = q4k_gemv_detail::pair(v[4 * i + 1], v[4 * i + 3]);
     r.sum += (static_cast<float>(r.ev[i][0]) + static_cast<float>(r.ev[i][1])) +
              (static_cast<float>(r.od[i][0]) + static_cast<float>(r.od[i][1]));
   }
@@ -113,7 +113,8 @@ __device__ __attribute__((always_inline)) inline float chunk_dot(const ChunkW& w
   const float sc_lo = static_cast<float>(static_cast<std::int8_t>(w.sc & 0xFFu));
   const float sc_hi = static_cast<float>(static_cast<std::int8_t>(w.sc >> 8));
   const float d = q4k_gemv_detail::half_bits(w.d_bits & 0xFFFFu);
-  return d * (sc_lo * (0x1p24f * lo - 32.0f * x.lo.sum) + sc_hi * (0x1p24f * hi - 32.0f * x.hi.sum));
+  return d * (sc_lo * (0x1p24f * lo - 32.0f * x.lo.sum) +
+              sc_hi * (0x1p24f * hi - 32.0f * x.hi.sum));
 }
 
 }  // namespace q6k_gemv_detail

@@ -650,7 +650,8 @@ void oracle_q4k_repack_r1(const uint8_t* src, size_t n_blocks, uint8_t* dst) {
       uint8_t sc0, m0, sc1, m1;
       oracle_q4k_scale_min(s, 2 * g, &sc0, &m0);
       oracle_q4k_scale_min(s, 2 * g + 1, &sc1, &m1);
-      const uint32_t v = (uint32_t)sc0 | (uint32_t)m0 << 6 | (uint32_t)sc1 << 12 | (uint32_t)m1 << 18;
+      const uint32_t v =
+          (uint32_t)sc0 | (uint32_t)m0 << 6 | (uint32_t)sc1 << 12 | (uint32_t)m1 << 18;
       for (int i = 0; i < 3; ++i) d[4 + 3 * g + i] = (uint8_t)(v >> (8 * i));
     }
   }
