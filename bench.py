@@ -3,7 +3,9 @@
 
 Headline (BASELINE.json metric, config C2): decode attention for 1 sequence / 1 token at context
 32768 (16 query heads, 2 KV heads, head_dim 256, f16 KV cache [2][32768][256], N(0,1) synthetic
-inputs), split-K over the KV length + LSE merge x sigmoid gate. A step = one decode call
+inputs), split-K over the KV length + LSE merge x sigmoid gate, in the reference's arithmetic
+(f32 query, scores, numerators and accumulation; the f16-query variant is a labelled
+other_configs line). A step = one decode call
 (split + combine kernels) over one KV cache; `value` = algorithmic KV bytes (67,108,864 B per
 step) / measured time, in GB/s. The inputs are resident in HBM; steps rotate over 6 distinct KV
 caches (384 MiB > the 256 MiB Infinity Cache) so every step streams from HBM.
@@ -15,13 +17,12 @@ Also reported:
   prefill       C4: 8192 new tokens after an 8192-token prefix, causal, f16 MFMA; TFLOP/s over
                 the unmasked (query, key) pairs (1.6493e12 FLOP) vs the 2516.6 TFLOP/s f16 peak.
   cpu_baseline  the FP64 oracle (a C restatement of the reference's host scalar attention) on a
-                bounded sample of the same workload on this host's CPU, rank 0 only.
-  sustained     a pure f16 MFMA loop on random operands over all CUs (libmiso_probe.so): the
-                shader clock the MFMA units hold under such a load and the dense rate it reaches;
-                the prefill is also reported against the peak at that clock.
-  lds           the LDS time of one prefill tile's K and V operand reads on every CU with no
-                MFMA (libmiso_probe.so), against the 1024 cycles the tile's MFMAs take.
-  other_configs C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
+                bounded sample of the same workload on this host's CPU, rank 0 only: single
+                thread and all cores (<= 16), with the CPU model and thread counts; its first
+                call also checks the bench's own timed C2 output (the bench exits 3 on a
+                mismatch).
+  other_configs C2_f16q (C2 with the f16-query variant), C2_engine_cap60 (C2 at the engine's
+                shipped split capacity of 60), C1 (decode, ctx 512: us per call), C3 (prefill, 2048 tokens, empty cache:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
                 and C5 over a pool of 16-row KV pages (the paged entry point); C2 over an fp8
                 (e4m3 rows) KV cache: us per decode step and GB/s of codes + row scales.
@@ -155,91 +156,6 @@ def device_state():
     return {"error": last}
 
 
-def mfma_sustained(torch):
-    """Shader clock and dense f16 MFMA rate of a pure MFMA loop on random operands, one workgroup
-    per CU (libmiso_probe.so); median of 3 launches."""
-    import ctypes
-    path = ROOT / "miso_amd" / "lib" / "libmiso_probe.so"
-    if not path.exists():
-        return None
-    lib = ctypes.CDLL(str(path))
-    fn = lib.miso_probe_mfma_clock
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_void_p]
-    fn.restype = ctypes.c_int
-    blocks = torch.cuda.get_device_properties(0).multi_processor_count
-    iters = 2048
-    out = torch.empty(blocks * 256, device="cuda")
-    cyc = torch.zeros(blocks, dtype=torch.int64, device="cuda")
-    stream = torch.cuda.current_stream().cuda_stream
-
-    def launch():
-        rc = fn(out.data_ptr(), cyc.data_ptr(), blocks, iters, stream)
-        if rc != 0:
-            raise RuntimeError(f"miso_probe_mfma_clock failed: {rc}")
-
-    launch()
-    torch.cuda.synchronize()
-    runs = []
-    for _ in range(3):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        launch()
-        e1.record()
-        torch.cuda.synchronize()
-        runs.append((e0.elapsed_time(e1), cyc.double().mean().item()))
-    runs.sort()
-    ms, cycles = runs[1]
-    ghz = cycles / (ms * 1e6)
-    flop = blocks * 4.0 * 16 * iters * 2 * 32 * 32 * 16
-    return {"clock_ghz": round(ghz, 3), "mfma_tflops": round(flop / (ms * 1e-3) / 1e12, 1),
-            "peak_at_clock_tflops": round(blocks * 4096 * ghz * 1e9 / 1e12, 1),
-            "probe": f"{blocks} workgroups x 4 waves, 8 accumulator chains of "
-                     f"v_mfma_f32_32x32x16_f16 on random f16, {16 * iters} MFMAs per wave; "
-                     "cycles from s_memtime, time from HIP events"}
-
-
-def lds_tile_cost(torch):
-    """LDS time of one prefill tile's operand reads (libmiso_probe.so): 4 waves per CU each read a
-    32-key K tile (16 ds_read_b128) and V tile (32 ds_read_b64_tr_b16) in the prefill's layout,
-    no MFMA; shader cycles per tile (median of 3 launches per mode) against the 1024 cycles the
-    tile's MFMAs occupy each SIMD (4 waves x 32 MFMAs x 32 cycles over 4 SIMDs)."""
-    import ctypes
-    path = ROOT / "miso_amd" / "lib" / "libmiso_probe.so"
-    if not path.exists():
-        return None
-    lib = ctypes.CDLL(str(path))
-    fn = lib.miso_probe_lds_tile
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
-                   ctypes.c_void_p]
-    fn.restype = ctypes.c_int
-    blocks = torch.cuda.get_device_properties(0).multi_processor_count
-    iters = 2048
-    out = torch.empty(blocks * 256, device="cuda")
-    cyc = torch.zeros(blocks * 4, dtype=torch.int64, device="cuda")
-    stream = torch.cuda.current_stream().cuda_stream
-    per_tile = {}
-    for mode in (0, 1, 2):
-        runs = []
-        for _ in range(4):  # the first is a warmup
-            rc = fn(out.data_ptr(), cyc.data_ptr(), blocks, mode, iters, stream)
-            if rc != 0:
-                raise RuntimeError(f"miso_probe_lds_tile failed: {rc}")
-            torch.cuda.synchronize()
-            runs.append(cyc.double().mean().item() / iters)
-        per_tile[mode] = sorted(runs[1:])[1]
-    mfma_cycles = 4 * 32 * 32 / 4
-    kv_bytes = 4 * 16384
-    return {"tile_read_cycles": round(per_tile[0], 1), "k_read_cycles": round(per_tile[1], 1),
-            "v_read_cycles": round(per_tile[2], 1),
-            "k_bytes_per_clk": round(kv_bytes / per_tile[1], 1),
-            "v_bytes_per_clk": round(kv_bytes / per_tile[2], 1),
-            "mfma_cycles_per_tile": mfma_cycles,
-            "mfma_ceiling_from_lds_reads": round(min(1.0, mfma_cycles / per_tile[0]), 4),
-            "probe": f"{blocks} workgroups x 4 waves; per wave and tile 16 KiB of K by "
-                     "ds_read_b128 and 16 KiB of V by ds_read_b64_tr_b16 at the prefill's "
-                     f"swizzled addresses, {iters} tiles; cycles from s_memtime"}
-
-
 def traffic_from_profiles(name):
     p = ROOT / "profiles" / f"{name}_traffic.json"
     if not p.exists():
@@ -250,7 +166,8 @@ def traffic_from_profiles(name):
         return None
 
 
-def bench_decode(torch, A, args):
+def decode_caches(torch, args):
+    """C2 inputs: q, qg and `buffers` distinct N(0,1) f16 KV caches of ctx positions."""
     L, R = args.ctx, args.buffers
     gen = torch.Generator(device="cuda")
     gen.manual_seed(L)
@@ -261,18 +178,30 @@ def bench_decode(torch, A, args):
         k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
         v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
         caches.append((k, v))
-    sc = A.DecodeScratch(args.max_splits)
-    n_splits = A.attn_n_splits(L, args.max_splits)
+    return q, qg, caches
+
+
+def bench_decode(torch, A, args, inputs, max_splits, f16_query=False, label="C2"):
+    """One decode call per step over rotated caches: step (split + combine), split alone and
+    combine alone, each as a graph of `buffers` calls replayed; per-call times in ms. Returns
+    the output of one call on cache 0 for the oracle check."""
+    q, qg, caches = inputs
+    L, R = args.ctx, args.buffers
+    sc = A.DecodeScratch(max_splits)
+    n_splits = A.attn_n_splits(L, max_splits)
     core = torch.empty(H * D, device="cuda")
     kv_bytes = 2 * KV * L * D * 2
 
     def step(i):
         k, v = caches[i % R]
-        A.attn_decode(q, qg, k, v, core, sc, L, L, n_splits)
+        A.attn_decode(q, qg, k, v, core, sc, L, L, n_splits, f16_query=f16_query)
 
     def split_only(i):
         k, v = caches[i % R]
-        A.attn_split(q, k, v, sc.part_m, sc.part_l, sc.part_o, L, L, n_splits)
+        if f16_query:
+            A.attn_decode(q, qg, k, v, core, sc, L, L, n_splits, f16_query=True)
+        else:
+            A.attn_split(q, k, v, sc.part_m, sc.part_l, sc.part_o, L, L, n_splits)
 
     def combine_only(i):
         A.attn_combine(sc.part_m, sc.part_l, sc.part_o, qg, core, n_splits)
@@ -292,17 +221,24 @@ def bench_decode(torch, A, args):
     t_step = ms_step / steps
     t_split = ms_split / steps
     t_comb = ms_comb / steps
-    log(f"decode C2: step {t_step * 1e3:.2f} us (wall {wall_step / steps * 1e3:.2f} us), "
+    if f16_query:
+        t_split -= t_comb  # the f16q graph above times split + combine
+    log(f"decode {label}: step {t_step * 1e3:.2f} us (wall {wall_step / steps * 1e3:.2f} us), "
         f"split {t_split * 1e3:.2f} us, combine {t_comb * 1e3:.2f} us, n_splits {n_splits}")
-    host = {
-        "q": q.cpu().numpy(), "qg": qg.cpu().numpy(),
-        "k": caches[0][0].view(torch.int16).cpu().numpy().view("uint16"),
-        "v": caches[0][1].view(torch.int16).cpu().numpy().view("uint16"),
-    }
+    step(0)
+    torch.cuda.synchronize()
     return {
         "steps": steps, "t_step_ms": t_step, "t_split_ms": t_split, "t_comb_ms": t_comb,
-        "kv_bytes": kv_bytes, "n_splits": n_splits, "host": host, "L": L,
+        "kv_bytes": kv_bytes, "n_splits": n_splits, "L": L, "core0": core.cpu().numpy(),
     }
+
+
+def decode_line(dec, workload):
+    gbs = dec["kv_bytes"] / (dec["t_step_ms"] * 1e-3) / 1e9
+    return {"workload": workload, "us_per_step": round(dec["t_step_ms"] * 1e3, 3),
+            "split_us": round(dec["t_split_ms"] * 1e3, 3),
+            "combine_us": round(dec["t_comb_ms"] * 1e3, 3), "n_splits": dec["n_splits"],
+            "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def bench_prefill(torch, A, args):
@@ -546,24 +482,81 @@ def bench_other(torch, A, args):
     return out
 
 
-def cpu_decode_baseline(dec):
-    """FP64 oracle, single thread, on full C2 calls over the bench's first KV cache; about
-    10 s of CPU work."""
+def cpu_info():
+    """The host CPU as the box reports it: model name, std::thread::hardware_concurrency()'s
+    equivalent (logical CPUs) and the CPUs this process may run on."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"model": model, "hardware_concurrency": os.cpu_count(), "usable_cpus": usable}
+
+
+def cpu_threads():
+    """All-core thread count for the oracle: the usable CPUs, at most 16 (the box's CPU share
+    per GPU)."""
+    return max(1, min(16, cpu_info()["usable_cpus"] or 1))
+
+
+def cpu_decode_baseline(dec, inputs):
+    """FP64 oracle on full C2 calls over the bench's first KV cache: single-thread (the
+    reference's loops) for ~10 s, then all cores for ~5 s. The first call's output is also the
+    check of the bench's own timed kernels: the step output on cache 0 must match it within the
+    north star's tolerance and the reference's per-head rel-L2 gate, or the bench fails."""
     from oracle import oracle as O
-    h, L = dec["host"], dec["L"]
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.decode_f64(h["q"], h["qg"], h["k"], h["v"], L, L, threads=1)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= 10.0 or reps >= 40:
-            break
+    q, qg, caches = inputs
+    h = {"q": q.cpu().numpy(), "qg": qg.cpu().numpy(),
+         "k": caches[0][0].view(torch_mod().int16).cpu().numpy().view("uint16"),
+         "v": caches[0][1].view(torch_mod().int16).cpu().numpy().view("uint16")}
+    L = dec["L"]
+
+    def timed(threads, budget, cap):
+        reps, t0, out = 0, time.perf_counter(), None
+        while True:
+            r = O.decode_f64(h["q"], h["qg"], h["k"], h["v"], L, L, threads=threads)
+            out = r if out is None else out
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= cap:
+                return reps, el, out
+
+    reps1, el1, ref = timed(1, 10.0, 40)
+    st = O.compare(dec["core0"].reshape(H, D), ref)
+    check = {"max_abs": st["max_abs"], "rel_l2_head": st["rel_l2_head"], "ok": bool(
+        st["ok"] and st["rel_l2_head"] <= 1e-5)}
+    if not check["ok"]:
+        print(f"bench.py: the timed C2 decode output disagrees with the FP64 oracle: {st}",
+              file=sys.stderr, flush=True)
+        sys.exit(3)
+    nt = cpu_threads()
+    repsn, eln, _ = timed(nt, 5.0, 400)
+    single = dec["kv_bytes"] * reps1 / el1 / 1e9
+    multi = dec["kv_bytes"] * repsn / eln / 1e9
     return {
-        "value": dec["kv_bytes"] * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"C2 decode (ctx 32768): {reps} full FP64 oracle calls on KV cache 0, "
-                  f"{el:.1f} s, single thread",
-        "ms_per_call": el / reps * 1e3,
+        "value": single, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"C2 decode (ctx 32768): {reps1} full FP64 oracle calls on KV cache 0, "
+                  f"{el1:.1f} s, single thread (the reference's host loops); all-core line below",
+        "ms_per_call": el1 / reps1 * 1e3,
+        "all_cores": {"value": multi, "unit": "GB/s", "cores": nt,
+                      "ms_per_call": eln / repsn * 1e3,
+                      "sample": f"{repsn} full C2 oracle calls, {eln:.1f} s, {nt} threads over "
+                                "the 16 heads"},
+        "cpu": cpu_info(),
+        "gpu_output_check": check,
     }
+
+
+def torch_mod():
+    import torch
+    return torch
 
 
 def cpu_prefill_baseline(pre):
@@ -608,11 +601,24 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
     if args.copy_calibration:
         copy_calibration(torch)
-    dec = bench_decode(torch, A, args)
+    inputs = decode_caches(torch, args)
+    dec = bench_decode(torch, A, args, inputs, args.max_splits)
+    other = {}
+    if not args.no_other:
+        d16 = bench_decode(torch, A, args, inputs, args.max_splits, f16_query=True,
+                           label="C2 f16 query")
+        other["C2_f16q"] = decode_line(
+            d16, "C2 with an f16 query and f16 numerators (v_dot2_f32_f16; miso_attn_decode_f16q):"
+                 " half the VALU work, per-head rel-L2 ~3e-4 -- not the reference's arithmetic")
+        d60 = bench_decode(torch, A, args, inputs, 60, label="C2 engine cap 60")
+        other["C2_engine_cap60"] = decode_line(
+            d60, "C2 at the engine's shipped partial capacity kMaxSplits = 60 "
+                 "(src/engine/attention.hpp:46): 60 splits x 2 KV heads = 120 workgroups")
     pre = None if args.no_prefill else bench_prefill(torch, A, args)
-    sustained = None if args.no_prefill else mfma_sustained(torch)
-    lds = None if args.no_prefill else lds_tile_cost(torch)
-    other = None if args.no_other else bench_other(torch, A, args)
+    if not args.no_other:
+        other.update(bench_other(torch, A, args))
+    else:
+        other = None
     # Right after the GPU runs, while the clocks are still up. Not under a profiler: its preloaded
     # library would initialise the GPU in the smi tools too, before they exec their interpreter.
     profiled = "rocprof" in os.environ.get("LD_PRELOAD", "")
@@ -631,13 +637,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "f32",
         "data": "synthetic",
         "config": {
             "workload": "C2: decode attention, 1 sequence x 1 token, ctx 32768, 16Q/2KV heads, "
                         "head_dim 256, f16 KV [2][32768][256], split-K + LSE merge x sigmoid gate",
             "ctx": dec["L"], "n_splits": dec["n_splits"], "kv_buffers_rotated": args.buffers,
             "step": "split kernel + combine kernel (one decode call)",
+            "arithmetic": "f32 query, scores, softmax numerators and accumulation over the f16 "
+                          "KV cache (the reference's, kernels/attention_decode.hpp:150-221); "
+                          "storage f16",
             "algorithmic_bytes_per_step": dec["kv_bytes"],
         },
         "roofline": {
@@ -664,20 +673,13 @@ def main():
                          "unit": "TFLOP/s", "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                          "traffic": traffic_from_profiles("prefill_c4")},
         }
-        if sustained is not None:
-            sustained["frac_of_peak_at_clock"] = round(
-                pre["tflops"] / sustained["peak_at_clock_tflops"], 4)
-            sustained["frac_of_probe_rate"] = round(pre["tflops"] / sustained["mfma_tflops"], 4)
-            out["prefill"]["sustained"] = sustained
-        if lds is not None:
-            out["prefill"]["lds"] = lds
     if other is not None:
         out["other_configs"] = other
     if device is not None:
         out["device"] = device
     if not args.no_cpu:
         log("cpu baseline (decode) ...")
-        out["cpu_baseline"] = cpu_decode_baseline(dec)
+        out["cpu_baseline"] = cpu_decode_baseline(dec, inputs)
         if pre is not None and pre["host"] is not None:
             log("cpu baseline (prefill sample) ...")
             out["prefill"]["cpu_baseline"] = cpu_prefill_baseline(pre)

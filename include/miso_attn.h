@@ -69,7 +69,9 @@ int miso_attn_prep_batch(const float* qg, const float* k, const float* v, const 
 /* Split-K partials: replaces attn_split_kernel<256><<<dim3(n_splits, 2), 256, 0, stream>>>(
  * AttnSplitParams{...}), src/engine/attention.hip:103-106 and tests/test_attn_splitk.hip:125-134
  * (kernels/attention_decode.hpp:117-236). Writes part_m/part_l [2][n_splits][8] and part_o
- * [2][n_splits][8][256] for keys [0, len). Rejects len == 0, len > max_ctx, n_splits == 0. */
+ * [2][n_splits][8][256] for keys [0, len), in the reference's arithmetic (f32 query, scores,
+ * numerators and accumulation over the f16 cache). Rejects len == 0, len > max_ctx,
+ * n_splits == 0. */
 int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     float* part_m, float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                     uint32_t n_splits, void* stream);
@@ -99,6 +101,17 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
                      const uint16_t* v_cache, float* core, float* part_m, float* part_l,
                      float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
                      void* stream);
+
+/* The decode step with an f16 query and f16 softmax numerators (v_dot2_f32_f16, two products
+ * per instruction): attn_split_f16q_kernel<256> then the combine of miso_attn_combine. No
+ * reference counterpart -- the reference computes in f32 (kernels/attention_decode.hpp:150-221),
+ * as miso_attn_split / miso_attn_decode do; this variant does half their VALU work at a per-head
+ * relative L2 error of ~3e-4 instead of ~1e-6. Same arguments, scratch and rejections as
+ * miso_attn_decode. */
+int miso_attn_decode_f16q(const float* q, const float* qg, const uint16_t* k_cache,
+                          const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                          float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
+                          void* stream);
 
 /* Causal prefill: replaces attn_prefill_kernel<256><<<attn_prefill_items(n), 256, 0, stream>>>(
  * AttnPrefillParams{...}), src/engine/attention.hip:141-144 and tests/test_attn_splitk.hip:224-233

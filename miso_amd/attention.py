@@ -146,8 +146,11 @@ class DecodeScratch:
 
 
 def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: int,
-                max_ctx: int, n_splits: Optional[int] = None, stream=None) -> int:
-    """Split + combine for one decode token over keys [0, length). Returns n_splits used."""
+                max_ctx: int, n_splits: Optional[int] = None, stream=None,
+                f16_query: bool = False) -> int:
+    """Split + combine for one decode token over keys [0, length), in the reference's f32
+    arithmetic (or, with f16_query, the f16-query / f16-numerator variant
+    miso_attn_decode_f16q). Returns n_splits used."""
     if n_splits is None:
         n_splits = attn_n_splits(length, scratch.max_splits)
     if n_splits > scratch.max_splits:
@@ -158,7 +161,9 @@ def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: i
     _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
     _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
     _need(core, "core", f32, Q_HEADS * DIM)
-    _lib.check(_lib.load().miso_attn_decode(
+    lib = _lib.load()
+    fn = lib.miso_attn_decode_f16q if f16_query else lib.miso_attn_decode
+    _lib.check(fn(
         _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), _ptr(scratch.part_m),
         _ptr(scratch.part_l), _ptr(scratch.part_o), length, max_ctx, n_splits, _stream(stream)))
     return n_splits

@@ -19,10 +19,6 @@ ROOT = PKG.parent
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libmiso_attn.so"
 SOURCES = [PKG / "csrc" / "miso_attn_capi.hip"]
-# Measurement infrastructure for bench.py (sustained MFMA clock, LDS read cost of a prefill
-# tile), not part of the C ABI.
-PROBE_LIB = LIB_DIR / "libmiso_probe.so"
-PROBE_SOURCES = [PKG / "csrc" / "mfma_clock_probe.hip", PKG / "csrc" / "lds_tile_probe.hip"]
 HEADERS = sorted((PKG / "kernels").glob("*.hpp")) + [ROOT / "include" / "miso_attn.h"]
 
 # Packed FP32 VALU forms are disabled for all device code built here.
@@ -47,9 +43,8 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile libmiso_attn.so (and the bench's libmiso_probe.so) for gfx950 (always recompiles)."""
+    """Compile libmiso_attn.so for gfx950 (always recompiles)."""
     _compile(SOURCES, LIB, verbose)
-    _compile(PROBE_SOURCES, PROBE_LIB, verbose)
     return LIB
 
 

@@ -106,7 +106,7 @@ extern "C" {
 
 const char* miso_attn_last_error(void) { return g_last_error.c_str(); }
 
-const char* miso_attn_version(void) { return "miso_attn gfx950 r1"; }
+const char* miso_attn_version(void) { return "miso_attn gfx950 2"; }
 
 uint32_t miso_attn_n_splits(uint32_t len, uint32_t max_splits) {
   return k::attn_n_splits(len, max_splits);
@@ -207,6 +207,28 @@ int miso_attn_combine_variant(int variant, const float* part_m, const float* par
     }
   }
   return launched("miso_attn_combine_variant");
+}
+
+int miso_attn_decode_f16q(const float* q, const float* qg, const uint16_t* k_cache,
+                          const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                          float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
+                          void* stream) {
+  if (any_bad(q, qg, k_cache, v_cache, core, part_o) || bad_scalars(part_m) ||
+      bad_scalars(part_l))
+    return fail("miso_attn_decode_f16q", kBadPtr);
+  if (len == 0)
+    return fail("miso_attn_decode_f16q", "len must be >= 1");
+  if (len > max_ctx)
+    return fail("miso_attn_decode_f16q", "len exceeds max_ctx");
+  if (n_splits == 0)
+    return fail("miso_attn_decode_f16q", "n_splits must be >= 1");
+  const k::AttnSplitParams p{q,      as_half(k_cache), as_half(v_cache), part_m, part_l,
+                             part_o, len,              max_ctx,          n_splits};
+  k::attn_split_f16q_kernel<256><<<dim3(n_splits, 2), 256, 0, as_stream(stream)>>>(p);
+  const int rc = launched("miso_attn_decode_f16q");
+  if (rc != 0)
+    return rc;
+  return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
 }
 
 int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,

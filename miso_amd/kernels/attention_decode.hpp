@@ -185,17 +185,20 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: numerators stay <= 2^8 bet
 template <int W, int R>
 struct SplitSharedT {
   static constexpr int kWaveCount = W, kRingUnits = R;
-  union {
-    unsigned char ring[W][R][kUnitBytes];
-    float merge_o[W][2][kGroup][attn::kDim];  // [wave][row parity][head][dim], unscaled
-  };
+  // Each wave's ring of units; after its stream, slot 0 of a wave's ring holds that wave's
+  // value accumulators for the cross-wave merge ([head][dim], 8 x 256 floats = 8 KiB), so a
+  // wave that finishes early never writes into a ring another wave still streams through.
+  unsigned char ring[W][R][kUnitBytes];
   float q[kGroup][attn::kDim];
   // Numerators of one unit as f16 pairs, [wave][row parity a][pair g][head]: the pair holds rows
-  // 2 g + a and 2 g + 4 + a of the unit.
+  // 2 g + a and 2 g + 4 + a of the unit (f16-query arithmetic).
   uint32_t p[W][2][2][kGroup];
+  // Numerators of one unit in f32, [wave][unit row][head] (f32 arithmetic).
+  float pf[W][kAttnDecodeUnit][kGroup];
   float stat_m[W][kGroup], stat_mt[W][kGroup], stat_l[W][2][kGroup];
-  static_assert(sizeof(float) * W * 2 * kGroup * attn::kDim <= sizeof(unsigned char) * W * R *
-                    kUnitBytes, "the merge area must fit in the ring");
+  static_assert(sizeof(float) * kGroup * attn::kDim <= kUnitBytes,
+                "a wave's merge rows must fit in one slot of its own ring");
+  __device__ float* merge_rows(int w) { return reinterpret_cast<float*>(ring[w][0]); }
 };
 using SplitShared = SplitSharedT<kWaves, kRing>;
 
@@ -283,11 +286,9 @@ __device__ __attribute__((always_inline)) inline float dot2_first(half2_t a, uns
 // (head 4 hq + dc / 4, unit row 4 rq + dc % 4), the span mask, the lazy rescale, and the f16
 // numerators, published to `pbuf` for P V. With kScaled, the score is multiplied by its row's K
 // scale and the published numerator by its row's V scale (the l sum stays unscaled).
-template <bool kScaled>
-__device__ __attribute__((always_inline)) inline void unit_numerators(
-    WaveState& st, const float (&part)[16], unsigned u0, unsigned span_end, float ksc, float vsc,
-    uint32_t (*pbuf)[2][kGroup], unsigned lane) {
-  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+// The reduce-scatter of the lane's 16 partial dot products (see process_unit) over the 16 lanes
+// of dc: returns the complete score of head 4 hq + dc / 4, unit row 4 rq + dc % 4.
+__device__ __attribute__((always_inline)) inline float unit_scores(const float (&part)[16]) {
   float r8[8], r4[4], r2[2];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
@@ -298,9 +299,18 @@ __device__ __attribute__((always_inline)) inline void unit_numerators(
 #pragma unroll
   for (int j = 0; j < 2; ++j)
     r2[j] = r4[j] + cdna4::dpp_mov<cdna4::kQuadXor2>(r4[j ^ 2]);
-  float s = r2[0] + cdna4::dpp_mov<cdna4::kQuadXor1>(r2[1]);
-  if constexpr (kScaled)
-    s *= ksc;
+  return r2[0] + cdna4::dpp_mov<cdna4::kQuadXor1>(r2[1]);
+}
+
+// Span mask, head max and lazy rescale of one unit's scores (lane layout of unit_scores): masks
+// rows past span_end to -inf, raises the true max mt, and moves the reference max m (rescaling l
+// and the value accumulators) only when the unit's head max exceeds it by more than the slack.
+// Returns the lane's (masked) score.
+__device__ __attribute__((always_inline)) inline float unit_softmax_state(WaveState& st, float s,
+                                                                          unsigned u0,
+                                                                          unsigned span_end,
+                                                                          unsigned lane) {
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u;
   const unsigned row = 4 * rq + (dc & 3u);
   if (u0 + row >= span_end)
     s = -__builtin_inff();
@@ -324,6 +334,19 @@ __device__ __attribute__((always_inline)) inline void unit_numerators(
         st.o[h][e] *= ch;
     }
   }
+  return s;
+}
+
+template <bool kScaled>
+__device__ __attribute__((always_inline)) inline void unit_numerators(
+    WaveState& st, const float (&part)[16], unsigned u0, unsigned span_end, float ksc, float vsc,
+    uint32_t (*pbuf)[2][kGroup], unsigned lane) {
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  float s = unit_scores(part);
+  if constexpr (kScaled)
+    s *= ksc;
+  const unsigned row = 4 * rq + (dc & 3u);
+  s = unit_softmax_state(st, s, u0, span_end, lane);
   const _Float16 p16 = static_cast<_Float16>(__builtin_amdgcn_exp2f(s - st.m));  // 0 if masked
   st.l += static_cast<float>(p16);  // the sum of exactly the numerators P V uses
   {
@@ -403,11 +426,74 @@ __device__ __attribute__((always_inline)) inline void process_unit(
   }
 }
 
+// The arithmetic of a split: the reference's (kernels/attention_decode.hpp:150-221: an f32
+// query, f32 scores, f32 numerators, f32 P V over f16 K/V widened exactly) or an f16 query and
+// f16 numerators through v_dot2_f32_f16 (two products per instruction, per-head rel-L2 ~3e-4).
+enum class DecodeArith { kF32, kF16Query };
+
+// One unit (8 rows) of the online softmax in f32 arithmetic. The lane layout is process_unit's;
+// every product is one v_fma_mix_f32 (an f16 operand widened exactly, f32 fused multiply-add).
+// S: the lane's 16 partial dot products (4 heads x 4 rows over its 16 dimensions) from its f32
+// query slice `qf` (slot hh = head 4 hq + (hh ^ dc / 4); entries 0-7 = dimensions 8 dc + j,
+// 8-15 = 128 + 8 dc + j) -- 256 products per lane. P V: o[h][e] over the lane's rows 2 i + a and
+// dimensions 8 c + e with the unit's f32 numerators from the per-wave buffer `pf[row][head]` --
+// another 256.
+__device__ __attribute__((always_inline)) inline void process_unit_f32(
+    WaveState& st, const unsigned char* slot, const unsigned (&koff)[4], const float (&qf)[4][16],
+    unsigned u0, unsigned span_end, float (*pf)[kGroup], unsigned lane) {
+  uint4 kr[4][2], vr[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    kr[rr][0] = *reinterpret_cast<const uint4*>(slot + koff[rr]);
+    kr[rr][1] = *reinterpret_cast<const uint4*>(slot + koff[rr] + 256);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    vr[i] = *reinterpret_cast<const uint4*>(slot + 4096 + 1024 * i + 16 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+  float part[16];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const cdna4::half8_t k0 = __builtin_bit_cast(cdna4::half8_t, kr[rr][0]);
+    const cdna4::half8_t k1 = __builtin_bit_cast(cdna4::half8_t, kr[rr][1]);
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      float acc = __builtin_fmaf(static_cast<float>(k0[0]), qf[hh][0], 0.0f);
+#pragma unroll
+      for (int j = 1; j < 8; ++j)
+        acc = __builtin_fmaf(static_cast<float>(k0[j]), qf[hh][j], acc);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc = __builtin_fmaf(static_cast<float>(k1[j]), qf[hh][8 + j], acc);
+      part[4 * hh + rr] = acc;
+    }
+  }
+  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  const float s = unit_softmax_state(st, unit_scores(part), u0, span_end, lane);
+  const float p = __builtin_amdgcn_exp2f(s - st.m);  // 0 if masked
+  st.l += p;
+  pf[4 * rq + (dc & 3u)][4 * hq + (dc >> 2)] = p;
+  const unsigned a = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 p0 = *reinterpret_cast<const float4*>(&pf[2 * i + a][0]);
+    const float4 p1 = *reinterpret_cast<const float4*>(&pf[2 * i + a][4]);
+    const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    const cdna4::half8_t v = __builtin_bit_cast(cdna4::half8_t, vr[i]);
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        st.o[h][e] = __builtin_fmaf(static_cast<float>(v[e]), pp[h], st.o[h][e]);
+  }
+}
+
 // Cross-wave merge relative to the split's true max M_h = max_w mt_w,h, so the partial is
-// exactly (max, sum exp(s - max), sum exp(s - max) v). Each wave stores its raw accumulators
-// (both row parities) and head statistics, then after one barrier every thread produces two
-// float4 chunks of the partial: o = sum_w exp2(m_w,h - M_h) (o_w,0 + o_w,1). `more` says whether
-// the workgroup runs another item afterwards (its LDS is then reused).
+// exactly (max, sum exp(s - max), sum exp(s - max) v). Each wave sums its two row parities across
+// its lane halves, stores the result (in slot 0 of its own ring) and its head statistics, then
+// after one barrier every thread produces two float4 chunks of the partial: o = sum_w exp2(m_w,h
+// - M_h) o_w. `more` says whether the workgroup runs another item afterwards (its LDS is then
+// reused).
 template <class Shared>
 __device__ __attribute__((always_inline)) inline void write_partial(
     const WaveState& st, Shared& sh, float* part_m, float* part_l, float* part_o,
@@ -426,12 +512,22 @@ __device__ __attribute__((always_inline)) inline void write_partial(
       sh.stat_m[wave][h] = st.m;
       sh.stat_mt[wave][h] = st.mt;
     }
+    // Sum the two row parities (lane c holds parity 0, lane c + 32 parity 1, of the same
+    // dimensions) across the wave halves: one v_permlane32_swap per pair of heads (h, h + 4)
+    // leaves heads 0-3 in the lower half and heads 4-7 in the upper half, summed.
     const unsigned a = lane >> 5;
 #pragma unroll
-    for (int hh = 0; hh < kGroup; ++hh) {
-      float4* dst = reinterpret_cast<float4*>(&sh.merge_o[wave][a][hh][8 * c]);
-      dst[0] = float4{st.o[hh][0], st.o[hh][1], st.o[hh][2], st.o[hh][3]};
-      dst[1] = float4{st.o[hh][4], st.o[hh][5], st.o[hh][6], st.o[hh][7]};
+    for (int hh = 0; hh < kGroup / 2; ++hh) {
+      float sum[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const cdna4::Pair pr = cdna4::swap32(st.o[hh][e], st.o[hh + kGroup / 2][e]);
+        sum[e] = pr.a + pr.b;
+      }
+      float4* dst =
+          reinterpret_cast<float4*>(sh.merge_rows(wave) + (4 * a + hh) * attn::kDim + 8 * c);
+      dst[0] = float4{sum[0], sum[1], sum[2], sum[3]};
+      dst[1] = float4{sum[4], sum[5], sum[6], sum[7]};
     }
   }
   __syncthreads();
@@ -442,10 +538,9 @@ __device__ __attribute__((always_inline)) inline void write_partial(
     constexpr unsigned kChunks = kGroup * attn::kDim / 4, kThreads = kW * 64;
     constexpr unsigned kPer = kChunks / kThreads, kHeadChunks = attn::kDim / 4;
     static_assert(kChunks % kThreads == 0, "chunks per thread");
-    const float4* src = reinterpret_cast<const float4*>(&sh.merge_o[0][0][0][0]);
     float4* dst = reinterpret_cast<float4*>(part_o + base * kGroup * attn::kDim);
     float m[kPer][kW], mt[kPer][kW], lw[kPer][kW];
-    float4 x[kPer][kW][2];
+    float4 x[kPer][kW];
 #pragma unroll
     for (unsigned j = 0; j < kPer; ++j) {
       const unsigned i = t + kThreads * j, h = i / kHeadChunks;
@@ -454,8 +549,7 @@ __device__ __attribute__((always_inline)) inline void write_partial(
         m[j][w] = sh.stat_m[w][h];
         mt[j][w] = sh.stat_mt[w][h];
         lw[j][w] = sh.stat_l[w][0][h] + sh.stat_l[w][1][h];
-        x[j][w][0] = src[(w * 2 + 0) * kChunks + i];
-        x[j][w][1] = src[(w * 2 + 1) * kChunks + i];
+        x[j][w] = reinterpret_cast<const float4*>(sh.merge_rows(w))[i];
       }
     }
 #pragma unroll
@@ -472,11 +566,11 @@ __device__ __attribute__((always_inline)) inline void write_partial(
 #pragma unroll
       for (int w = 0; w < kW; ++w) {
         const float sc = __builtin_amdgcn_exp2f(m[j][w] - Mc);
-        const float4 x0 = x[j][w][0], x1 = x[j][w][1];
-        acc.x = __builtin_fmaf(sc, x0.x + x1.x, acc.x);
-        acc.y = __builtin_fmaf(sc, x0.y + x1.y, acc.y);
-        acc.z = __builtin_fmaf(sc, x0.z + x1.z, acc.z);
-        acc.w = __builtin_fmaf(sc, x0.w + x1.w, acc.w);
+        const float4 x0 = x[j][w];
+        acc.x = __builtin_fmaf(sc, x0.x, acc.x);
+        acc.y = __builtin_fmaf(sc, x0.y, acc.y);
+        acc.z = __builtin_fmaf(sc, x0.z, acc.z);
+        acc.w = __builtin_fmaf(sc, x0.w, acc.w);
         L = __builtin_fmaf(sc, lw[j][w], L);
       }
       dst[i] = acc;
@@ -507,23 +601,28 @@ struct PagedRows {
   std::size_t head_off;     // kvh << log2_page rows of 256 halves
 };
 
-// Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh, written at `base` (=
-// kvh * n_splits + split) in the reference's partial layout. Wave w streams units w, w + W, ...
-// of the span through its R-unit LDS ring (R - 1 units in flight while one is processed); the
-// waves merge through LDS at the end. Every vector-memory load of the kernel is a direct LDS
-// load with an explicit wait, except the paged layout's page-table slice, which is waited for
-// before the first unit is issued. `more` says whether the workgroup runs another item
-// afterwards (its LDS is then reused).
-template <class Shared, class Rows>
+// Partial (m, l, o) for KV head kvh, written at `base` (= kvh * n_splits + split) in the
+// reference's partial layout, over the rows of groups of kW units: the group starting at row
+// span.begin and every `stride` rows after it, up to row span.end (rows past it are masked).
+// Every caller passes stride = kW * 8, i.e. the contiguous span [span.begin, span.end) (a
+// variant whose splits took interleaved 32-row groups, so that all workgroups stream
+// neighbouring parts of the cache, measured no faster). Wave w streams unit w of each group
+// through its R-unit LDS ring (R - 1 units in flight while one is processed); the waves merge
+// through LDS at the end. Every vector-memory load of the kernel is a direct LDS load with an
+// explicit wait, except the paged layout's page-table slice, which is waited for before the
+// first unit is issued. `more` says whether the workgroup runs another item afterwards (its LDS
+// is then reused).
+template <DecodeArith kArith, class Shared, class Rows>
 __device__ __attribute__((always_inline)) inline void split_partial_rows(
-    const float* __restrict__ q, const Rows& rows, unsigned len, AttnSpan span, unsigned kvh,
-    float* part_m, float* part_l, float* part_o, std::size_t base, Shared& sh, bool more) {
+    const float* __restrict__ q, const Rows& rows, unsigned len, AttnSpan span, unsigned stride,
+    unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base, Shared& sh,
+    bool more) {
   constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
   static_assert(kR >= 2 && kR <= 4 && kGroup % kW == 0, "ring depth / wave count");
   const unsigned t = threadIdx.x, lane = t & 63u, c = lane & 31u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned last_row = len - 1;
-  constexpr unsigned kStride = kW * kAttnDecodeUnit;
+  const unsigned kStride = stride;
   const unsigned first = span.begin + wave * kAttnDecodeUnit;
   const unsigned n_units = first < span.end ? (span.end - first + kStride - 1) / kStride : 0;
   const unsigned ring0 = cdna4::lds_offset(sh.ring[wave][0]);
@@ -542,7 +641,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_rows(
     tab = lane < npages ? rows.table[page0 + lane] : 0;
     lane_at = std::size_t{lane >> 5} * attn::kDim + c * 8;
   }
-  constexpr std::size_t kUnitStep = std::size_t{kStride} * attn::kDim;
+  const std::size_t kUnitStep = std::size_t{kStride} * attn::kDim;
   auto issue = [&](unsigned k) {
     const unsigned u0 = first + k * kStride;
     const unsigned slot = ring0 + (k % kR) * kUnitBytes;
@@ -582,11 +681,14 @@ __device__ __attribute__((always_inline)) inline void split_partial_rows(
   wait_units_after(n_units < kR - 1 ? n_units : kR - 1);  // the query loads are older
   __syncthreads();
 
-  // Query slices as f16 pairs pre-scaled by log2(e)/16: slot hh = head 4 hq + (hh ^ dc / 4),
-  // dimensions 8 dc .. 8 dc + 7 (pairs 0-3) and 128 + 8 dc .. 128 + 8 dc + 7 (pairs 4-7).
+  // The lane's query slice pre-scaled by log2(e)/16 (1/sqrt(256) in log2 units): slot hh = head
+  // 4 hq + (hh ^ dc / 4), dimensions 8 dc .. 8 dc + 7 and 128 + 8 dc .. 128 + 8 dc + 7. In f32
+  // (qf[hh][j], j < 8 the first run) or as f16 pairs (qh[hh][p], pairs 0-3 the first run).
   const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
+  constexpr bool kF32 = kArith == DecodeArith::kF32;
+  constexpr float kScale = kLog2e / 16.0f;
+  float qf[4][16];
   half2_t qh[4][8];
-  constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
 #pragma unroll
   for (int hh = 0; hh < 4; ++hh) {
     const unsigned h = 4 * hq + (hh ^ (dc >> 2));
@@ -594,14 +696,17 @@ __device__ __attribute__((always_inline)) inline void split_partial_rows(
     for (int half = 0; half < 2; ++half) {
       const float4 x0 = *reinterpret_cast<const float4*>(&sh.q[h][128 * half + 8 * dc]);
       const float4 x1 = *reinterpret_cast<const float4*>(&sh.q[h][128 * half + 8 * dc + 4]);
-      qh[hh][4 * half + 0] = half2_t{static_cast<_Float16>(x0.x * kScale),
-                                     static_cast<_Float16>(x0.y * kScale)};
-      qh[hh][4 * half + 1] = half2_t{static_cast<_Float16>(x0.z * kScale),
-                                     static_cast<_Float16>(x0.w * kScale)};
-      qh[hh][4 * half + 2] = half2_t{static_cast<_Float16>(x1.x * kScale),
-                                     static_cast<_Float16>(x1.y * kScale)};
-      qh[hh][4 * half + 3] = half2_t{static_cast<_Float16>(x1.z * kScale),
-                                     static_cast<_Float16>(x1.w * kScale)};
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      if constexpr (kF32) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          qf[hh][8 * half + j] = x[j] * kScale;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          qh[hh][4 * half + j] = half2_t{static_cast<_Float16>(x[2 * j] * kScale),
+                                         static_cast<_Float16>(x[2 * j + 1] * kScale)};
+      }
     }
   }
   // K read offsets in a slot: row 4 rq + (rr ^ dc % 4), 16-byte chunk dc (and dc + 16, +256 B).
@@ -622,58 +727,91 @@ __device__ __attribute__((always_inline)) inline void split_partial_rows(
 
   // Steady state: one unit issued and one consumed per iteration, a fixed wait. Its slot held
   // unit k - 1, already read back into registers.
+  auto unit = [&](unsigned k) {
+    if constexpr (kF32)
+      process_unit_f32(st, sh.ring[wave][k % kR], koff, qf, first + k * kStride, span.end,
+                       sh.pf[wave], lane);
+    else
+      process_unit(st, sh.ring[wave][k % kR], koff, qh, first + k * kStride, span.end,
+                   sh.p[wave], lane);
+  };
   unsigned k = 0;
   for (; k + kR - 1 < n_units; ++k) {
     issue(k + kR - 1);
     cdna4::wait_vmcnt<8 * (kR - 1)>();
-    process_unit(st, sh.ring[wave][k % kR], koff, qh, first + k * kStride, span.end, sh.p[wave],
-                 lane);
+    unit(k);
   }
   // Drain: the last units, already in flight.
   for (; k < n_units; ++k) {
     wait_units_after(n_units - 1 - k);
-    process_unit(st, sh.ring[wave][k % kR], koff, qh, first + k * kStride, span.end, sh.p[wave],
-                 lane);
+    unit(k);
   }
 
   write_partial(st, sh, part_m, part_l, part_o, base, more);
 }
 
-template <class Shared>
+template <DecodeArith kArith, class Shared>
 __device__ __attribute__((always_inline)) inline void split_partial(
     const float* __restrict__ q, const attn::half_t* K, const attn::half_t* V, unsigned len,
-    AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o, std::size_t base,
-    Shared& sh, bool more) {
-  split_partial_rows(q, LinearRows{K, V}, len, span, kvh, part_m, part_l, part_o, base, sh, more);
+    AttnSpan span, unsigned stride, unsigned kvh, float* part_m, float* part_l, float* part_o,
+    std::size_t base, Shared& sh, bool more) {
+  split_partial_rows<kArith>(q, LinearRows{K, V}, len, span, stride, kvh, part_m, part_l, part_o,
+                             base, sh, more);
 }
 
 }  // namespace decode_detail
 
-// Split-K flash decoding on wave64 VALU (no MFMA). Item = kvh * n_splits + split (grid-stride,
-// as the reference). Each split's keys are streamed in 8-row units: every lane loads 16 bytes of
-// K and of V per row-pair (1 KiB coalesced per wave instruction), scores use v_dot2_f32_f16
-// against the lane's f16 query slice and a DPP/crossbar reduce-scatter, the online softmax runs
-// in log2 units, and P V uses v_dot2_f32_f16 over row pairs. Output: the reference's partial
-// layout, m in natural-log units.
-template <int kBlock>
-__device__ void attn_split_op(const AttnSplitParams& p, unsigned first, unsigned count) {
-  static_assert(kBlock == 256, "four waves per split workgroup");
-  __shared__ decode_detail::SplitShared sh;
+namespace decode_detail {
+
+// Items [first, first + count) of a split launch, item = kvh * n_splits + split (grid-stride, as
+// the reference), in the given arithmetic.
+template <DecodeArith kArith>
+__device__ __attribute__((always_inline)) inline void split_items(const AttnSplitParams& p,
+                                                                  unsigned first,
+                                                                  unsigned count) {
+  static_assert(kAttnSubChunk == SplitShared::kWaveCount * kAttnDecodeUnit,
+                "a sub-chunk is one unit per wave");
+  __shared__ SplitShared sh;
   for (unsigned item = first + blockIdx.y * gridDim.x + blockIdx.x; item < first + count;
        item += gridDim.x * gridDim.y) {
     const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
     const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
     const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * attn::kDim;
-    decode_detail::split_partial(p.q, K, V, p.len, attn_split_span(p.len, p.n_splits, split),
-                                 kvh, p.part_m, p.part_l, p.part_o,
-                                 std::size_t{kvh} * p.n_splits + split, sh,
-                                 item + gridDim.x * gridDim.y < first + count);
+    split_partial<kArith>(p.q, K, V, p.len, attn_split_span(p.len, p.n_splits, split),
+                          kAttnSubChunk, kvh, p.part_m, p.part_l, p.part_o,
+                          std::size_t{kvh} * p.n_splits + split, sh,
+                          item + gridDim.x * gridDim.y < first + count);
   }
+}
+
+}  // namespace decode_detail
+
+// Split-K flash decoding on wave64 VALU (no MFMA), in the reference's arithmetic: f32 query, f32
+// scores and numerators, f32 accumulation over f16 K/V (kernels/attention_decode.hpp:150-221).
+// Each split's keys are streamed in 8-row units through per-wave LDS rings (direct global -> LDS
+// loads, 1 KiB coalesced per wave instruction); scores are v_fma_mix_f32 products of the lane's
+// f32 query slice and f16 K, summed by a DPP/crossbar reduce-scatter; the online softmax runs in
+// log2 units; P V is v_fma_mix_f32 of f32 numerators and f16 V. Output: the reference's partial
+// layout, m in natural-log units.
+template <int kBlock>
+__device__ void attn_split_op(const AttnSplitParams& p, unsigned first, unsigned count) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  decode_detail::split_items<decode_detail::DecodeArith::kF32>(p, first, count);
 }
 
 template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_split_kernel(AttnSplitParams p) {
   attn_split_op<kBlock>(p, 0, attn::kKvHeads * p.n_splits);
+}
+
+// The same split with an f16 query and f16 numerators through v_dot2_f32_f16 (two products per
+// instruction): half the VALU work of attn_split_kernel, per-head rel-L2 ~3e-4 against the FP64
+// reference instead of ~1e-6 (no reference counterpart; same launch shape and partial layout).
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_split_f16q_kernel(AttnSplitParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  decode_detail::split_items<decode_detail::DecodeArith::kF16Query>(p, 0,
+                                                                    attn::kKvHeads * p.n_splits);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -691,136 +829,110 @@ struct AttnCombineParams {
 
 namespace decode_detail {
 
-// The merge of one head at dimension d, computed by a full wave whose 64 lanes own 64 adjacent
-// dimensions of the same head. The result follows the reference's frozen FP32 order exactly:
-// M = max_c m_c; for c in split order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o);
-// core = o / L / (1 + __expf(-gate)). Split statistics are per head, hence the same for the whole
-// wave: lane c of a chunk of splits loads m_c, l_c and forms w_c (a max is order-free and w_c
-// depends only on m_c and M), the wave publishes (w_c, l_c) through LDS, and every lane then runs
-// the ordered FMA chains. A chunk past the last split is padded with w = 0 and a clamped, finite
-// o: fma(0, x, acc) == acc exactly, so the padding cannot change a bit. Every template variant
-// and the batched path use this routine, so all are bit-identical to one another and to a
-// one-thread-per-dimension serial loop.
-//
-// For 16, 64 or 128 splits (the policy's counts at the bench's contexts) all loads of the merge go
-// out at once -- m and l of the lane's splits and the lane's o of every split -- so the merge costs
-// one memory latency plus the two FMA chains; the L chain runs while the o values are in flight.
+// The merge of one head over one 64-dimension tile, computed by a full wave (lane = dimension).
+// The result follows the reference's frozen FP32 order exactly: M = max_c m_c; for c in split
+// order w = __expf(m_c - M), L = fma(w, l_c, L), o = fma(w, o_c, o); core = o / L / (1 + __expf(
+// -gate)). Split statistics are per head, hence the same for the whole wave: lane c of a chunk
+// loads m_c, l_c and forms w_c (a max is order-free and w_c depends only on m_c and M), and the
+// wave publishes (w_c, l_c) through LDS. The tile's partial rows of a chunk of up to 128 splits
+// (256 bytes each) are fetched with 16-byte loads -- lane l of load i takes split 4 i + l / 16,
+// dimensions 4 (l % 16) .. + 3 -- all issued at once (32 loads per lane, under the 63
+// outstanding loads a wave may have), and transposed through LDS, so a chunk costs one memory
+// round trip; every lane then runs the ordered FMA chains over its dimension. Chunk entries past
+// the last split are padded with w = l = 0 and a clamped, finite o: fma(0, x, acc) == acc
+// exactly, so the padding cannot change a bit. Every template variant and the batched paths use
+// this routine, so all are bit-identical to one another and to a one-thread-per-dimension serial
+// loop.
+constexpr unsigned kCombineChunk = 128;
+
 struct CombineLds {
-  float w[2 * cdna4::kLanes], l[2 * cdna4::kLanes];
+  float w[kCombineChunk], l[kCombineChunk];
+  float o[kCombineChunk][cdna4::kLanes];  // [split of the chunk][dimension of the tile]
 };
 
-// Exactly kN == n_splits splits, all in registers (kN = 16, 64 or 128).
-template <unsigned kN>
-__device__ __attribute__((always_inline)) inline float combine_wave_all(
-    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po,
-    unsigned n_splits, float gate, CombineLds& lds) {
+// One chunk of splits [base, base + nc), nc <= 4 kLoads, staged with kLoads 16-byte loads per
+// lane and merged into (L, o). M is computed from the first chunk's statistics (and, past 128
+// splits, the rest) when base == 0.
+template <unsigned kLoads>
+__device__ __attribute__((always_inline)) inline void combine_chunk(
+    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po_tile,
+    unsigned n_splits, unsigned base, float& M, float& L, float& o, CombineLds& lds) {
   constexpr unsigned kStride = kGroup;  // partial rows per split
   constexpr std::size_t kOStride = std::size_t{kStride} * attn::kDim;
-  constexpr unsigned kLanesUsed = kN < cdna4::kLanes ? kN : cdna4::kLanes;
-  constexpr unsigned kPerLane = (kN + cdna4::kLanes - 1) / cdna4::kLanes;
-  const unsigned lane = cdna4::lane_id();
-  float mv[kPerLane], lv[kPerLane];
+  const unsigned lane = cdna4::lane_id(), sub = lane >> 4, col = 4 * (lane & 15u);
+  const unsigned last = n_splits - 1;
+  float4 r[kLoads];
 #pragma unroll
-  for (unsigned j = 0; j < kPerLane; ++j) {
-    const unsigned c = j * cdna4::kLanes + lane;
-    const unsigned cc = c < n_splits ? c : 0;
-    mv[j] = pm[cc * kStride];
-    lv[j] = pl[cc * kStride];
+  for (unsigned i = 0; i < kLoads; ++i) {
+    const unsigned c = base + 4 * i + sub;
+    r[i] = *reinterpret_cast<const float4*>(po_tile + (c < last ? c : last) * kOStride + col);
   }
-  // o of every split, 8 loads at a time; the scheduling barriers keep each group's address
-  // arithmetic next to its loads instead of 128 addresses live at once.
-  float ov[kN];
+  constexpr unsigned kStat = kLoads * 4 > cdna4::kLanes ? 2 : 1;  // statistics per lane
+  float mv[kStat], lv[kStat];
 #pragma unroll
-  for (unsigned g = 0; g < kN; g += 8) {
-#pragma unroll
-    for (unsigned r = g; r < g + 8; ++r)
-      ov[r] = po[r * kOStride];
-    __builtin_amdgcn_sched_barrier(0);
+  for (unsigned j = 0; j < kStat; ++j) {
+    const unsigned c = base + cdna4::kLanes * j + lane;
+    mv[j] = c < n_splits ? pm[c * kStride] : -__builtin_inff();
+    lv[j] = c < n_splits ? pl[c * kStride] : 0.0f;
   }
-  float M = -__builtin_inff();
+  if (base == 0) {
+    M = mv[0];
 #pragma unroll
-  for (unsigned j = 0; j < kPerLane; ++j)
-    if (j * cdna4::kLanes + lane < n_splits)
+    for (unsigned j = 1; j < kStat; ++j)
       M = fmaxf(M, mv[j]);
-  M = cdna4::wave_allmax(M);
+    for (unsigned c = kCombineChunk + lane; c < n_splits; c += cdna4::kLanes)  // > 128 splits
+      M = fmaxf(M, pm[c * kStride]);
+    M = cdna4::wave_allmax(M);
+  }
 #pragma unroll
-  for (unsigned j = 0; j < kPerLane; ++j) {
-    const unsigned c = j * cdna4::kLanes + lane;
-    if (lane < kLanesUsed) {
-      lds.w[c] = c < n_splits ? __expf(mv[j] - M) : 0.0f;
-      lds.l[c] = c < n_splits ? lv[j] : 0.0f;
+  for (unsigned j = 0; j < kStat; ++j) {
+    const unsigned c = cdna4::kLanes * j + lane;
+    if (c < 4 * kLoads) {
+      lds.w[c] = base + c < n_splits ? __expf(mv[j] - M) : 0.0f;
+      lds.l[c] = lv[j];
     }
   }
+#pragma unroll
+  for (unsigned i = 0; i < kLoads; ++i)
+    *reinterpret_cast<float4*>(&lds.o[4 * i + sub][col]) = r[i];
   __builtin_amdgcn_wave_barrier();
-  float L = 0.0f;
+  // Every LDS value of the chunk into registers first (the reads pipeline), then the two ordered
+  // chains from registers. Entries past the last split have w = l = 0 and a finite o.
+  constexpr unsigned kN = 4 * kLoads;
+  float ov[kN], wv[kN], lw[kN];
 #pragma unroll
-  for (unsigned r = 0; r < kN; r += 4) {
-    const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
-    const float4 l4 = *reinterpret_cast<const float4*>(&lds.l[r]);
-    L = __builtin_fmaf(w4.x, l4.x, L);
-    L = __builtin_fmaf(w4.y, l4.y, L);
-    L = __builtin_fmaf(w4.z, l4.z, L);
-    L = __builtin_fmaf(w4.w, l4.w, L);
+  for (unsigned c = 0; c < kN; c += 4) {
+    const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[c]);
+    const float4 l4 = *reinterpret_cast<const float4*>(&lds.l[c]);
+    wv[c] = w4.x, wv[c + 1] = w4.y, wv[c + 2] = w4.z, wv[c + 3] = w4.w;
+    lw[c] = l4.x, lw[c + 1] = l4.y, lw[c + 2] = l4.z, lw[c + 3] = l4.w;
   }
-  float o = 0.0f;
 #pragma unroll
-  for (unsigned r = 0; r < kN; r += 4) {
-    const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
-    o = __builtin_fmaf(w4.x, ov[r], o);
-    o = __builtin_fmaf(w4.y, ov[r + 1], o);
-    o = __builtin_fmaf(w4.z, ov[r + 2], o);
-    o = __builtin_fmaf(w4.w, ov[r + 3], o);
+  for (unsigned c = 0; c < kN; ++c)
+    ov[c] = lds.o[c][lane];
+#pragma unroll
+  for (unsigned c = 0; c < kN; ++c) {
+    L = __builtin_fmaf(wv[c], lw[c], L);
+    o = __builtin_fmaf(wv[c], ov[c], o);
   }
-  __builtin_amdgcn_wave_barrier();  // a later merge by this wave overwrites the broadcast slots
-  return o / L / (1.0f + __expf(-gate));
+  __builtin_amdgcn_wave_barrier();  // the next chunk (or merge) overwrites the LDS
 }
 
+// po_tile points at dimension 0 of the tile in split 0's row of the head (16-byte aligned); pm /
+// pl at split 0's statistics; consecutive splits are kGroup rows apart.
 __device__ __attribute__((always_inline)) inline float combine_wave(
-    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po,
+    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po_tile,
     unsigned n_splits, float gate, CombineLds& lds) {
-  if (n_splits == 16)
-    return combine_wave_all<16>(pm, pl, po, n_splits, gate, lds);
-  if (n_splits == 64)
-    return combine_wave_all<64>(pm, pl, po, n_splits, gate, lds);
-  if (n_splits == 128)
-    return combine_wave_all<128>(pm, pl, po, n_splits, gate, lds);
-  // Other split counts: chunks of 64, the loads of one chunk in flight at a time.
-  constexpr unsigned kChunk = cdna4::kLanes, kStride = kGroup;
-  constexpr std::size_t kOStride = std::size_t{kStride} * attn::kDim;
-  const unsigned lane = cdna4::lane_id();
-  float M = -__builtin_inff();
-  for (unsigned c = lane; c < n_splits; c += kChunk)
-    M = fmaxf(M, pm[c * kStride]);
-  M = cdna4::wave_allmax(M);
-  const unsigned last = n_splits - 1;
-  float L = 0.0f, o = 0.0f;
-  for (unsigned base = 0; base < n_splits; base += kChunk) {
-    float ov[kChunk];
-#pragma unroll
-    for (unsigned r = 0; r < kChunk; ++r) {
-      const unsigned c = base + r < last ? base + r : last;
-      ov[r] = po[c * kOStride];
-    }
-    const unsigned mine = base + lane;
-    const float w_l = mine < n_splits ? __expf(pm[mine * kStride] - M) : 0.0f;
-    const float l_l = mine < n_splits ? pl[mine * kStride] : 0.0f;
-    lds.w[lane] = w_l;
-    lds.l[lane] = l_l;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (unsigned r = 0; r < kChunk; r += 4) {
-      const float4 w4 = *reinterpret_cast<const float4*>(&lds.w[r]);
-      const float4 l4 = *reinterpret_cast<const float4*>(&lds.l[r]);
-      L = __builtin_fmaf(w4.x, l4.x, L);
-      o = __builtin_fmaf(w4.x, ov[r], o);
-      L = __builtin_fmaf(w4.y, l4.y, L);
-      o = __builtin_fmaf(w4.y, ov[r + 1], o);
-      L = __builtin_fmaf(w4.z, l4.z, L);
-      o = __builtin_fmaf(w4.z, ov[r + 2], o);
-      L = __builtin_fmaf(w4.w, l4.w, L);
-      o = __builtin_fmaf(w4.w, ov[r + 3], o);
-    }
-    __builtin_amdgcn_wave_barrier();  // the next chunk overwrites the broadcast slots
+  float L = 0.0f, o = 0.0f, M = -__builtin_inff();
+  if (n_splits <= 16) {
+    combine_chunk<4>(pm, pl, po_tile, n_splits, 0, M, L, o, lds);
+  } else if (n_splits <= 32) {
+    combine_chunk<8>(pm, pl, po_tile, n_splits, 0, M, L, o, lds);
+  } else if (n_splits <= 64) {
+    combine_chunk<16>(pm, pl, po_tile, n_splits, 0, M, L, o, lds);
+  } else {
+    for (unsigned base = 0; base < n_splits; base += kCombineChunk)
+      combine_chunk<kCombineChunk / 4>(pm, pl, po_tile, n_splits, base, M, L, o, lds);
   }
   return o / L / (1.0f + __expf(-gate));
 }
@@ -838,13 +950,15 @@ __device__ void attn_combine_op(const AttnCombineParams& p, unsigned first, unsi
   static_assert(!kPrepared || kBlock == cdna4::kLanes);
   static_assert(kPipeline == 1 || (kPrepared && kPipeline == 4));
   __shared__ decode_detail::CombineLds lds[kBlock / cdna4::kLanes];
+  const unsigned wave = threadIdx.x / cdna4::kLanes;
   for (unsigned item = first + blockIdx.x; item < first + count; item += gridDim.x) {
-    const unsigned h = item / kTiles, d = (item % kTiles) * kBlock + threadIdx.x;
+    const unsigned h = item / kTiles, d0 = (item % kTiles) * kBlock + cdna4::kLanes * wave;
+    const unsigned d = d0 + cdna4::lane_id();
     const unsigned kvh = h / kGroup, hl = h % kGroup;
     const std::size_t i0 = std::size_t{kvh} * p.n_splits * kGroup + hl;
     p.core[h * kDim + d] = decode_detail::combine_wave(
-        p.part_m + i0, p.part_l + i0, p.part_o + i0 * kDim + d, p.n_splits,
-        p.qg[h * 2 * kDim + kDim + d], lds[threadIdx.x / cdna4::kLanes]);
+        p.part_m + i0, p.part_l + i0, p.part_o + i0 * kDim + d0, p.n_splits,
+        p.qg[h * 2 * kDim + kDim + d], lds[wave]);
   }
 }
 
@@ -902,11 +1016,10 @@ __global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedPar
   if (split >= n_splits)
     return;
   const std::size_t kv0 = p.kv_offsets[seq] + std::size_t{kvh} * len * attn::kDim;
-  decode_detail::split_partial(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
-                               p.k_cache + kv0, p.v_cache + kv0, len,
-                               attn_split_span(len, n_splits, split), kvh, p.part_m, p.part_l,
-                               p.part_o, (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
-                               sh, false);
+  decode_detail::split_partial<decode_detail::DecodeArith::kF32>(
+      p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, p.k_cache + kv0, p.v_cache + kv0, len,
+      attn_split_span(len, n_splits, split), kAttnSubChunk, kvh, p.part_m, p.part_l, p.part_o,
+      (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
 }
 
 // One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's.
@@ -927,8 +1040,8 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
   const std::size_t i0 = (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max * kGroup + hl;
   __shared__ decode_detail::CombineLds lds;
   p.core[out] = decode_detail::combine_wave(p.part_m + i0, p.part_l + i0,
-                                           p.part_o + i0 * attn::kDim + d, n_splits, p.gate[out],
-                                           lds);
+                                           p.part_o + i0 * attn::kDim + (d - threadIdx.x),
+                                           n_splits, p.gate[out], lds);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -969,11 +1082,10 @@ __global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParam
       p.k_pages, p.v_pages, p.page_table + std::size_t{seq} * p.max_pages, p.log2_page,
       std::size_t{2} * attn::kDim << p.log2_page,
       std::size_t{kvh} * attn::kDim << p.log2_page};
-  decode_detail::split_partial_rows(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, rows,
-                                    len, attn_split_span(len, n_splits, split), kvh, p.part_m,
-                                    p.part_l, p.part_o,
-                                    (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
-                                    sh, false);
+  decode_detail::split_partial_rows<decode_detail::DecodeArith::kF32>(
+      p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, rows, len,
+      attn_split_span(len, n_splits, split), kAttnSubChunk, kvh, p.part_m, p.part_l, p.part_o,
+      (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
 }
 
 }  // namespace miso::kernels

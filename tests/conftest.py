@@ -65,6 +65,13 @@ def to_host(t) -> np.ndarray:
     return t.cpu().numpy()
 
 
+# The reference's own accuracy gate for its decode and prefill kernels: per-(token, head) relative
+# L2 error against the FP64 host reference <= 1e-5 (tests/test_attn_splitk.hip:174, :267). The
+# f32-arithmetic decode paths are held to it on top of the elementwise north-star tolerance.
+REF_REL_L2 = 1e-5
+
+
 def report(name: str, stats: dict) -> None:
     print(f"[{name}] max_abs={stats['max_abs']:.3e} max_rel={stats['max_rel']:.3e} "
-          f"rel_l2={stats['rel_l2']:.3e} bad={stats['n_bad']}", flush=True)
+          f"rel_l2={stats['rel_l2']:.3e} rel_l2_head={stats['rel_l2_head']:.3e} "
+          f"bad={stats['n_bad']}", flush=True)

@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import report, to_dev, to_host
+from conftest import REF_REL_L2, report, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -29,6 +29,7 @@ def test_decode_full_262k_cache(O, attn, torch_mod, n_splits):
     st = O.compare(got, ref)
     report(f"decode len={length} splits={n_splits}", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
 
 
 def test_prefill_chunk_after_128k_prefix(O, attn, torch_mod):
@@ -65,6 +66,7 @@ def test_ragged_sequence_far_past_max_len(O, attn, torch_mod):
     st = O.compare(got, ref)
     report("ragged far past max_len", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
 
 
 def test_decode_fp8_full_262k_cache(O, attn, torch_mod):

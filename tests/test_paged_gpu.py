@@ -6,7 +6,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import report, to_dev, to_host
+from conftest import REF_REL_L2, report, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -76,6 +76,7 @@ def test_paged_long_spans_read_table_beyond_lane_slice(O, attn, torch_mod):
     st = O.compare(paged, ref)
     report("paged long spans", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
 
 
 def test_paged_c5_shape(O, attn, torch_mod):

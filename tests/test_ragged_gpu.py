@@ -6,7 +6,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import report, to_dev, to_host
+from conftest import REF_REL_L2, report, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +34,7 @@ def test_ragged_c5(O, attn, torch_mod):
     st = O.compare(got, ref)
     report(f"C5 sum_len={int(lens.sum())}", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
 
 
 def test_ragged_edges(O, attn, torch_mod):
@@ -45,6 +46,7 @@ def test_ragged_edges(O, attn, torch_mod):
         ref = O.ragged_f64(r["q"], r["gate"], r["k"], r["v"], r["offsets"], lens)
         st = O.compare(got, ref)
         assert st["ok"], (max_len, st)
+        assert st["rel_l2_head"] <= REF_REL_L2, (max_len, st)
 
 
 def test_ragged_empty_sequence_is_zero(O, attn, torch_mod):

@@ -9,7 +9,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import report, to_dev, to_host
+from conftest import REF_REL_L2, report, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -50,6 +50,7 @@ def test_decode_late_max_moves(O, attn, torch_mod, length, n_splits):
     st = O.compare(got, ref)
     report(f"decode rescale len={length} splits={n_splits}", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
 
 
 @pytest.mark.parametrize("pos0,n", [(0, 300), (1000, 64), (37, 50)])
@@ -104,3 +105,4 @@ def test_ragged_late_max_moves(O, attn, torch_mod):
     st = O.compare(got, ref)
     report("ragged rescale", st)
     assert st["ok"], st
+    assert st["rel_l2_head"] <= REF_REL_L2, st
