@@ -113,6 +113,19 @@ int miso_attn_decode_f16q(const float* q, const float* qg, const uint16_t* k_cac
                           float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
                           void* stream);
 
+/* miso_attn_decode without caller scratch (no reference counterpart; for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The split partials live in the library's own device array of
+ * MISO_ATTN_NOALLOC_MAX_SPLITS splits (2,105,344 bytes per GPU, held until the process ends);
+ * the call itself allocates nothing. Same kernels, arguments and results as miso_attn_decode
+ * (bit-identical outputs). Rejects n_splits == 0 or n_splits > MISO_ATTN_NOALLOC_MAX_SPLITS, and
+ * the arguments miso_attn_decode rejects. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (different streams or host threads without ordering) race. */
+#define MISO_ATTN_NOALLOC_MAX_SPLITS 128
+int miso_attn_decode_noalloc(const float* q, const float* qg, const uint16_t* k_cache,
+                             const uint16_t* v_cache, float* core, uint32_t len, uint32_t max_ctx,
+                             uint32_t n_splits, void* stream);
+
 /* Causal prefill: replaces attn_prefill_kernel<256><<<attn_prefill_items(n), 256, 0, stream>>>(
  * AttnPrefillParams{...}), src/engine/attention.hip:141-144 and tests/test_attn_splitk.hip:224-233
  * (kernels/attention_prefill.hpp:42-161). Tokens pos0 .. pos0 + n - 1; q [n][16][256] (unscaled),

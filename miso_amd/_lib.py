@@ -27,6 +27,7 @@ SIGNATURES = {
                                           c_uint32, P]),
     "miso_attn_decode": (c_int, [P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_decode_f16q": (c_int, [P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
+    "miso_attn_decode_noalloc": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_prefill": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_ragged_splits": (c_uint32, [c_uint32]),
     "miso_attn_ragged_partials": (c_uint64, [c_uint32, c_uint32]),

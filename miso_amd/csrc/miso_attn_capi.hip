@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/miso_attn.h"
@@ -97,6 +98,47 @@ bool any_bad(const P*... p) {
 constexpr const char* kBadPtr = "a tensor pointer is NULL or not 16-byte aligned";
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// The split partials of miso_attn_decode_noalloc: part_o [2][128][8][256], then part_m and
+// part_l [2][128][8] (2,105,344 bytes per device).
+constexpr uint32_t kNoAllocMaxSplits = MISO_ATTN_NOALLOC_MAX_SPLITS;
+constexpr std::size_t kNoAllocStats = std::size_t{2} * kNoAllocMaxSplits * 8;
+constexpr std::size_t kNoAllocFloats = kNoAllocStats * 256 + 2 * kNoAllocStats;
+
+}  // namespace
+
+// Device memory of the allocation-free decode (one copy per GPU, alive until the process ends).
+// Host code never uses this name as an address: each device's copy is reached through the
+// pointer hipGetSymbolAddress returns for it (noalloc_scratch below).
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's current device's copy of `scratch`, looked up once per device (with that
+// device current) and kept; nullptr with a message on failure.
+float* noalloc_scratch(const char* fn) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(fn, "no usable current device (hipGetDevice failed or id >= 64)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      g_last_error = std::string(fn) + ": hipGetSymbolAddress(scratch) failed: " +
+                     hipGetErrorName(err);
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
 const half_t* as_half(const uint16_t* p) { return reinterpret_cast<const half_t*>(p); }
 half_t* as_half(uint16_t* p) { return reinterpret_cast<half_t*>(p); }
 
@@ -240,6 +282,30 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
   if (rc != 0)
     return rc;
   return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
+}
+
+int miso_attn_decode_noalloc(const float* q, const float* qg, const uint16_t* k_cache,
+                             const uint16_t* v_cache, float* core, uint32_t len, uint32_t max_ctx,
+                             uint32_t n_splits, void* stream) {
+  constexpr const char* fn = "miso_attn_decode_noalloc";
+  if (any_bad(q, qg, k_cache, v_cache, core))
+    return fail(fn, kBadPtr);
+  if (len == 0)
+    return fail(fn, "len must be >= 1");
+  if (len > max_ctx)
+    return fail(fn, "len exceeds max_ctx");
+  if (n_splits == 0 || n_splits > kNoAllocMaxSplits)
+    return fail(fn, "n_splits must be in [1, MISO_ATTN_NOALLOC_MAX_SPLITS = 128]");
+  float* const base = noalloc_scratch(fn);
+  if (base == nullptr)
+    return MISO_ATTN_EINVAL;
+  // Every partial the combine reads is written by the split first (empty spans included), so
+  // nothing is cleared between calls.
+  float* const part_o = base;
+  float* const part_m = base + kNoAllocStats * 256;
+  float* const part_l = part_m + kNoAllocStats;
+  return miso_attn_decode(q, qg, k_cache, v_cache, core, part_m, part_l, part_o, len, max_ctx,
+                          n_splits, stream);
 }
 
 int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,

@@ -60,6 +60,10 @@ def test_host_validation_rejects_bad_arguments(lib):
     rejected(lib.miso_attn_split(P, P, P, P, P, P, 5, 10, 0, N), lib, "n_splits")
     rejected(lib.miso_attn_combine(P, P, P, P, P, 0, N), lib, "n_splits")
     rejected(lib.miso_attn_decode(P, P, P, P, P, P, P, P, 0, 10, 4, N), lib, "len must be")
+    # the allocation-free decode rejects split counts beyond its array before touching a device
+    rejected(lib.miso_attn_decode_noalloc(P, P, P, P, P, 5, 10, 129, N), lib, "n_splits")
+    rejected(lib.miso_attn_decode_noalloc(P, P, P, P, P, 5, 10, 0, N), lib, "n_splits")
+    rejected(lib.miso_attn_decode_noalloc(P, P, P, P, P, 11, 10, 4, N), lib, "max_ctx")
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 0, 10, 8192, N), lib, "n must be >= 1")
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 8, 3, 10, 8192, N), lib, "KV cache is full")
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 3, 10, 100, N), lib, "qg_stride")
