@@ -8,7 +8,9 @@
 //                    softmax in f32 registers, sigmoid gate fused into the output store.
 //
 // Source-compatible drop-in for miso's kernels/attention_prefill.hpp (same structs, field order,
-// kernel names and template parameters; attn_prefill_items sizes the caller's grid).
+// kernel names and template parameters; attn_prefill_items sizes the caller's grid). The MFMAs
+// are issued from inline assembly so that O holds the AGPR file and the scores stay in VGPRs;
+// the wait states the compiler would add around them are explicit (drain_pv, the step's s_nop).
 
 #include <hip/hip_runtime.h>
 
@@ -61,15 +63,22 @@ struct AttnPrefillParams {
   unsigned qg_stride;  // 8192 packed, or 9216 when q/k/v share a proj buffer
 };
 
-// Tokens per workgroup: 4 waves x 4 tokens; a wave's 4 tokens x 8 query heads are the 32 rows of
-// one MFMA column block.
+// Tokens per workgroup. Each wave owns 4 tokens x 8 query heads per 32-row MFMA column block;
+// short launches give each wave one block (16 tokens per workgroup, so more workgroups share a
+// causal prefill), launches of kAttnWideMin tokens or more two blocks (32 tokens per workgroup:
+// each K and V operand read from LDS feeds two MFMAs).
 constexpr unsigned kAttnQBlock = 16;
+constexpr unsigned kAttnWideMin = 4096;
+__host__ __device__ constexpr unsigned attn_prefill_row_blocks(unsigned n) {
+  return n >= kAttnWideMin ? 2 : 1;
+}
 
 // Grid size. Items come in groups of 8 (one per XCD of the round-robin dispatch): slots 0-3 of a
 // group serve KV head 0 and slots 4-7 KV head 1, so each XCD's L2 holds one KV head's stream, and
 // ranks are handed out heaviest token block first. Slots past the last block exit at once.
 __host__ __device__ inline unsigned attn_prefill_items(unsigned n) {
-  const unsigned blocks = (n + kAttnQBlock - 1) / kAttnQBlock;
+  const unsigned tokens = kAttnQBlock * attn_prefill_row_blocks(n);
+  const unsigned blocks = (n + tokens - 1) / tokens;
   return 8 * ((blocks + 3) / 4);
 }
 
@@ -91,8 +100,12 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: numerators stay <= 2^8 bet
 // base plus a compile-time offset below 64 KiB (the ring slot is folded into the offset).
 constexpr unsigned kVBase = kStages * kTileBytes;
 // 1 KiB alignment keeps the base clear of the address bits the swizzle XORs (4-8).
+// After the ring: each wave's Q^T B operands of its second row block (16 k-steps x 64 lanes x
+// 16 bytes), read from LDS per tile instead of occupying 64 more VGPRs.
+constexpr unsigned kQ1Bytes = 16 * 64 * 16;
 struct alignas(1024) Shared {
   unsigned char kv[2 * kStages * kTileBytes];
+  unsigned char q1[4][kQ1Bytes];
 };
 
 // 16-byte chunk c of tile row r lives at chunk position c ^ s(r) of that row (64 banks of 4 bytes
@@ -168,23 +181,58 @@ __device__ __attribute__((always_inline)) inline half4_t read_tr(unsigned addr) 
   return __builtin_bit_cast(half4_t, raw);
 }
 
-// Per-lane state of one wave (32 query rows = one MFMA column block): the Q^T B operands, dims
-// 16 s + 8 hi + j of the lane's row, x log2(e)/16; the reference max m and running sum l; and -m
-// in all 16 elements, the initial S^T accumulator, so the scores come out of the MFMAs relative
-// to m.
-struct Rows {
-  half8_t q[16];
-  float m, l;
-  float16_t negm;
+// One instruction of copy_tile, issued on its own so a tile's copy can be spread between MFMAs:
+// instruction i (< 4: K row pair i of this wave's 8 rows, else V row pair i - 4), lane offset
+// `off` from the tile's first row `row0`, to LDS byte `lds` + 1024 (i % 4) + 16 lane. M0 is
+// saved and restored.
+template <unsigned kI>
+__device__ __attribute__((always_inline)) inline void copy_one(const void* row0, unsigned off,
+                                                               unsigned lds) {
+  static_assert(kI < 8, "eight instructions per wave and tile");
+  unsigned saved;
+  if constexpr (kI % 4 == 0)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(off), "s"(row0), "s"(lds) : "memory");
+  else if constexpr (kI % 4 == 1)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2 offset:1024\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(off), "s"(row0), "s"(lds) : "memory");
+  else if constexpr (kI % 4 == 2)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2 offset:2048\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(off), "s"(row0), "s"(lds) : "memory");
+  else
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2 offset:3072\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(off), "s"(row0), "s"(lds) : "memory");
+}
+
+// Where a tile copy goes: the tile's first K and V rows (wave-uniform), this wave's 4 KiB of the
+// K and V slots, and the lane's offsets (copy_tile's koff / voff).
+struct TileCopy {
+  const attn::half_t* kt;
+  const attn::half_t* vt;
+  unsigned k_lds, v_lds;
 };
 
-__device__ __attribute__((always_inline)) inline float16_t splat16(float x) {
-  float16_t v;
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    v[r] = x;
-  return v;
-}
+// Per-lane state of one wave: two MFMA column blocks of 32 query rows (block c: tokens
+// 4 c .. 4 c + 3 of the wave's 8, row n = token n / 8, head n % 8; the lane holds row col =
+// lane % 32 of each). q0: block 0's Q^T B operands, dims 16 s + 8 hi + j of the lane's row,
+// x log2(e)/16 (block 1's are in LDS at q1 + 1024 s + 16 lane). m[c]: the reference max in log2
+// units (-inf before the first tile); l[c]: the lane half's share of the running sum.
+struct Rows2 {
+  half8_t q0[16];
+  unsigned q1;
+  float m[2], l[2];
+};
+
+// A decided tile of both blocks: its numerators as P^T B operands, [block][key step]; k-slot
+// 8 hi + j of key step k holds key 16 k + 4 hi + (j < 4 ? j : j + 4) of the tile, which is how
+// the S^T accumulator elements lie in the lane.
+struct Numer {
+  half8_t p[2][2];
+};
 
 // max(a, b, c) in one instruction (the scores are never NaN; no canonicalisation is needed).
 __device__ __attribute__((always_inline)) inline float max3(float a, float b, float c) {
@@ -199,17 +247,6 @@ __device__ __attribute__((always_inline)) inline float max3(float a, float b, fl
 __device__ __attribute__((always_inline)) inline unsigned opaque(unsigned x) {
   asm volatile("" : "+v"(x));
   return x;
-}
-
-// S^T[key][row] = K Q^T for one tile (32 keys x 32 rows): 16 k-steps over head_dim. kb: the
-// lane's operand address in the tile's slot before the per-step XOR.
-__device__ __attribute__((always_inline)) inline float16_t scores(const Rows& rw, unsigned kb) {
-  float16_t s{};
-#pragma unroll
-  for (unsigned st = 0; st < 16; ++st)
-    s = __builtin_amdgcn_mfma_f32_32x32x16_f16(lds_read_b128(kb ^ (32u * st)), rw.q[st], s, 0, 0,
-                                               0);
-  return s;
 }
 
 // o *= c for accumulators that live in AGPRs, element by element in place (read to a VGPR,
@@ -233,70 +270,26 @@ __device__ __attribute__((always_inline)) inline void scale_acc(float16_t (&o)[8
     }
 }
 
-// The scores of one tile as the softmax consumes them: S^T values of the lane (keys 8 (r / 4) +
-// 4 hi + r % 4 of the tile, row col) in log2 units relative to the reference max m, with the
-// causal mask applied, and the factor by which O and l were scaled when m moved for this tile.
-struct Pending {
-  float s[16];
-  float corr;
-};
-
-// Scores of a finished S^T accumulator (relative to m) -> Pending: mask (keys past lim, diagonal
-// tiles only), row max over the 32 keys (16 per lane half), and the lazy rescale decision: m
-// moves only when the tile exceeds it by more than the slack, wave-uniformly. The work is split
-// into part(0) .. part(4) so it can sit between MFMAs; after part(4), `moved` says whether m moved
-// (by `delta` >= 0 in the lane's row), and the caller must then finish(): shift the pending
-// scores, reset the accumulator init, and scale O by pend.corr before the tile's P V is added.
+// Softmax decision for one block of one tile. `acc`: the block's S^T accumulator (raw scores in
+// log2 units; element r = key k0 + 8 (r / 4) + 4 hi + r % 4, the lane's row). Keys past `lim` are
+// masked when kMasked. The reference max m moves only when the tile's row max exceeds it by more
+// than the slack (2^8), decided wave-wide so the rescale branch is uniform; on the first tile (m =
+// -inf) it always moves. Writes the f16 numerators 2^(s - m) as the block's two P^T operands,
+// updates l = l corr + their sum (the sum of the rounded values the MFMAs use), and returns
+// corr = 2^(m_old - m_new), the factor the block's O must be scaled by (1 if m stayed; `moved`
+// says whether any lane's m moved).
 template <bool kMasked>
-struct Decide {
-  float run, delta;
-  bool moved;
-  __device__ __attribute__((always_inline)) inline void part(unsigned i, const float16_t& acc,
-                                                              Pending& pend, Rows& rw, unsigned k0,
-                                                              unsigned lim, unsigned hi) {
-    if (i < 4) {  // read 4 scores, mask, running max
-#pragma unroll
-      for (unsigned j = 0; j < 4; ++j) {
-        const unsigned r = 4 * i + j;
-        float x = acc[r];
-        asm volatile("" : "+v"(x));  // the pending scores live in VGPRs, not in the accumulator
-        if (kMasked) {
-          const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
-          x = key <= lim ? x : -__builtin_inff();
-        }
-        pend.s[r] = x;
-      }
-      const float* v = pend.s + 4 * i;
-      run = i == 0 ? max3(v[0], v[1], v[2]) : max3(run, v[0], v[1]);
-      run = i == 0 ? max3(run, v[3], v[3]) : max3(run, v[2], v[3]);
-    } else if (i == 4) {
-      const float mx = cdna4::max_xor32(run);
-      moved = __builtin_amdgcn_ballot_w64(mx > kRescaleSlack) != 0;
-      delta = moved ? fmaxf(mx, 0.0f) : 0.0f;
-      pend.corr = __builtin_amdgcn_exp2f(-delta);
-      rw.m += delta;
-    }
-  }
-  __device__ __attribute__((always_inline)) inline void finish(Pending& pend, Rows& rw) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      pend.s[r] -= delta;
-    rw.negm = splat16(-rw.m);
-    asm volatile("" : "+a"(rw.negm));  // kept where the MFMA reads its accumulator input
-  }
-};
-
-// The first tile of an item: O and l are still 0, so m is simply the tile's row max.
-template <bool kMasked>
-__device__ __attribute__((always_inline)) inline void first_tile(const float16_t& acc,
-                                                                Pending& pend, Rows& rw,
-                                                                unsigned lim, unsigned hi) {
+__device__ __attribute__((always_inline)) inline float decide_block(const float16_t& acc,
+                                                                   float& m, float& l,
+                                                                   half8_t (&pb)[2], unsigned k0,
+                                                                   unsigned lim, unsigned hi,
+                                                                   bool& moved) {
   float x[16];
 #pragma unroll
   for (unsigned r = 0; r < 16; ++r) {
     x[r] = acc[r];
     if (kMasked) {
-      const unsigned key = 8 * (r / 4) + 4 * hi + (r % 4);
+      const unsigned key = k0 + 8 * (r / 4) + 4 * hi + (r % 4);
       x[r] = key <= lim ? x[r] : -__builtin_inff();
     }
   }
@@ -304,157 +297,245 @@ __device__ __attribute__((always_inline)) inline void first_tile(const float16_t
 #pragma unroll
   for (int r = 3; r < 15; r += 2)
     run = max3(run, x[r], x[r + 1]);
-  rw.m = cdna4::max_xor32(fmaxf(run, x[15]));  // finite: key 0 is visible to every row
+  const float mx = cdna4::max_xor32(fmaxf(run, x[15]));
+  moved = __builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0;
+  float corr = 1.0f;
+  if (moved) {
+    const float mn = fmaxf(m, mx);
+    corr = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile (m = -inf)
+    m = mn;
+  }
+  const cdna4::half2_t ones{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  cdna4::half2_t e2[8];
+  float lsum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r)
-    pend.s[r] = x[r] - rw.m;
-  pend.corr = 0.0f;
-  rw.negm = splat16(-rw.m);
-  asm volatile("" : "+a"(rw.negm));
+  for (int j = 0; j < 8; ++j) {
+    e2[j] = cdna4::half2_t{static_cast<_Float16>(__builtin_amdgcn_exp2f(x[2 * j] - m)),
+                           static_cast<_Float16>(__builtin_amdgcn_exp2f(x[2 * j + 1] - m))};
+    lsum = __builtin_amdgcn_fdot2(e2[j], ones, lsum, false);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    pb[h] = half8_t{e2[4 * h][0],     e2[4 * h][1],     e2[4 * h + 1][0], e2[4 * h + 1][1],
+                    e2[4 * h + 2][0], e2[4 * h + 2][1], e2[4 * h + 3][0], e2[4 * h + 3][1]};
+  l = l * corr + lsum;
+  return corr;
 }
 
-// One tile of a wave, software-pipelined: tile ti's softmax numerators (from `cur`, decided in
-// the previous step), O += V^T(ti) P^T(ti), and the scores of tile ti + 1 (kNext), which are
-// decided at the end into `cur` for the next step. Three groups of MFMAs, each with the VALU work
-// that depends only on earlier groups, interleaved one MFMA at a time (scheduling barriers):
-//   A: S(ti + 1) k-steps 0-7; numerators of keys r = 0-7 -> P half 0, their sum;
-//   B: S(ti + 1) k-steps 8-15 alternating with the P V MFMAs of key step 0; numerators r = 8-15;
-//   C: the P V MFMAs of key step 1; scores of tile ti + 1 read, masked (kMaskNext) and decided.
-// If m moved for tile ti + 1, O (now holding every tile <= ti) is rescaled at the end.
-// k-slot 8 hi + j of a P V step holds key 16 step + 4 hi + (j < 4 ? j : j + 4), which is how the
-// S^T accumulator rows lie in the lane, so P^T is the numerators as they are. kb: K operand
-// address in slot 0 and
-// k_off the byte offset of tile ti + 1's slot; vb[c] + v_off: the V^T transpose-read address of
-// 32-dim block c (rows 0-7 of key step 0) in tile ti's slot. Block b + 4 lies 256 bytes above
-// block b and rows 8-15 4096 +- 256 bytes above rows 0-7, so four lane bases serve all 32 reads
-// (the rest are instruction offsets).
-template <bool kMaskNext, bool kNext>
-__device__ __attribute__((always_inline)) inline void tile_step(Pending& cur, Rows& rw,
-                                                               float16_t (&o)[8], unsigned kb,
-                                                               unsigned k_off,
-                                                               const unsigned (&vb)[4],
-                                                               unsigned v_off, unsigned k0_next,
-                                                               unsigned lim, unsigned hi) {
+// o += a b on the MFMA unit with the accumulator in AGPRs. Written as assembly so that O holds
+// the AGPR file and the score accumulators (builtin MFMAs) stay in VGPRs, where the softmax reads
+// them. The accumulator input is the output (exactly overlapping, which the hardware chains
+// without wait states); every VALU access to o goes through scale_acc or the epilogue, both
+// behind explicit wait states, and the B operands are rewritten only after drain_pv().
+__device__ __attribute__((always_inline)) inline void pv_mfma(float16_t& o, const half8_t& a,
+                                                             const half8_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(o) : "v"(a), "v"(b));
+}
+
+// s = a b (first k-step, zero accumulator input) and s += a b on the MFMA unit with the score
+// accumulator in VGPRs; the early-clobber output keeps the destination apart from the operands.
+__device__ __attribute__((always_inline)) inline void s_mfma_first(float16_t& s, const half8_t& a,
+                                                                  const half8_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(s) : "v"(a), "v"(b));
+}
+__device__ __attribute__((always_inline)) inline void s_mfma(float16_t& s, const half8_t& a,
+                                                            const half8_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(s) : "v"(a), "v"(b));
+}
+
+// Wait states after an MFMA before a VALU reads its result or writes its operand registers (more
+// than the 8-pass MFMA's 10). The MFMAs are assembly, so the compiler does not insert them.
+__device__ __attribute__((always_inline)) inline void drain_pv() {
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+// S^T = K Q^T of one tile for both blocks: 16 k-steps over head_dim, each K operand read once
+// for two MFMAs. kb: the lane's operand address in the tile's slot before the per-step XOR.
+template <int kBlocks>
+__device__ __attribute__((always_inline)) inline void scores2(const Rows2& rw, unsigned kb,
+                                                             float16_t (&s)[kBlocks]) {
+  kb = opaque(kb);  // the 16 swizzled addresses are formed at their reads, not kept live
+#pragma unroll
+  for (unsigned st = 0; st < 16; ++st) {
+    const half8_t ka = lds_read_b128(kb ^ (32u * st));
+    if (st == 0)
+      s_mfma_first(s[0], ka, rw.q0[0]);
+    else
+      s_mfma(s[0], ka, rw.q0[st]);
+    if constexpr (kBlocks == 2) {
+      const half8_t q1 = lds_read_b128(rw.q1 + 1024u * st);
+      if (st == 0)
+        s_mfma_first(s[1], ka, q1);
+      else
+        s_mfma(s[1], ka, q1);
+    }
+  }
+  drain_pv();  // the scores are read by the softmax next
+}
+
+// One tile ti of a wave, software-pipelined over two groups of MFMAs (scheduling barriers keep
+// the interleave):
+//   A: S^T(ti + 1) of both blocks (32 MFMAs; each K operand read once for two) with O +=
+//      V^T(ti) P^T(ti) for key step 0 (16 MFMAs: 8 dimension blocks x 2 row blocks, each V^T
+//      operand read once for two), one P V MFMA after every second S MFMA, and the copy of tile
+//      ti + 2 (kCopy) spread one instruction per two k-steps;
+//   B: O += V^T(ti) P^T(ti) for key step 1 (16 MFMAs) with the decisions and numerators of tile
+//      ti + 1 for both blocks (kNext; masked when kMaskNext) into `cur`.
+// A block whose m moved for tile ti + 1 has its O (holding every tile <= ti) rescaled at the end.
+// kb: K operand address in slot 0, k_off the byte offset of tile ti + 1's slot; vb[c] + v_off:
+// the V^T transpose-read address of 32-dim block c (rows 0-7 of key step 0) in tile ti's slot.
+// Block b + 4 lies 256 bytes above block b and rows 8-15 4096 +- 256 bytes above rows 0-7, so four
+// lane bases serve all 32 reads (the rest are instruction offsets).
+template <int kBlocks, bool kMaskNext, bool kNext>
+__device__ __attribute__((always_inline)) inline void tile_step2(
+    Numer& cur, Rows2& rw, float16_t (&o)[kBlocks][8], unsigned kb, unsigned k_off,
+    const unsigned (&vb)[4], unsigned v_off, unsigned k0_next, const unsigned (&lim)[2],
+    unsigned hi, bool do_copy, const TileCopy& cp, const unsigned (&koff)[4],
+    const unsigned (&voff)[4]) {
+  // Wait states between VALU writes of this step's MFMA operands -- the numerators (written by
+  // the previous decision and moved into `cur`), O (zeroed, or rescaled by scale_acc) -- and the
+  // first MFMA reading them; the MFMAs are assembly, so the compiler does not insert them.
+  asm volatile("s_nop 4" ::: "memory");
   const unsigned ks = kb + k_off;  // k_off has no bits below 14: the XORs below commute with it
   unsigned vt[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     vt[c] = opaque(vb[c] + v_off);
-  half8_t ka[16];
-  float16_t s_acc;
+  half8_t ka[16], qa[16];
+  float16_t s[kBlocks];
   auto kread = [&](unsigned st) __attribute__((always_inline)) {
-    if (kNext && st < 16)
+    if (kNext && st < 16) {
       ka[st] = lds_read_b128(ks ^ (32u * st));
+      if (kBlocks == 2)
+        qa[st] = lds_read_b128(rw.q1 + 1024u * st);
+    }
   };
   auto smma = [&](unsigned st) __attribute__((always_inline)) {
-    if (kNext)
-      s_acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st], rw.q[st],
-                                                     st == 0 ? rw.negm : s_acc, 0, 0, 0);
+    if (kNext) {
+      if (st == 0) {
+        s_mfma_first(s[0], ka[0], rw.q0[0]);
+        if constexpr (kBlocks == 2)
+          s_mfma_first(s[1], ka[0], qa[0]);
+      } else {
+        s_mfma(s[0], ka[st], rw.q0[st]);
+        if constexpr (kBlocks == 2)
+          s_mfma(s[1], ka[st], qa[st]);
+      }
+    }
   };
-  // V^T operands in MFMA order (key step 0 for blocks 0-7, then key step 1), four ahead.
-  constexpr unsigned kAhead = 4;
-  half4_t vlo[kAhead], vup[kAhead];
+  // V^T operands in MFMA order (dimension blocks 0-7 of key step 0, then of key step 1), each
+  // used by both row blocks, three ahead.
+  constexpr unsigned kAhead = 3;
+  half8_t va[kAhead];
   auto vread = [&](unsigned i) __attribute__((always_inline)) {
     if (i < 16) {
       const unsigned b = i % 8, step = i / 8;
       const unsigned at = vt[b % 4] + 256u * (b / 4) + 8192u * step;
-      vlo[i % kAhead] = read_tr(at);
-      vup[i % kAhead] = read_tr(at + (b < 4 ? 4096u + 256u : 4096u - 256u));
+      const half4_t lo = read_tr(at);
+      const half4_t up = read_tr(at + (b < 4 ? 4096u + 256u : 4096u - 256u));
+      va[i % kAhead] = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
     }
   };
-  half8_t p[2];
-  auto pv = [&](unsigned i) __attribute__((always_inline)) {
-    const half4_t lo = vlo[i % kAhead], up = vup[i % kAhead];
-    const half8_t av = half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-    vread(i + kAhead);
-    o[i % 8] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, p[i / 8], o[i % 8], 0, 0, 0);
+  auto pv = [&](unsigned i, unsigned c) __attribute__((always_inline)) {
+    const unsigned b = i % 8, step = i / 8;
+    pv_mfma(o[c][b], va[i % kAhead], cur.p[c][step]);
   };
-  // Numerators e(r) = 2^s(r) (s is relative to m) as f16 pairs, one exponential per call
-  // (num(2 j) and num(2 j + 1) make pair j: keys r = 2 j, 2 j + 1); their sum, of the rounded
-  // values the MFMAs use, by dot products with (1, 1).
-  const cdna4::half2_t ones{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-  cdna4::half2_t e2[8];
-  float x_even[8];
-  float lsum = 0.0f;
-  auto num = [&](unsigned r) __attribute__((always_inline)) {
-    const float x = __builtin_amdgcn_exp2f(cur.s[r]);
-    if (r % 2 == 0) {
-      x_even[r / 2] = x;
-    } else {
-      e2[r / 2] = cdna4::half2_t{static_cast<_Float16>(x_even[r / 2]), static_cast<_Float16>(x)};
-      lsum = __builtin_amdgcn_fdot2(e2[r / 2], ones, lsum, false);
+  half8_t next[2][2];
+  auto copy = [&](unsigned st) __attribute__((always_inline)) {
+    if (do_copy) {  // uniform
+      switch (st) {
+        case 1: copy_one<0>(cp.kt, koff[0], cp.k_lds); break;
+        case 3: copy_one<1>(cp.kt, koff[1], cp.k_lds); break;
+        case 5: copy_one<2>(cp.kt, koff[2], cp.k_lds); break;
+        case 7: copy_one<3>(cp.kt, koff[3], cp.k_lds); break;
+        case 9: copy_one<4>(cp.vt, voff[0], cp.v_lds); break;
+        case 11: copy_one<5>(cp.vt, voff[1], cp.v_lds); break;
+        case 13: copy_one<6>(cp.vt, voff[2], cp.v_lds); break;
+        case 15: copy_one<7>(cp.vt, voff[3], cp.v_lds); break;
+        default: break;
+      }
     }
-  };
-  auto pack = [&](unsigned h) __attribute__((always_inline)) {
-    p[h] = half8_t{e2[4 * h][0],     e2[4 * h][1],     e2[4 * h + 1][0], e2[4 * h + 1][1],
-                   e2[4 * h + 2][0], e2[4 * h + 2][1], e2[4 * h + 3][0], e2[4 * h + 3][1]};
   };
 
   // Group A.
   kread(0);
   kread(1);
 #pragma unroll
-  for (unsigned st = 0; st < 8; ++st) {
+  for (unsigned i = 0; i < kAhead; ++i)
+    vread(i);
+#pragma unroll
+  for (unsigned st = 0; st < 16; ++st) {
     kread(st + 2);
     smma(st);
-    num(st);
-    if (st == 3)
-      vread(0), vread(1);
-    if (st == 7)
-      vread(2), vread(3);
+    if (st % 2 == 1) {
+      const unsigned i = st / 2;  // dimension block i of key step 0
+#pragma unroll
+      for (int c = 0; c < kBlocks; ++c)
+        pv(i, c);
+      vread(i + kAhead);
+    }
+    copy(st);
     __builtin_amdgcn_sched_barrier(0);
   }
-  pack(0);
   // Group B.
+  bool moved[2] = {false, false};
+  float corr[2] = {1.0f, 1.0f};
 #pragma unroll
   for (unsigned j = 0; j < 8; ++j) {
-    kread(j + 10);
-    smma(j + 8);
-    num(8 + j);
-    pv(j);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  pack(1);
-  rw.l = rw.l * cur.corr + lsum;
-  // Group C.
-  Decide<kMaskNext> dec;
 #pragma unroll
-  for (unsigned j = 0; j < 8; ++j) {
-    pv(8 + j);
-    if (kNext && j >= 1 && j <= 5)
-      dec.part(j - 1, s_acc, cur, rw, k0_next, lim, hi);
+    for (int c = 0; c < kBlocks; ++c)
+      pv(8 + j, c);
+    vread(8 + j + kAhead);
+    if (kNext && j == 1)
+      drain_pv();  // the last score MFMA is 6 MFMAs back; its result is read next
+    if (kNext && j == 1)
+      corr[0] = decide_block<kMaskNext>(s[0], rw.m[0], rw.l[0], next[0], k0_next, lim[0], hi,
+                                        moved[0]);
+    if (kNext && kBlocks == 2 && j == 5)
+      corr[1] = decide_block<kMaskNext>(s[1], rw.m[1], rw.l[1], next[1], k0_next, lim[1], hi,
+                                        moved[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (kNext && dec.moved) {
-    dec.finish(cur, rw);
-    scale_acc(o, cur.corr);
+  drain_pv();
+  if (kNext) {
+#pragma unroll
+    for (int c = 0; c < kBlocks; ++c)
+      cur.p[c][0] = next[c][0], cur.p[c][1] = next[c][1];
+#pragma unroll
+    for (int c = 0; c < kBlocks; ++c)
+      if (moved[c])
+        scale_acc(o[c], corr[c]);
   }
 }
 
 }  // namespace prefill_detail
 
 // Items [first, first + count) (grid-stride). Item -> (KV head, token block) as described at
-// attn_prefill_items. Per workgroup: tokens [16 b, 16 b + 16) x 8 heads of one KV head; wave w
-// owns tokens 16 b + 4 w .. + 4, the 32 query rows of one MFMA column block (row n = token offset
-// n / 8, head n % 8).
+// attn_prefill_items. Per workgroup: 16 kBlocks tokens x 8 heads of one KV head; wave w owns
+// 4 kBlocks of them, kBlocks MFMA column blocks of 4 tokens x 8 heads (row n of a block = token
+// offset n / 8, head n % 8).
 //
-// K/V tiles of 32 keys stream into a 3-stage LDS ring by direct global->LDS loads; one barrier
-// per tile. Per tile i (tile_step): the numerators of tile i, O^T += V^T P^T(i) (16 MFMAs, V^T
-// from ds_read_b64_tr_b16) and S^T(i + 1) = K Q^T (16 MFMAs, Q^T resident as f16 pre-scaled by
-// log2(e)/16), whose row max and rescale decision close the step. Keys past a row's causal limit
-// are masked only in the diagonal tiles of a wave; the gate and 1/l are applied at the store.
-template <int kBlock>
-__device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsigned count) {
-  using namespace prefill_detail;
+// K/V tiles of 32 keys stream into a 3-stage LDS ring by direct global->LDS loads (each wave
+// copies 8 rows of each, one instruction at a time between its MFMAs); one barrier per tile. Per
+// tile i (tile_step2): O^T += V^T P^T(i) for every block (16 MFMAs per block, V^T from
+// ds_read_b64_tr_b16, each operand feeding every block) and S^T(i + 1) = K Q^T (16 MFMAs per
+// block; the first block's Q^T resident in VGPRs as f16 pre-scaled by log2(e)/16, the second's in
+// LDS), whose decisions and numerators close the step. Keys past a row's causal limit are masked
+// only in the diagonal tiles of a wave; the gate and 1/l are applied at the store.
+namespace prefill_detail {
+
+template <int kBlocks>
+__device__ __attribute__((always_inline)) inline void prefill_items(const AttnPrefillParams& p,
+                                                                    unsigned first,
+                                                                    unsigned count, Shared& sh) {
   using attn::kDim;
-  static_assert(kBlock == 256, "four waves per prefill workgroup");
   constexpr int kGroup = attn::kQHeads / attn::kKvHeads;
-  constexpr unsigned kWaveTokens = kAttnQBlock / 4;
-  __shared__ Shared sh;
+  constexpr unsigned kItemTokens = kAttnQBlock * kBlocks;
+  constexpr unsigned kWaveTokens = kItemTokens / 4;
   const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned col = lane & 31u, hi = lane >> 5;  // MFMA column / lane half
-  const unsigned blocks = (p.n + kAttnQBlock - 1) / kAttnQBlock;
+  const unsigned blocks = (p.n + kItemTokens - 1) / kItemTokens;
   const unsigned lds0 = cdna4::lds_offset(sh.kv);
 
   // Per-lane constant addresses. Copy: instruction i moves rows 8 w + 2 i + lane / 32 (its
@@ -490,8 +571,8 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     if (rank >= blocks)
       continue;  // uniform across the workgroup
     const unsigned blk = blocks - 1 - rank;
-    const unsigned t0 = blk * kAttnQBlock;
-    const unsigned t_end = min(t0 + kAttnQBlock, p.n);
+    const unsigned t0 = blk * kItemTokens;
+    const unsigned t_end = min(t0 + kItemTokens, p.n);
     const unsigned kv_end = p.pos0 + t_end;
     const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * kDim;
     const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * kDim;
@@ -500,20 +581,26 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     // ti + 2 goes to `spare`.
     unsigned slot_cur = 0, slot_next = kTileBytes, slot_spare = 2 * kTileBytes;
     auto rotate = [&]() __attribute__((always_inline)) {
-      const unsigned t = slot_cur;
+      const unsigned tmp = slot_cur;
       slot_cur = slot_next;
       slot_next = slot_spare;
-      slot_spare = t;
+      slot_spare = tmp;
     };
+    auto full_tile = [&](unsigned ti) __attribute__((always_inline)) {
+      return (ti + 1) * kKeys <= kv_end;
+    };
+    auto dest = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
+      return TileCopy{K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
+                      lds0 + slot + wave * 4096, lds0 + kVBase + slot + wave * 4096};
+    };
+    // A whole tile copy at once (the first two tiles, and the last one when it crosses kv_end).
     auto copy = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
-      const unsigned k_lds = lds0 + slot + wave * 4096;
-      const unsigned v_lds = lds0 + kVBase + slot + wave * 4096;
-      if ((ti + 1) * kKeys <= kv_end)
-        copy_tile(K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
-                  copy_koff, copy_voff, k_lds, v_lds);
+      const TileCopy d = dest(ti, slot);
+      if (full_tile(ti))
+        copy_tile(d.kt, d.vt, copy_koff, copy_voff, d.k_lds, d.v_lds);
       else
-        copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, k_lds - wave * 4096,
-                          v_lds - wave * 4096, wave, lane);
+        copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, d.k_lds - wave * 4096,
+                          d.v_lds - wave * 4096, wave, lane);
     };
 
     // Start streaming before anything else: tiles 0 and 1.
@@ -521,12 +608,17 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
     if (tiles > 1)
       copy(1, slot_next);
 
-    // This wave's rows: token tq = tw + col / 8, head kvh * 8 + col % 8.
+    // This wave's rows: block c, token tw + 4 c + col / 8, head kvh * 8 + col % 8.
     const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
-    const unsigned raw_t = tw + col / kGroup;
-    const bool q_valid = raw_t < p.n;
-    const unsigned tq = q_valid ? raw_t : p.n - 1;
-    const unsigned lim = p.pos0 + tq;  // last visible key
+    unsigned tq[2] = {0, 0}, lim[2] = {0, 0};
+    bool q_valid[2] = {false, false};
+#pragma unroll
+    for (int c = 0; c < kBlocks; ++c) {
+      const unsigned raw_t = tw + 4 * c + col / kGroup;
+      q_valid[c] = raw_t < p.n;
+      tq[c] = q_valid[c] ? raw_t : p.n - 1;
+      lim[c] = p.pos0 + tq[c];  // last visible key
+    }
     const bool wave_active = tw < p.n;
     // Tiles this wave needs, and how many of them every row of the wave sees in full (always
     // fewer: the last tile of a wave is a diagonal one).
@@ -534,109 +626,149 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
         wave_active ? (p.pos0 + min(tw + kWaveTokens - 1, p.n - 1)) / kKeys + 1 : 0;
     const unsigned full_tiles = wave_active ? (p.pos0 + tw + 1) / kKeys : 0;
 
-    Rows rw;
+    Rows2 rw;
+    rw.q1 = cdna4::lds_offset(sh.q1[wave]) + 16 * lane;
     {
       constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
-      const float* src =
-          p.q + (std::size_t{tq} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
-      const float z = q_valid ? kScale : 0.0f;
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
-        const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
-        rw.q[st] = half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
-                           static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
-                           static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
-                           static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
+      for (int c = 0; c < kBlocks; ++c) {
+        const float* src =
+            p.q + (std::size_t{tq[c]} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
+        const float z = q_valid[c] ? kScale : 0.0f;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
+          const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
+          const half8_t v =
+              half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
+                      static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
+                      static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
+                      static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
+          if (c == 0)
+            rw.q0[st] = v;
+          else  // this wave's own region: its later reads are ordered after these writes
+            *reinterpret_cast<__attribute__((address_space(3))) half8_t*>(rw.q1 + 1024u * st) = v;
+        }
+        rw.m[c] = -__builtin_inff();
+        rw.l[c] = 0.0f;
       }
-      rw.m = 0.0f;
-      rw.l = 0.0f;
-      rw.negm = float16_t{};
     }
-    float16_t oacc[8];
+    float16_t oacc[kBlocks][8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-      oacc[b] = float16_t{};
+    for (int c = 0; c < kBlocks; ++c)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        oacc[c][b] = float16_t{};
 
-    // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (it is the
-    // only copy in flight), every wave's by the barrier, which also says that all waves are done
-    // with tile ti - 1, whose slot then receives tile ti + 2.
-    auto sync_copy = [&](unsigned ti) __attribute__((always_inline)) {
+    // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (its
+    // copy was the last one issued), every wave's by the barrier, which also says that all waves
+    // are done with tile ti - 1, whose slot then receives tile ti + 2 during the step.
+    auto sync = [&](unsigned ti) __attribute__((always_inline)) {
       if (ti + 1 < tiles) {
         cdna4::wait_vmcnt<0>();
         __syncthreads();
-        if (ti + 2 < tiles)
-          copy(ti + 2, slot_spare);
       }
+    };
+    // The step's copy of tile ti + 2: spread inside the step for a full tile, else at once.
+    auto next_copy = [&](unsigned ti) __attribute__((always_inline)) {
+      const bool spread = ti + 2 < tiles && full_tile(ti + 2);
+      if (ti + 2 < tiles && !spread)
+        copy(ti + 2, slot_spare);
+      return spread;
     };
 
     cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
     __syncthreads();
-    // cur: the decided scores of tile ti at the top of iteration ti (tile 0: here; O is still 0,
-    // so the first decision needs no rescale).
-    Pending cur;
-    if (wave_tiles > 0) {
-      const float16_t s0 = scores(rw, kb);
-      if (full_tiles > 0)
-        first_tile<false>(s0, cur, rw, lim, hi);
-      else
-        first_tile<true>(s0, cur, rw, lim, hi);
+    // cur: the decided numerators of tile ti at the top of iteration ti (tile 0: here; O is
+    // still 0, so the first decision needs no rescale).
+    Numer cur;
+    if (wave_active) {
+      float16_t s0[kBlocks];
+      scores2<kBlocks>(rw, kb, s0);
+      bool mv;
+#pragma unroll
+      for (int c = 0; c < kBlocks; ++c) {
+        if (full_tiles > 0)
+          decide_block<false>(s0[c], rw.m[c], rw.l[c], cur.p[c], 0, lim[c], hi, mv);
+        else
+          decide_block<true>(s0[c], rw.m[c], rw.l[c], cur.p[c], 0, lim[c], hi, mv);
+      }
     }
     // One pass over the workgroup's tiles in phases per wave, each a loop with a single body
-    // (the per-wave bounds differ; every wave still runs sync_copy once per tile, in order):
-    // tiles whose successor the wave's rows see in full, tiles whose successor is diagonal, the
-    // last tile (no successor), then the tiles the wave does not need.
+    // (the per-wave bounds differ; every wave still runs sync once per tile, in order): tiles
+    // whose successor the wave's rows see in full, tiles whose successor is diagonal, the last
+    // tile (no successor), then the tiles the wave does not need.
     unsigned ti = 0;
-    for (; ti + 1 < full_tiles; ++ti, rotate()) {
-      sync_copy(ti);
-      tile_step<false, true>(cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim,
-                             hi);
-    }
-    for (; ti + 1 < wave_tiles; ++ti, rotate()) {
-      sync_copy(ti);
-      tile_step<true, true>(cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim, hi);
-    }
+    auto step = [&](auto mask_next, auto has_next) __attribute__((always_inline)) {
+      sync(ti);
+      const bool spread = next_copy(ti);
+      tile_step2<kBlocks, decltype(mask_next)::value, decltype(has_next)::value>(
+          cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim, hi, spread,
+          dest(ti + 2, slot_spare), copy_koff, copy_voff);
+    };
+    using F = std::false_type;
+    using T = std::true_type;
+    for (; ti + 1 < full_tiles; ++ti, rotate())
+      step(F{}, T{});
+    for (; ti + 1 < wave_tiles; ++ti, rotate())
+      step(T{}, T{});
     if (ti < wave_tiles) {
-      sync_copy(ti);
-      tile_step<false, false>(cur, rw, oacc, kb, 0, vb, slot_cur, 0, lim, hi);
+      step(F{}, F{});
       ++ti;
       rotate();
     }
-    for (; ti < tiles; ++ti, rotate())
-      sync_copy(ti);
+    for (; ti < tiles; ++ti, rotate()) {
+      sync(ti);
+      if (ti + 2 < tiles)
+        copy(ti + 2, slot_spare);
+    }
     __syncthreads();  // the ring is reused by the next item
+    drain_pv();
 
-    // Row total: each column's keys per tile were split between the lane halves.
-    const float l_tot = cdna4::sum_xor32(rw.l);
-    if (q_valid) {
-      const unsigned head = kvh * kGroup + hq;
-      const float inv_l = __builtin_amdgcn_rcpf(l_tot);
-      const float* gate = p.qg + std::size_t{tq} * p.qg_stride + head * 2 * kDim + kDim;
-      float* out = p.core + (std::size_t{tq} * attn::kQHeads + head) * kDim;
-      // Every gate load before the first store: the compiler cannot tell qg from core apart, so
-      // interleaved, each load would wait behind the previous store (32 memory round trips).
-      float4 gv[8][4];
 #pragma unroll
-      for (int b = 0; b < 8; ++b)
+    for (int c = 0; c < kBlocks; ++c) {
+      // Row total: each column's keys per tile were split between the lane halves.
+      const float l_tot = cdna4::sum_xor32(rw.l[c]);
+      if (q_valid[c]) {
+        const unsigned head = kvh * kGroup + hq;
+        const float inv_l = __builtin_amdgcn_rcpf(l_tot);
+        const float* gate = p.qg + std::size_t{tq[c]} * p.qg_stride + head * 2 * kDim + kDim;
+        float* out = p.core + (std::size_t{tq[c]} * attn::kQHeads + head) * kDim;
+        // The gate loads of a 32-dimension block before its stores: the compiler cannot tell qg
+        // from core apart, so interleaved, each load would wait behind the previous store.
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          gv[b][r4] = *reinterpret_cast<const float4*>(gate + 32 * b + 8 * r4 + 4 * hi);
+        for (int b = 0; b < 8; ++b) {
+          float4 gv[4];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
+          for (int r4 = 0; r4 < 4; ++r4)
+            gv[r4] = *reinterpret_cast<const float4*>(gate + 32 * b + 8 * r4 + 4 * hi);
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
-          const float4 g = gv[b][r4];
-          float4 o;
-          o.x = oacc[b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
-          o.y = oacc[b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.y));
-          o.z = oacc[b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.z));
-          o.w = oacc[b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.w));
-          *reinterpret_cast<float4*>(out + d0) = o;
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
+            const float4 g = gv[r4];
+            float4 o;
+            o.x = oacc[c][b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
+            o.y = oacc[c][b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.y));
+            o.z = oacc[c][b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.z));
+            o.w = oacc[c][b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.w));
+            *reinterpret_cast<float4*>(out + d0) = o;
+          }
         }
       }
     }
   }
+}
+
+}  // namespace prefill_detail
+
+template <int kBlock>
+__device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsigned count) {
+  static_assert(kBlock == 256, "four waves per prefill workgroup");
+  __shared__ prefill_detail::Shared sh;
+  if (attn_prefill_row_blocks(p.n) == 2)  // uniform: the item size follows n
+    prefill_detail::prefill_items<2>(p, first, count, sh);
+  else
+    prefill_detail::prefill_items<1>(p, first, count, sh);
 }
 
 template <int kBlock>

@@ -175,9 +175,10 @@ def test_split_policy_contract(lib):
 
 
 def test_prefill_grid_covers_every_block(lib):
-    for n in (1, 15, 16, 17, 63, 64, 65, 2048, 8192, 10**5):
+    for n in (1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 2048, 4095, 4096, 8192, 10**5):
         items = lib.miso_attn_prefill_items(n)
-        blocks = (n + 15) // 16
+        tokens = 32 if n >= 4096 else 16  # tokens per workgroup (two row blocks per wave from 4096)
+        blocks = (n + tokens - 1) // tokens
         assert items % 8 == 0 and items >= 2 * blocks and items < 2 * blocks + 8
         # item -> (kv head, rank): a bijection onto {0,1} x [0, blocks) plus idle slots
         seen = set()
