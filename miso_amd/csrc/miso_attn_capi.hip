@@ -39,14 +39,15 @@ int launched(const char* fn) {
   return static_cast<int>(err);
 }
 
-// Q4_K GEMV launch shapes, from a sweep of workgroup size x rows per wave step at the engine's
-// Q4_K projections (f16 activations, HBM-resident weights): up to 1024 rows, one-wave workgroups
-// and one row per step (attn_k, 512 rows: 2.50 us against 3.62 us with 4-wave workgroups and 4
-// rows); more rows, 4-wave workgroups and K / 512 rows per step (attn_q 8192 x 2048: 5.35 us,
-// attn_output 2048 x 4096: 4.25 us). One step per wave up to 8192 workgroups (grid-stride beyond).
+// Q4_K GEMV launch shapes, from a sweep of workgroup size x passes per wave at the engine's
+// projections (f16 activations, HBM-resident weights, graph-replayed). Up to 1024 rows: workgroups
+// of max(128, K / 32) threads and one pass per wave (attn_k 512 x 2048: 2.38 us against 2.67 us
+// with one-wave workgroups and 3.65 us with 4-wave workgroups of 4 passes). More rows: 4-wave
+// workgroups with two passes (attn_q 8192 x 2048: 4.30 us, 4 passes 4.42 us; attn_output 2048 x
+// 4096: 3.31 us), one for K = 8192. One step per wave up to 8192 workgroups (grid-stride beyond).
 template <k::ActFormat A, unsigned K, int kBlock, int kRows>
 void launch_q4k_shape(const k::Q4kGemvParams& p, hipStream_t stream) {
-  const unsigned per_wg = (kBlock / 64) * kRows;
+  const unsigned per_wg = (kBlock / 64) * k::q4k_gemv_wave_rows<K, kRows>();
   unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
   grid = grid < 8192u ? grid : 8192u;
   k::q4k_gemv_kernel<A, K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
@@ -55,15 +56,15 @@ void launch_q4k_shape(const k::Q4kGemvParams& p, hipStream_t stream) {
 template <k::ActFormat A, unsigned K>
 void launch_q4k(const k::Q4kGemvParams& p, hipStream_t stream) {
   if (p.n_rows <= 1024)
-    launch_q4k_shape<A, K, 64, 1>(p, stream);
+    launch_q4k_shape<A, K, (K / 32 > 128 ? K / 32 : 128), 1>(p, stream);
   else
-    launch_q4k_shape<A, K, 256, (K == 2048 ? 4 : K == 4096 ? 2 : 1)>(p, stream);
+    launch_q4k_shape<A, K, 256, (K == 8192 ? 1 : 2)>(p, stream);
 }
 
-// Q6_K GEMV launch, the same shape rule as the Q4_K one.
+// Q6_K GEMV launch, the same shape rule as the Q4_K one (attn_v 512 x 2048: 2.57 us).
 template <unsigned K, int kBlock, int kRows>
 void launch_q6k_shape(const k::Q6kGemvParams& p, hipStream_t stream) {
-  const unsigned per_wg = (kBlock / 64) * kRows;
+  const unsigned per_wg = (kBlock / 64) * k::q6k_gemv_wave_rows<K, kRows>();
   unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
   grid = grid < 8192u ? grid : 8192u;
   k::q6k_gemv_kernel<K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
@@ -72,9 +73,9 @@ void launch_q6k_shape(const k::Q6kGemvParams& p, hipStream_t stream) {
 template <unsigned K>
 void launch_q6k(const k::Q6kGemvParams& p, hipStream_t stream) {
   if (p.n_rows <= 1024)
-    launch_q6k_shape<K, 64, 1>(p, stream);
+    launch_q6k_shape<K, (K / 32 > 128 ? K / 32 : 128), 1>(p, stream);
   else
-    launch_q6k_shape<K, 256, (K == 2048 ? 4 : K == 4096 ? 2 : 1)>(p, stream);
+    launch_q6k_shape<K, 256, (K == 8192 ? 1 : 2)>(p, stream);
 }
 
 template <bool kPrepared, int kPipeline>
@@ -501,8 +502,8 @@ int miso_attn_q4k_q6k_gemv_pair(const uint8_t* w4, uint32_t n4, float* y4, const
   if (n4 == 0 || n6 == 0)
     return fail("miso_attn_q4k_q6k_gemv_pair", "both row counts must be >= 1");
   // Logical grids sized for the attention's attn_q (8192 rows, 16 per Q4_K workgroup) and attn_v
-  // (512 rows, 4 per Q6_K workgroup); other row counts grid-stride.
-  constexpr unsigned kQ6Grid = 128, kQ4Grid = 512;
+  // (512 rows, 8 per Q6_K workgroup); other row counts grid-stride.
+  constexpr unsigned kQ6Grid = 64, kQ4Grid = 512;
   const k::Q6kGemvParams p6{w6, x, y6, n6};
   const k::Q4kGemvParams p4{w4, x, y4, n4};
   k::mixed_gemv_kernel<1, kQ6Grid, kQ4Grid, 256>
@@ -518,8 +519,8 @@ int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t*
   if (nq == 0 || nk == 0 || nv == 0)
     return fail("miso_attn_qkv_gemv", "all three row counts must be >= 1");
   // Logical grids sized for attn_q (8192 rows) and attn_k (512 rows), 16 rows per Q4_K
-  // workgroup, and attn_v (512 rows), 4 per Q6_K workgroup; other row counts grid-stride.
-  constexpr unsigned kQ = 512, kK = 32, kV = 128;
+  // workgroup, and attn_v (512 rows, 8 per Q6_K workgroup); other row counts grid-stride.
+  constexpr unsigned kQ = 512, kK = 32, kV = 64;
   const k::Q4kGemvParams pq{wq, x, yq, nq}, pk{wk, x, yk, nk};
   const k::Q6kGemvParams pv{wv, x, yv, nv};
   k::qkv_gemv_kernel<kQ, kK, kV, 256><<<kQ + kK + kV, 256, 0, as_stream(stream)>>>(pq, pk, pv);
