@@ -233,6 +233,24 @@ int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t*
                        float* yk, const uint8_t* wv, uint32_t nv, float* yv, const float* x,
                        void* stream);
 
+/* Prefill activations for the projection GEMMs: rounds x to f16 and sums every 32-element group of
+ * the rounded values. Replaces gemm_input() (src/engine/weights.hip:306-314, the
+ * qgemm_act_kernel launch of kernels/qgemm.hpp). x: n_tok x k floats, xh: n_tok x k binary16,
+ * xs: n_tok x k / 32 floats, all 16-byte aligned. n_tok == 0 is a no-op. Rejects k == 0 or
+ * k % 256 != 0 (the reference throws "gemm_input: chunk does not fit"). */
+int miso_attn_gemm_input(const float* x, uint16_t* xh, float* xs, uint32_t k, uint32_t n_tok,
+                         void* stream);
+
+/* Prefill projection GEMM y[t * ldy + n] = sum_k W[n][k] xh[t][k] over n_rows quantized rows.
+ * Replaces gemm() (src/engine/weights.hip:316-330, the qgemm_kernel<QFormat> launch of
+ * kernels/qgemm.hpp). format 0: Q4_K r1 rows (144 bytes per 256 weights; uses xs), 1: Q6_K r1
+ * rows (k / 256 x 210 bytes rounded up to 16). xh / xs as written by miso_attn_gemm_input for the
+ * same k and n_tok; y: n_tok rows of stride ldy >= n_rows floats. n_tok == 0 or n_rows == 0 is a
+ * no-op. Rejects k % 256 != 0, ldy < n_rows and any other format (the reference throws
+ * "gemm: unsupported type"). */
+int miso_attn_gemm(const uint8_t* w, int format, const uint16_t* xh, const float* xs, float* y,
+                   uint32_t k, uint32_t n_rows, uint32_t n_tok, uint32_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,8 @@ SIGNATURES = {
     "miso_attn_q6k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, P]),
     "miso_attn_q4k_q6k_gemv_pair": (c_int, [P, c_uint32, P, P, c_uint32, P, P, P]),
     "miso_attn_qkv_gemv": (c_int, [P, c_uint32, P, P, c_uint32, P, P, c_uint32, P, P, P]),
+    "miso_attn_gemm_input": (c_int, [P, P, P, c_uint32, c_uint32, P]),
+    "miso_attn_gemm": (c_int, [P, c_int, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P]),
 }
 
 _lib = None

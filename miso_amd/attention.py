@@ -367,3 +367,46 @@ def qkv_gemv(wq, nq: int, yq, wk, nk: int, yk, wv, nv: int, yv, x, stream=None) 
         _need(t, name, torch.float32, n)
     _lib.check(_lib.load().miso_attn_qkv_gemv(_ptr(wq), nq, _ptr(yq), _ptr(wk), nk, _ptr(yk),
                                               _ptr(wv), nv, _ptr(yv), _ptr(x), _stream(stream)))
+
+
+# ------------------------------------------------------------------------------------------------
+# Prefill projection GEMMs (src/engine/weights.hpp:78-90: GemmInput, gemm_input, gemm)
+# ------------------------------------------------------------------------------------------------
+
+class GemmInput:
+    """Activations of a token chunk prepared for the prefill GEMMs (the reference's GemmInput,
+    src/engine/weights.hpp:78-84): xh, max_tok x max_k f16 values, and xs, their per-32 sums."""
+
+    def __init__(self, max_tok: int, max_k: int, device="cuda"):
+        self.xh = torch.empty(max_tok * max_k, dtype=torch.float16, device=device)
+        self.xs = torch.empty(max_tok * max_k // 32, dtype=torch.float32, device=device)
+        self.k = 0
+        self.n_tok = 0
+
+
+def gemm_input(x, k: int, n_tok: int, inp: GemmInput, stream=None) -> None:
+    """Prepares x ([n_tok][k] floats) as GEMM input (src/engine/weights.hip:306-314)."""
+    if n_tok * k > inp.xh.numel() or k % 256 != 0:
+        raise RuntimeError("gemm_input: chunk does not fit")
+    _need(x, "x", torch.float32, n_tok * k)
+    inp.k, inp.n_tok = k, n_tok
+    _lib.check(_lib.load().miso_attn_gemm_input(_ptr(x), _ptr(inp.xh), _ptr(inp.xs), k, n_tok,
+                                                _stream(stream)))
+
+
+GEMM_FORMATS = {"q4_k": 0, "q6_k": 1}
+
+
+def gemm(w, fmt: str, n_rows: int, k: int, inp: GemmInput, y, ldy: int, stream=None) -> None:
+    """Y[t][n] = W x[t] for the prepared chunk, row t of Y at y + t * ldy (src/engine/weights.hip:
+    316-330). w: n_rows rows of k weights in the Q4_K r1 ("q4_k") or Q6_K r1 ("q6_k") layout."""
+    if k != inp.k:
+        raise RuntimeError("gemm: K mismatch")
+    if fmt not in GEMM_FORMATS:
+        raise RuntimeError("gemm: unsupported type")
+    row = k // 256 * 144 if fmt == "q4_k" else q6k_row_bytes(k)
+    _need(w, "w", torch.uint8, n_rows * row)
+    if inp.n_tok:
+        _need(y, "y", torch.float32, (inp.n_tok - 1) * ldy + n_rows)
+    _lib.check(_lib.load().miso_attn_gemm(_ptr(w), GEMM_FORMATS[fmt], _ptr(inp.xh), _ptr(inp.xs),
+                                          _ptr(y), k, n_rows, inp.n_tok, ldy, _stream(stream)))

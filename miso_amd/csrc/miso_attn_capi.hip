@@ -16,6 +16,7 @@
 #include "q4k_gemv.hpp"
 #include "q6k_gemv.hpp"
 #include "mixed_gemv.hpp"
+#include "qgemm.hpp"
 
 namespace k = miso::kernels;
 using k::attn::half_t;
@@ -525,6 +526,43 @@ int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t*
   const k::Q6kGemvParams pv{wv, x, yv, nv};
   k::qkv_gemv_kernel<kQ, kK, kV, 256><<<kQ + kK + kV, 256, 0, as_stream(stream)>>>(pq, pk, pv);
   return launched("miso_attn_qkv_gemv");
+}
+
+int miso_attn_gemm_input(const float* x, uint16_t* xh, float* xs, uint32_t k, uint32_t n_tok,
+                         void* stream) {
+  if (n_tok == 0)
+    return 0;
+  if (any_bad(x, xh, xs))
+    return fail("miso_attn_gemm_input", kBadPtr);
+  if (k == 0 || k % 256 != 0)
+    return fail("miso_attn_gemm_input", "k must be a positive multiple of 256");
+  const k::QGemmActParams p{x, reinterpret_cast<_Float16*>(xh), xs, k, n_tok};
+  // One thread per 8 elements (the kernel grid-strides, so the reference's one-thread-per-group
+  // grid also works, with four passes per thread).
+  const unsigned quarters = n_tok * (k / 8);
+  k::qgemm_act_kernel<<<(quarters + 255) / 256, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_gemm_input");
+}
+
+int miso_attn_gemm(const uint8_t* w, int format, const uint16_t* xh, const float* xs, float* y,
+                   uint32_t k, uint32_t n_rows, uint32_t n_tok, uint32_t ldy, void* stream) {
+  if (n_tok == 0 || n_rows == 0)
+    return 0;
+  if (any_bad(w, xh) || (format == 0 && bad_ptr(xs)) || bad_scalars(y))
+    return fail("miso_attn_gemm", kBadPtr);
+  if (k == 0 || k % 256 != 0)
+    return fail("miso_attn_gemm", "k must be a positive multiple of 256");
+  if (ldy < n_rows)
+    return fail("miso_attn_gemm", "ldy must be >= n_rows");
+  const k::QGemmParams p{w, reinterpret_cast<const _Float16*>(xh), xs, y, k, n_rows, n_tok, ldy};
+  const unsigned grid = k::qgemm_tiles(n_rows, n_tok);
+  if (format == 0)
+    k::qgemm_kernel<k::QFormat::Q4K><<<grid, 256, 0, as_stream(stream)>>>(p);
+  else if (format == 1)
+    k::qgemm_kernel<k::QFormat::Q6K><<<grid, 256, 0, as_stream(stream)>>>(p);
+  else
+    return fail("miso_attn_gemm", "format must be 0 (Q4_K) or 1 (Q6_K)");
+  return launched("miso_attn_gemm");
 }
 
 }  // extern "C"

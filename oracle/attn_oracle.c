@@ -30,7 +30,8 @@
  *                          and oracle_decode_f64 over its dequantized rows (no reference
  *                          function: the reference's cache is f16). The encoder is a search
  *                          for the nearest code, not the kernels' bit arithmetic.
- *   - oracle_q4k_scale_min / oracle_q4k_dequant: GGUF Q4_K, src/dequant.cpp:45-61,80-84.
+ *   - oracle_q4k_scale_min / oracle_q4k_dequant: GGUF Q4_K, src/dequant.cpp:45-61,80-84;
+ *                          oracle_q4k_mins: each element's dmin m (for the GEMM test's bound).
  *   - oracle_q4k_repack_r1: the r1 layout of the GPU GEMV, src/repack.cpp:9-25.
  *   - oracle_q4k_gemv_f64: y = W x in double over the dequantized rows, the reference of
  *                          tests/test_q4k_gemv.hip:80-90.
@@ -635,6 +636,20 @@ void oracle_q4k_dequant(const uint8_t* blocks, size_t n_blocks, float* out, floa
         out[b * 256 + 32 * j + l] = dj * (float)v - mj;
         if (ds) ds[b * 256 + 32 * j + l] = dj;
       }
+    }
+  }
+}
+
+/* dmin m of each element's sub-block for n_blocks GGUF Q4_K blocks (the magnitude of a weight's
+ * min term, one of the two parts of the per-element bound of tests/test_qgemm.hip:46-53). */
+void oracle_q4k_mins(const uint8_t* blocks, size_t n_blocks, float* dm) {
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t* blk = blocks + b * 144;
+    const float dmin = f16_at(blk + 2);
+    for (int j = 0; j < 8; ++j) {
+      uint8_t sc, m;
+      oracle_q4k_scale_min(blk, j, &sc, &m);
+      for (int l = 0; l < 32; ++l) dm[b * 256 + 32 * j + l] = dmin * (float)m;
     }
   }
 }

@@ -61,6 +61,7 @@ def lib() -> ctypes.CDLL:
             "oracle_fp8_encode_rows": (None, [V, ctypes.c_size_t, V, V]),
             "oracle_decode_fp8_f64": (None, [V, V, V, V, V, V, c_uint32, c_uint32, V, c_int]),
             "oracle_q4k_dequant": (None, [V, ctypes.c_size_t, V, V]),
+            "oracle_q4k_mins": (None, [V, ctypes.c_size_t, V]),
             "oracle_q4k_repack_r1": (None, [V, ctypes.c_size_t, V]),
             "oracle_q4k_gemv_f64": (None, [V, V, c_uint32, c_uint32, V]),
             "oracle_q6k_dequant": (None, [V, ctypes.c_size_t, V]),
@@ -261,6 +262,29 @@ def q4k_dequant(blocks) -> tuple[np.ndarray, np.ndarray]:
     ds = np.empty(nb * 256, np.float32)
     lib().oracle_q4k_dequant(_ptr(blocks), nb, _ptr(w), _ptr(ds))
     return w, ds
+
+
+def q4k_mins(blocks) -> np.ndarray:
+    """GGUF Q4_K blocks -> dmin * m of each weight's sub-block (f32)."""
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    nb = blocks.size // 144
+    dm = np.empty(nb * 256, np.float32)
+    lib().oracle_q4k_mins(_ptr(blocks), nb, _ptr(dm))
+    return dm
+
+
+def qgemm_act_ref(x) -> tuple[np.ndarray, np.ndarray]:
+    """The prefill GEMM's activation prep, the reference's CPU rule (tests/test_qgemm.hip:92-104):
+    h = x rounded to f16 (RNE); per 32-group the f32 sum, added in order to 0, of the chunk sums
+    ((h0 + h1) + h2) + h3 of its 8 four-element chunks. Returns (h as float16, sums as float32)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    h = x.astype(np.float16)
+    g = h.astype(np.float32).reshape(-1, 32)
+    s = np.zeros(g.shape[0], np.float32)
+    for c in range(8):
+        q = g[:, 4 * c:4 * c + 4]
+        s = s + (((q[:, 0] + q[:, 1]) + q[:, 2]) + q[:, 3])
+    return h, s
 
 
 def q4k_repack_r1(blocks) -> np.ndarray:

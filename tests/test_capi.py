@@ -104,6 +104,16 @@ def test_host_validation_rejects_bad_arguments(lib):
     for nq, nk, nv in ((0, 5, 5), (5, 0, 5), (5, 5, 0)):
         rejected(qkv(P, nq, P, P, nk, P, P, nv, P, P, N), lib, "row counts")
     rejected(qkv(P, 5, P, P, 5, P, P + 4, 5, P, P, N), lib, "NULL or not 16-byte aligned")
+    gin, gemm = lib.miso_attn_gemm_input, lib.miso_attn_gemm
+    for bad_k in (0, 128, 2049):
+        rejected(gin(P, P, P, bad_k, 4, N), lib, "multiple of 256")
+        rejected(gemm(P, 0, P, P, P, bad_k, 8, 4, 8, N), lib, "multiple of 256")
+    assert gin(N, N, N, 7, 0, N) == 0  # n_tok == 0: no-op
+    assert gemm(N, 9, N, N, N, 7, 8, 0, 0, N) == 0 and gemm(N, 9, N, N, N, 7, 0, 4, 0, N) == 0
+    rejected(gemm(P, 2, P, P, P, 2048, 8, 4, 8, N), lib, "format")
+    rejected(gemm(P, 0, P, P, P, 2048, 8, 4, 7, N), lib, "ldy")
+    rejected(gemm(P, 0, P, P + 4, P, 2048, 8, 4, 8, N), lib, "NULL or not 16-byte aligned")
+    assert gemm(P, 1, P, N, P, 2048, 8, 0, 8, N) == 0
     rejected(lib.miso_attn_combine_variant(7, P, P, P, P, P, 4, 0, 0, 0, N), lib, "variant")
     rejected(lib.miso_attn_combine_variant(0, P, P, P, P, P, 4, 0, 8, 2, N), lib, "range form")
     rejected(lib.miso_attn_combine_variant(1, P, P, P, P, P, 4, 60, 8, 2, N), lib, "range form")

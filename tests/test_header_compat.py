@@ -1,7 +1,8 @@
 """Drop-in check of the C++ header API (CPU, compile-only): the reference's own callers of the
 attention kernels -- src/engine/attention.hip, tests/test_attn_splitk.hip and
-bench/attention/*.hip -- and of the Q4_K / Q6_K GEMVs -- tests/test_q4k_gemv.hip,
-tests/test_q6k_gemv.hip -- compile UNCHANGED for gfx950 with this repository's miso_amd/kernels
+bench/attention/*.hip -- and of the Q4_K / Q6_K GEMVs and prefill GEMMs -- src/engine/weights.hip,
+tests/test_q4k_gemv.hip, tests/test_q6k_gemv.hip, tests/test_gemv_dispatch.hip,
+tests/test_qgemm.hip -- compile UNCHANGED for gfx950 with this repository's miso_amd/kernels
 ahead of the reference's kernels/ on the include path, and the preprocessor really picks this repository's headers (while the
 reference's own rmsnorm.hpp and wave.hpp stay reachable in the same translation unit without
 clashes).
@@ -30,9 +31,11 @@ CALLERS = [
     ("tests/test_q4k_gemv.hip", "q4k_gemv.hpp"),
     ("tests/test_q6k_gemv.hip", "q6k_gemv.hpp"),
     ("tests/test_gemv_dispatch.hip", "mixed_gemv.hpp"),
+    ("tests/test_qgemm.hip", "qgemm.hpp"),
+    ("src/engine/weights.hip", "qgemm.hpp"),
 ]
 OURS = ("attention_decode.hpp", "attention_prefill.hpp", "q4k_gemv.hpp", "q6k_gemv.hpp",
-        "mixed_gemv.hpp")
+        "mixed_gemv.hpp", "qgemm.hpp")
 
 pytestmark = pytest.mark.skipif(not (REF / "kernels").is_dir() or not Path(HIPCC).exists(),
                                 reason="reference tree or hipcc not available")
