@@ -160,8 +160,10 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
  * the keys in a pool of pages instead of contiguous per-sequence buffers: page g holds
  * [2 KV heads][page_size][256] f16 at g * 2 * page_size * 256 halves of k_pages / v_pages, and
  * sequence s's positions [j * page_size, (j + 1) * page_size) are in page
- * page_table[s * max_pages + j]. page_table and lens are DEVICE arrays (not validated on the host:
- * every page id of a sequence's first ceil(lens[s] / page_size) entries must lie in the pool).
+ * page_table[s * max_pages + j]. A sequence attends to min(lens[s], max_pages * page_size) keys:
+ * a longer lens[s] is clamped to what its page-table row can address. page_table and lens are
+ * DEVICE arrays (not validated on the host: every page id of a sequence's first
+ * ceil(min(lens[s], max_pages * page_size) / page_size) entries must lie in the pool).
  * Rejects batch == 0, max_len == 0, max_pages == 0, page_size not a power of two in [8, 65536],
  * and max_pages * page_size < max_len. */
 int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_pages,

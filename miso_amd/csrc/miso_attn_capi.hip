@@ -347,9 +347,9 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
   if (max_len == 0)
     return fail("miso_attn_decode_ragged", "max_len must be >= 1");
   const unsigned s_max = k::attn_ragged_splits(max_len);
-  const k::AttnRaggedParams p{q,      gate,   as_half(k_cache), as_half(v_cache), kv_offsets,
-                              lens,   core,   part_m,           part_l,           part_o,
-                              batch,  s_max};
+  const k::AttnRaggedParams p{q,     gate,  as_half(k_cache), as_half(v_cache), kv_offsets,
+                              lens,  core,  part_m,           part_l,           part_o,
+                              batch, s_max, 0xFFFFFFFFu};
   const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
   if (items > 0x7FFFFFFFull)
     return fail("miso_attn_decode_ragged", "batch x splits too large for one grid");
@@ -395,9 +395,9 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
   if (rc != 0)
     return rc;
   // The merge reads only the partials, lens, gate and core of the ragged parameters.
-  const k::AttnRaggedParams r{q,      gate,   nullptr, nullptr, nullptr,
-                              lens,   core,   part_m,  part_l,  part_o,
-                              batch,  s_max};
+  const k::AttnRaggedParams r{q,     gate,   nullptr, nullptr, nullptr,
+                              lens,  core,   part_m,  part_l,  part_o,
+                              batch, s_max,  k::attn_paged_len_cap(max_pages, p.log2_page)};
   const unsigned tiles = batch * k::attn::kQHeads * (k::attn::kDim / 64);
   k::attn_ragged_combine_kernel<<<tiles, 64, 0, as_stream(stream)>>>(r);
   return launched("miso_attn_decode_paged(combine)");

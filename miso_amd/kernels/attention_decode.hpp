@@ -285,7 +285,8 @@ __device__ __attribute__((always_inline)) inline float dot2_first(half2_t a, uns
 // reduce-scatter of the lane's 16 partial dot products (see process_unit) to one score per lane
 // (head 4 hq + dc / 4, unit row 4 rq + dc % 4), the span mask, the lazy rescale, and the f16
 // numerators, published to `pbuf` for P V. With kScaled, the score is multiplied by its row's K
-// scale and the published numerator by its row's V scale (the l sum stays unscaled).
+// scale and the published numerator by vsc, the row's V scale relative to its unit's largest
+// (vsc <= 1; the l sum stays unscaled).
 // The reduce-scatter of the lane's 16 partial dot products (see process_unit) over the 16 lanes
 // of dc: returns the complete score of head 4 hq + dc / 4, unit row 4 rq + dc % 4.
 __device__ __attribute__((always_inline)) inline float unit_scores(const float (&part)[16]) {
@@ -993,6 +994,8 @@ struct AttnRaggedParams {
   float* part_l;
   float* part_o;  // [batch][2][s_max][8][256]
   unsigned batch, s_max;
+  unsigned len_cap;  // keys a sequence can hold (the paged layout's pages x page size); lens
+                     // past it count as len_cap. ~0u for the contiguous ragged layout.
 };
 
 // Splits of a sequence of len keys: one per kAttnRaggedChunk keys, at most s_max.
@@ -1031,7 +1034,8 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
   if (seq >= p.batch)
     return;
   const std::size_t out = (std::size_t{seq} * attn::kQHeads + h) * attn::kDim + d;
-  const unsigned n_splits = attn_ragged_seq_splits(p.lens[seq], p.s_max);
+  const unsigned len = p.lens[seq] < p.len_cap ? p.lens[seq] : p.len_cap;
+  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
   if (n_splits == 0) {
     p.core[out] = 0.0f;
     return;
@@ -1047,9 +1051,10 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
 // ------------------------------------------------------------------------------------------------
 // Paged batched decode (no reference counterpart): the ragged decode over a pool of KV pages.
 // Page id g holds [2 KV heads][page][256] f16 at g * 2 * page * 256 halves of k_pages / v_pages;
-// sequence s's positions [j page, (j + 1) page) are in page page_table[s * max_pages + j]. Same
-// splits, arithmetic and partial layout as the ragged path, so the outputs are bit-identical to
-// it on the same keys; attn_ragged_combine_kernel merges the partials.
+// sequence s's positions [j page, (j + 1) page) are in page page_table[s * max_pages + j]; a
+// sequence attends to min(lens[s], max_pages x page) keys. Same splits, arithmetic and partial
+// layout as the ragged path, so the outputs are bit-identical to it on the same keys;
+// attn_ragged_combine_kernel (with that cap) merges the partials.
 // ------------------------------------------------------------------------------------------------
 
 struct AttnPagedParams {
@@ -1064,6 +1069,13 @@ struct AttnPagedParams {
   unsigned batch, s_max, max_pages, log2_page;
 };
 
+// Keys a paged sequence can hold: a longer lens[s] attends to its first max_pages pages only
+// (its page-table row has no entries past them).
+__host__ __device__ inline unsigned attn_paged_len_cap(unsigned max_pages, unsigned log2_page) {
+  const unsigned long long cap = static_cast<unsigned long long>(max_pages) << log2_page;
+  return cap < 0xFFFFFFFFull ? static_cast<unsigned>(cap) : 0xFFFFFFFFu;
+}
+
 // One workgroup per (sequence, KV head, split slot), as attn_ragged_split_kernel.
 template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParams p) {
@@ -1074,7 +1086,8 @@ __global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParam
   const unsigned seq = item / (p.s_max * attn::kKvHeads);
   if (seq >= p.batch)
     return;
-  const unsigned len = p.lens[seq];
+  const unsigned cap = attn_paged_len_cap(p.max_pages, p.log2_page);
+  const unsigned len = p.lens[seq] < cap ? p.lens[seq] : cap;
   const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
   if (split >= n_splits)
     return;

@@ -279,11 +279,14 @@ __device__ __attribute__((always_inline)) inline void wait_fp8_units_after(unsig
 // One 8-row half of an e4m3 unit: the lane layout of process_unit, with the K chunk of a row
 // being dimensions 16 dc .. 16 dc + 15 (16 bytes) and the V chunk dimensions 8 c .. 8 c + 7 of
 // rows 2 i + a (8 bytes). Codes widen to f16 exactly; the row scales enter through
-// unit_numerators (scores x K scale, numerators x V scale).
+// unit_numerators: scores x K scale (f32), numerators x the row's V scale relative to the unit's
+// largest (vratio <= 1, so the f16 numerator never exceeds the unscaled one). The half's P V
+// accumulates into the unit's f32 sums t (kFirst: the unit's first half starts them).
+template <bool kFirst>
 __device__ __attribute__((always_inline)) inline void process_half_fp8(
-    WaveState& st, const uint4 (&kr)[4], const uint2 (&vr)[4], float ksc, float vsc,
+    WaveState& st, const uint4 (&kr)[4], const uint2 (&vr)[4], float ksc, float vratio,
     const half2_t (&qh)[4][8], unsigned r0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
-    unsigned lane) {
+    float (&t)[kGroup][8], unsigned lane) {
   float part[16];
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) {
@@ -303,7 +306,23 @@ __device__ __attribute__((always_inline)) inline void process_half_fp8(
       part[4 * hh + rr] = acc;
     }
   }
-  unit_numerators<true>(st, part, r0, span_end, ksc, vsc, pbuf, lane);
+  const float m_before = st.m;
+  unit_numerators<true>(st, part, r0, span_end, ksc, vratio, pbuf, lane);
+  if constexpr (!kFirst) {
+    // The first half's sums in t were taken against the previous reference max: when this
+    // half moved it, t takes the same per-head correction as o (unit_softmax_state's).
+    if (__builtin_amdgcn_ballot_w64(st.m != m_before)) {  // wave-uniform branch
+      const float corr = __builtin_amdgcn_exp2f(m_before - st.m);
+#pragma unroll
+      for (int h = 0; h < kGroup; ++h) {
+        const float ch =
+            cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), head_lane(h)));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          t[h][e] *= ch;
+      }
+    }
+  }
   // P V over this lane's rows 2 i + a, dimensions 8 c .. 8 c + 7: the byte permutes interleave
   // rows 2 g + a and 2 g + 4 + a so that one conversion yields their f16 pair for a dimension.
   const unsigned a = lane >> 5;
@@ -313,25 +332,35 @@ __device__ __attribute__((always_inline)) inline void process_half_fp8(
     const uint4 p1 = *reinterpret_cast<const uint4*>(&pbuf[a][g][4]);
     const unsigned pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
     const unsigned r0w[2] = {vr[g].x, vr[g].y}, r1w[2] = {vr[g + 2].x, vr[g + 2].y};
-    half2_t pv[8];
+    unsigned pv[8];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const unsigned lo = __builtin_amdgcn_perm(r1w[j], r0w[j], 0x05010400u);
       const unsigned hi = __builtin_amdgcn_perm(r1w[j], r0w[j], 0x07030602u);
-      pv[4 * j + 0] = cdna4::as_half2(fp8kv::pair_lo(lo));
-      pv[4 * j + 1] = cdna4::as_half2(fp8kv::pair_hi(lo));
-      pv[4 * j + 2] = cdna4::as_half2(fp8kv::pair_lo(hi));
-      pv[4 * j + 3] = cdna4::as_half2(fp8kv::pair_hi(hi));
+      pv[4 * j + 0] = fp8kv::pair_lo(lo);
+      pv[4 * j + 1] = fp8kv::pair_hi(lo);
+      pv[4 * j + 2] = fp8kv::pair_lo(hi);
+      pv[4 * j + 3] = fp8kv::pair_hi(hi);
     }
 #pragma unroll
     for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        st.o[h][e] = __builtin_amdgcn_fdot2(cdna4::as_half2(pp[h]), pv[e], st.o[h][e], false);
+      for (int e = 0; e < 8; ++e) {
+        if (kFirst && g == 0)
+          t[h][e] = dot2_first(cdna4::as_half2(pp[h]), pv[e]);
+        else
+          t[h][e] = __builtin_amdgcn_fdot2(cdna4::as_half2(pp[h]), cdna4::as_half2(pv[e]),
+                                           t[h][e], false);
+      }
   }
 }
 
-// One 16-row e4m3 unit: every LDS read of both halves first, then the halves in order.
+// One 16-row e4m3 unit: every LDS read of both halves first, then the halves in order. The
+// unit's V reference is its largest V row scale among the rows of the span (wave-uniform): the
+// numerators carry each row's scale relative to it, the unit's P V sums stay in f32 and enter o
+// times the reference. A common power-of-two factor on every V scale therefore leaves the f16
+// numerators unchanged (no f16 overflow at the largest scales, no underflow at the smallest);
+// only the spread of V scales within 16 consecutive rows scales them down.
 __device__ __attribute__((always_inline)) inline void process_unit_fp8(
     WaveState& st, const unsigned char* slot, const float* scl, const unsigned (&koff)[4],
     const half2_t (&qh)[4][8], unsigned u0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
@@ -354,10 +383,21 @@ __device__ __attribute__((always_inline)) inline void process_unit_fp8(
     vsc[hf] = scl[16 + 8 * hf + srow];
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Rows past the span are masked (p = 0) and stay out of the reference; row u0 is in the span.
+  const float v0 = u0 + srow < span_end ? vsc[0] : 0.0f;
+  const float v1 = u0 + 8 + srow < span_end ? vsc[1] : 0.0f;
+  const float uref = cdna4::wave_allmax(fmaxf(v0, v1));
+  const float inv = uref > 0.0f ? 1.0f / uref : 0.0f;
+  float t[kGroup][8];
+  process_half_fp8<true>(st, kr[0], vr[0], ksc[0], vsc[0] * inv, qh, u0, span_end, pbuf, t,
+                         lane);
+  process_half_fp8<false>(st, kr[1], vr[1], ksc[1], vsc[1] * inv, qh, u0 + 8, span_end, pbuf, t,
+                          lane);
 #pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-    process_half_fp8(st, kr[hf], vr[hf], ksc[hf], vsc[hf], qh, u0 + 8 * hf, span_end, pbuf,
-                     lane);
+  for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      st.o[h][e] = __builtin_fmaf(t[h][e], uref, st.o[h][e]);
 }
 
 // Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh over e4m3 rows (K8 / V8 /

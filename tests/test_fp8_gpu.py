@@ -142,6 +142,41 @@ def test_decode_fp8_every_code(O, attn, torch_mod):
     assert st["ok"], st
 
 
+def test_decode_fp8_v_scale_range(O, attn, torch_mod):
+    """The V row scales enter the f16 numerators only relative to the largest scale of their
+    16-row unit, and the unit's f32 P V sums are multiplied by that scale in f32. So multiplying
+    every V scale by 2^k (V rows near 2^-12 .. 2^-20 for k = -14, max |v| near 2^15 for k = 13)
+    multiplies the output by exactly 2^k, bit for bit, as the exact result does; and rows whose
+    scales spread over 2^8 inside a unit (2^-12 .. 2^-20) stay within a relative tolerance of
+    the oracle."""
+    torch = torch_mod
+    L = max_ctx = 4101
+    d = O.decode_inputs(L, L, max_ctx, q_scale=2.0)
+    k8, ks, v8, vs = encode_host(O, d["k"], d["v"], max_ctx)
+    base = None
+    for k in (0, -14, 13):
+        cache = upload(attn, torch, k8, ks, v8, (vs * np.float32(2.0 ** k)).astype(np.float32),
+                       max_ctx)
+        got, _ = run_decode_fp8(attn, torch, d["q"], d["qg"], cache, L, 128)
+        if base is None:
+            base = got
+            ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs, L, max_ctx)
+            st = O.compare(got, ref)
+            report("fp8 decode unscaled", st)
+            assert st["ok"], st
+        else:
+            assert np.isfinite(got).all()
+            assert np.array_equal(got, (base.astype(np.float64) * 2.0 ** k).astype(np.float32)), k
+    rng = np.random.default_rng(23)
+    vs_mixed = (vs * 2.0 ** (-12 - rng.integers(0, 9, vs.size))).astype(np.float32)
+    cache = upload(attn, torch, k8, ks, v8, vs_mixed, max_ctx)
+    got, n = run_decode_fp8(attn, torch, d["q"], d["qg"], cache, L, 128)
+    ref = O.decode_fp8_f64(d["q"], d["qg"], k8, v8, ks, vs_mixed, L, max_ctx)
+    st = O.compare(got, ref)
+    report(f"fp8 decode V scales 2^-12..2^-20 splits={n}", st)
+    assert np.isfinite(got).all() and st["rel_l2_head"] < 2e-3, st
+
+
 def test_prep_fp8_and_engine_sequence(O, attn, torch_mod):
     """prep_fp8 at several positions: q equals attn_prep's bit for bit, V codes equal the
     oracle's, K within half a code step of the oracle's row; then decode over the cache the

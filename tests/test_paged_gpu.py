@@ -92,3 +92,31 @@ def test_paged_empty_sequence_is_zero(O, attn, torch_mod):
     _, ragged, paged = run_both(O, attn, torch_mod, lens, 6, 8, max_len=16)
     assert not paged[1].any()
     assert np.array_equal(ragged.view(np.uint32), paged.view(np.uint32))
+
+
+def test_paged_lens_past_the_table_are_clamped(O, attn, torch_mod):
+    """lens[s] above max_pages * page_size: the sequence attends to the keys its page-table row
+    addresses (the first max_pages pages), in the split and in the merge, i.e. exactly the ragged
+    decode of the clamped lengths. The table's allocation continues with valid page ids past its
+    last row, so a read beyond a row would show as different values, not as a fault."""
+    torch = torch_mod
+    page, max_pages = 8, 4
+    cap = page * max_pages
+    lens = np.array([40, 100, 7, 33], np.uint32)
+    cut = np.minimum(lens, cap).astype(np.uint32)
+    batch = len(lens)
+    r = O.ragged_inputs(31, cut)
+    sc = attn.RaggedScratch(batch, cap)
+    q, gate = to_dev(torch, r["q"]), to_dev(torch, r["gate"])
+    ragged = torch.full((batch * H * D,), -9123.5, device="cuda")
+    attn.attn_decode_ragged(q, gate, to_dev(torch, r["k"]), to_dev(torch, r["v"]),
+                            to_dev(torch, r["offsets"]), to_dev(torch, cut), ragged, sc)
+    kp, vp, table = paginate(r, cut, page, 31)
+    assert table.shape == (batch, max_pages)
+    padded = torch.zeros((batch + 16, max_pages), dtype=torch.int32, device="cuda")
+    padded[:batch] = torch.from_numpy(table).cuda()
+    paged = torch.full((batch * H * D,), 7777.25, device="cuda")
+    attn.attn_decode_paged(q, gate, to_dev(torch, kp), to_dev(torch, vp), padded[:batch], page,
+                           to_dev(torch, lens), paged, sc)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(ragged).view(np.uint32), to_host(paged).view(np.uint32))
