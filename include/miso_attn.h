@@ -253,6 +253,71 @@ int miso_attn_gemm_input(const float* x, uint16_t* xh, float* xs, uint32_t k, ui
 int miso_attn_gemm(const uint8_t* w, int format, const uint16_t* xh, const float* xs, float* y,
                    uint32_t k, uint32_t n_rows, uint32_t n_tok, uint32_t ldy, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * One attention layer step: the host wiring of the engine's attention_decode / attention_prefill
+ * (src/engine/attention.hip:76-148) over the entry points above, with the engine's sizing
+ * retuned for one MI355X (the reference's values in brackets):
+ *   MISO_ATTN_LAYER_MAX_SPLITS         decode split cap         [60,  src/engine/attention.hpp:46]
+ *   MISO_ATTN_LAYER_MAX_CHUNK          prefill chunk, tokens    [512, src/engine/model.hpp:58]
+ *   MISO_ATTN_LAYER_PREFILL_MIN_TOKENS prefill from this many   [8,   src/engine/model.hpp:80]
+ * ------------------------------------------------------------------------------------------- */
+#define MISO_ATTN_LAYER_MAX_SPLITS 128
+#define MISO_ATTN_LAYER_MAX_CHUNK 4096
+#define MISO_ATTN_LAYER_PREFILL_MIN_TOKENS 12
+
+/* A quantized matrix (device): n_rows rows of k weights in the r1 layout of `format` (0: Q4_K, 144
+ * bytes per 256 weights; 1: Q6_K, k / 256 x 210 bytes rounded up to 16 per row). */
+typedef struct miso_attn_qmatrix {
+  const uint8_t* w;
+  int32_t format;
+  uint32_t n_rows;
+  uint32_t k;
+} miso_attn_qmatrix;
+
+/* One layer's weights (device), the engine's AttentionLayer (src/engine/attention.hpp:15-26) as
+ * four separate matrices: q (8192 x 2048: per head 256 query then 256 gate rows), k and v
+ * (512 x 2048), o (2048 x 4096); attn_norm [2048], q_norm / k_norm [256] (GGUF stores 1 + w),
+ * inv_freq [32] (RoPE). */
+typedef struct miso_attn_layer {
+  miso_attn_qmatrix q, k, v, o;
+  const float* attn_norm;
+  const float* q_norm;
+  const float* k_norm;
+  const float* inv_freq;
+} miso_attn_layer;
+
+/* Device floats of the decode / prefill workspaces (the engine's AttentionScratch and
+ * AttentionPrefillScratch, src/engine/attention.hpp:44-69), for chunks of up to max_tok tokens. */
+uint64_t miso_attn_layer_decode_ws(void);
+uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok);
+
+/* The token at position len: h += delta (delta may be NULL), y = o(Attention(RMSNorm(h))), K/V
+ * appended at len. Replaces attention_decode() (src/engine/attention.hip:76-114): RMSNorm, the
+ * q / k / v projections in one launch (Q4_K q and k, Q6_K v; other mixes one GEMV each), prep,
+ * split + combine over len + 1 keys with miso_attn_n_splits(len + 1, MISO_ATTN_LAYER_MAX_SPLITS)
+ * splits, output projection. h, y: 2048 floats; ws: miso_attn_layer_decode_ws() floats. Rejects
+ * len >= max_ctx ("KV cache is full", as the reference) and matrices of other shapes. */
+int miso_attn_layer_decode(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                           uint32_t len, uint32_t max_ctx, float* h, const float* delta, float* y,
+                           float eps, float* ws, void* stream);
+
+/* n consecutive tokens at pos0 (h, delta, y: [n][2048]). Replaces attention_prefill()
+ * (src/engine/attention.hip:116-148): RMSNorm, the prefill GEMMs, batched prep, causal attention
+ * over the cache up to each token, output GEMM. ws: miso_attn_layer_prefill_ws(max_tok) floats.
+ * Rejects n > max_tok and pos0 + n > max_ctx. n == 0 is a no-op. */
+int miso_attn_layer_prefill(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                            uint32_t pos0, uint32_t n, uint32_t max_ctx, float* h,
+                            const float* delta, float* y, float eps, float* ws, uint32_t max_tok,
+                            void* stream);
+
+/* n tokens at pos0 with the engine's policy (src/engine/model.hip:130-175, for this layer):
+ * n < MISO_ATTN_LAYER_PREFILL_MIN_TOKENS, one decode step per token; otherwise prefill chunks of
+ * min(chunk ? chunk : MISO_ATTN_LAYER_MAX_CHUNK, max_tok) tokens. */
+int miso_attn_layer_ingest(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                           uint32_t pos0, uint32_t n, uint32_t max_ctx, float* h,
+                           const float* delta, float* y, float eps, float* decode_ws,
+                           float* prefill_ws, uint32_t max_tok, uint32_t chunk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

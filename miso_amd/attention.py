@@ -10,6 +10,7 @@ torch is used for device memory and streams only; all arithmetic runs in the HIP
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -410,3 +411,108 @@ def gemm(w, fmt: str, n_rows: int, k: int, inp: GemmInput, y, ldy: int, stream=N
         _need(y, "y", torch.float32, (inp.n_tok - 1) * ldy + n_rows)
     _lib.check(_lib.load().miso_attn_gemm(_ptr(w), GEMM_FORMATS[fmt], _ptr(inp.xh), _ptr(inp.xs),
                                           _ptr(y), k, n_rows, inp.n_tok, ldy, _stream(stream)))
+
+
+# ------------------------------------------------------------------------------------------------
+# One attention layer step (src/engine/attention.hip:76-148), engine sizing retuned for MI355X
+# ------------------------------------------------------------------------------------------------
+
+LAYER_MAX_SPLITS = 128        # decode split cap (reference: 60, src/engine/attention.hpp:46)
+LAYER_MAX_CHUNK = 4096        # prefill chunk (reference: 512, src/engine/model.hpp:58)
+LAYER_PREFILL_MIN_TOKENS = 12  # prefill from this many tokens (reference: 8, model.hpp:80)
+
+
+class _QMatrix(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("format", ctypes.c_int32), ("n_rows", ctypes.c_uint32),
+                ("k", ctypes.c_uint32)]
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [("q", _QMatrix), ("k", _QMatrix), ("v", _QMatrix), ("o", _QMatrix),
+                ("attn_norm", ctypes.c_void_p), ("q_norm", ctypes.c_void_p),
+                ("k_norm", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p)]
+
+
+class Layer:
+    """One attention layer's device weights: (r1 bytes, "q4_k" | "q6_k") for q (8192 x 2048), k and
+    v (512 x 2048) and o (2048 x 4096); attn_norm [2048], q_norm / k_norm [256], inv_freq [32]
+    (float32). Keeps the tensors alive for the C description it holds."""
+
+    SHAPES = {"q": (8192, 2048), "k": (512, 2048), "v": (512, 2048), "o": (2048, 4096)}
+
+    def __init__(self, q, k, v, o, attn_norm, q_norm, k_norm, inv_freq):
+        self._keep = (q, k, v, o, attn_norm, q_norm, k_norm, inv_freq)
+        mats = {}
+        for name, (t, fmt) in (("q", q), ("k", k), ("v", v), ("o", o)):
+            if fmt not in GEMM_FORMATS:
+                raise ValueError(f"{name}: format must be 'q4_k' or 'q6_k'")
+            n, kk = self.SHAPES[name]
+            row = kk // 256 * 144 if fmt == "q4_k" else q6k_row_bytes(kk)
+            _need(t, name, torch.uint8, n * row)
+            mats[name] = _QMatrix(_ptr(t), GEMM_FORMATS[fmt], n, kk)
+        for name, t, n in (("attn_norm", attn_norm, 2048), ("q_norm", q_norm, DIM),
+                           ("k_norm", k_norm, DIM), ("inv_freq", inv_freq, 32)):
+            _need(t, name, torch.float32, n)
+        self.c = _Layer(mats["q"], mats["k"], mats["v"], mats["o"], _ptr(attn_norm),
+                        _ptr(q_norm), _ptr(k_norm), _ptr(inv_freq))
+
+
+class LayerWorkspace:
+    """Device workspaces of the layer steps: decode, and prefill chunks of up to max_tok tokens."""
+
+    def __init__(self, max_tok: int = LAYER_MAX_CHUNK, device="cuda"):
+        lib = _lib.load()
+        self.max_tok = max_tok
+        self.decode = torch.empty(int(lib.miso_attn_layer_decode_ws()), dtype=torch.float32,
+                                  device=device)
+        self.prefill = torch.empty(max(1, int(lib.miso_attn_layer_prefill_ws(max_tok))),
+                                   dtype=torch.float32, device=device)
+
+
+def _layer_cache(k_cache, v_cache, max_ctx: int):
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(t, name, _cache_dtype(t), KV_HEADS * max_ctx * DIM)
+    return _ptr(k_cache), _ptr(v_cache)
+
+
+def layer_decode(layer: Layer, k_cache, v_cache, max_ctx: int, length: int, h, delta, y,
+                 eps: float, ws: LayerWorkspace, stream=None) -> None:
+    """The token at position `length`: h += delta (delta may be None), y = the layer's output;
+    K/V appended at `length` (src/engine/attention.hip:76-114)."""
+    _need(h, "h", torch.float32, 2048)
+    _need(y, "y", torch.float32, 2048)
+    if delta is not None:
+        _need(delta, "delta", torch.float32, 2048)
+    kc, vc = _layer_cache(k_cache, v_cache, max_ctx)
+    _lib.check(_lib.load().miso_attn_layer_decode(
+        ctypes.addressof(layer.c), kc, vc, length, max_ctx, _ptr(h), _ptr(delta), _ptr(y), eps,
+        _ptr(ws.decode), _stream(stream)))
+
+
+def _rows(n: int, **tensors):
+    for name, t in tensors.items():
+        if t is not None:
+            _need(t, name, torch.float32, n * 2048)
+
+
+def layer_prefill(layer: Layer, k_cache, v_cache, max_ctx: int, pos0: int, n: int, h, delta, y,
+                  eps: float, ws: LayerWorkspace, stream=None) -> None:
+    """n tokens at pos0 ([n][2048] h / delta / y) in one prefill step
+    (src/engine/attention.hip:116-148)."""
+    _rows(n, h=h, delta=delta, y=y)
+    kc, vc = _layer_cache(k_cache, v_cache, max_ctx)
+    _lib.check(_lib.load().miso_attn_layer_prefill(
+        ctypes.addressof(layer.c), kc, vc, pos0, n, max_ctx, _ptr(h), _ptr(delta), _ptr(y), eps,
+        _ptr(ws.prefill), ws.max_tok, _stream(stream)))
+
+
+def layer_ingest(layer: Layer, k_cache, v_cache, max_ctx: int, pos0: int, n: int, h, delta, y,
+                 eps: float, ws: LayerWorkspace, chunk: int = 0, stream=None) -> None:
+    """n tokens at pos0 with the engine's policy: one decode step per token below
+    LAYER_PREFILL_MIN_TOKENS, otherwise prefill chunks of min(chunk or LAYER_MAX_CHUNK,
+    ws.max_tok) tokens."""
+    _rows(n, h=h, delta=delta, y=y)
+    kc, vc = _layer_cache(k_cache, v_cache, max_ctx)
+    _lib.check(_lib.load().miso_attn_layer_ingest(
+        ctypes.addressof(layer.c), kc, vc, pos0, n, max_ctx, _ptr(h), _ptr(delta), _ptr(y), eps,
+        _ptr(ws.decode), _ptr(ws.prefill), ws.max_tok, chunk, _stream(stream)))

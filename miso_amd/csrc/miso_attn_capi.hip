@@ -15,6 +15,7 @@
 #include "attention_prefill.hpp"
 #include "q4k_gemv.hpp"
 #include "q6k_gemv.hpp"
+#include "attention_layer.hpp"
 #include "mixed_gemv.hpp"
 #include "qgemm.hpp"
 
@@ -40,44 +41,10 @@ int launched(const char* fn) {
   return static_cast<int>(err);
 }
 
-// Q4_K GEMV launch shapes, from a sweep of workgroup size x passes per wave at the engine's
-// projections (f16 activations, HBM-resident weights, graph-replayed). Up to 1024 rows: workgroups
-// of max(128, K / 32) threads and one pass per wave (attn_k 512 x 2048: 2.38 us against 2.67 us
-// with one-wave workgroups and 3.65 us with 4-wave workgroups of 4 passes). More rows: 4-wave
-// workgroups with two passes (attn_q 8192 x 2048: 4.30 us, 4 passes 4.42 us; attn_output 2048 x
-// 4096: 3.31 us), one for K = 8192. One step per wave up to 8192 workgroups (grid-stride beyond).
-template <k::ActFormat A, unsigned K, int kBlock, int kRows>
-void launch_q4k_shape(const k::Q4kGemvParams& p, hipStream_t stream) {
-  const unsigned per_wg = (kBlock / 64) * k::q4k_gemv_wave_rows<K, kRows>();
-  unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
-  grid = grid < 8192u ? grid : 8192u;
-  k::q4k_gemv_kernel<A, K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
-}
-
-template <k::ActFormat A, unsigned K>
-void launch_q4k(const k::Q4kGemvParams& p, hipStream_t stream) {
-  if (p.n_rows <= 1024)
-    launch_q4k_shape<A, K, (K / 32 > 128 ? K / 32 : 128), 1>(p, stream);
-  else
-    launch_q4k_shape<A, K, 256, (K == 8192 ? 1 : 2)>(p, stream);
-}
-
-// Q6_K GEMV launch, the same shape rule as the Q4_K one (attn_v 512 x 2048: 2.57 us).
-template <unsigned K, int kBlock, int kRows>
-void launch_q6k_shape(const k::Q6kGemvParams& p, hipStream_t stream) {
-  const unsigned per_wg = (kBlock / 64) * k::q6k_gemv_wave_rows<K, kRows>();
-  unsigned grid = (p.n_rows + per_wg - 1) / per_wg;
-  grid = grid < 8192u ? grid : 8192u;
-  k::q6k_gemv_kernel<K, kBlock, kRows><<<grid, kBlock, 0, stream>>>(p);
-}
-
-template <unsigned K>
-void launch_q6k(const k::Q6kGemvParams& p, hipStream_t stream) {
-  if (p.n_rows <= 1024)
-    launch_q6k_shape<K, (K / 32 > 128 ? K / 32 : 128), 1>(p, stream);
-  else
-    launch_q6k_shape<K, 256, (K == 8192 ? 1 : 2)>(p, stream);
-}
+// The GEMV launch shapes are the layer wiring's (attention_layer.hpp: a sweep at the engine's
+// projections).
+using k::layer::q4k_gemv;
+using k::layer::q6k_gemv;
 
 template <bool kPrepared, int kPipeline>
 __global__ void __launch_bounds__(64) combine_range_kernel(k::AttnCombineParams p, unsigned first,
@@ -469,13 +436,13 @@ int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
   const k::Q4kGemvParams p{w, x, y, n_rows};
   const hipStream_t st = as_stream(stream);
   if (act_format == 1) {
-    if (k == 2048) launch_q4k<k::ActFormat::Fp16, 2048>(p, st);
-    else if (k == 4096) launch_q4k<k::ActFormat::Fp16, 4096>(p, st);
-    else launch_q4k<k::ActFormat::Fp16, 8192>(p, st);
+    if (k == 2048) q4k_gemv<k::ActFormat::Fp16, 2048>(p, st);
+    else if (k == 4096) q4k_gemv<k::ActFormat::Fp16, 4096>(p, st);
+    else q4k_gemv<k::ActFormat::Fp16, 8192>(p, st);
   } else {
-    if (k == 2048) launch_q4k<k::ActFormat::Int8, 2048>(p, st);
-    else if (k == 4096) launch_q4k<k::ActFormat::Int8, 4096>(p, st);
-    else launch_q4k<k::ActFormat::Int8, 8192>(p, st);
+    if (k == 2048) q4k_gemv<k::ActFormat::Int8, 2048>(p, st);
+    else if (k == 4096) q4k_gemv<k::ActFormat::Int8, 4096>(p, st);
+    else q4k_gemv<k::ActFormat::Int8, 8192>(p, st);
   }
   return launched("miso_attn_q4k_gemv");
 }
@@ -490,9 +457,9 @@ int miso_attn_q6k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_ro
     return fail("miso_attn_q6k_gemv", "k must be 2048, 4096 or 8192");
   const k::Q6kGemvParams p{w, x, y, n_rows};
   const hipStream_t st = as_stream(stream);
-  if (k == 2048) launch_q6k<2048>(p, st);
-  else if (k == 4096) launch_q6k<4096>(p, st);
-  else launch_q6k<8192>(p, st);
+  if (k == 2048) q6k_gemv<2048>(p, st);
+  else if (k == 4096) q6k_gemv<4096>(p, st);
+  else q6k_gemv<8192>(p, st);
   return launched("miso_attn_q6k_gemv");
 }
 
@@ -519,12 +486,11 @@ int miso_attn_qkv_gemv(const uint8_t* wq, uint32_t nq, float* yq, const uint8_t*
     return fail("miso_attn_qkv_gemv", kBadPtr);
   if (nq == 0 || nk == 0 || nv == 0)
     return fail("miso_attn_qkv_gemv", "all three row counts must be >= 1");
-  // Logical grids sized for attn_q (8192 rows) and attn_k (512 rows), 16 rows per Q4_K
-  // workgroup, and attn_v (512 rows, 8 per Q6_K workgroup); other row counts grid-stride.
-  constexpr unsigned kQ = 512, kK = 32, kV = 64;
+  // One launch; its logical grids are sized for 8192 / 512 / 512 rows (16 rows per Q4_K workgroup,
+  // 8 per Q6_K), other counts grid-stride.
   const k::Q4kGemvParams pq{wq, x, yq, nq}, pk{wk, x, yk, nk};
   const k::Q6kGemvParams pv{wv, x, yv, nv};
-  k::qkv_gemv_kernel<kQ, kK, kV, 256><<<kQ + kK + kV, 256, 0, as_stream(stream)>>>(pq, pk, pv);
+  k::qkv_gemv_kernel<512, 32, 64, 256><<<512 + 32 + 64, 256, 0, as_stream(stream)>>>(pq, pk, pv);
   return launched("miso_attn_qkv_gemv");
 }
 
@@ -536,11 +502,9 @@ int miso_attn_gemm_input(const float* x, uint16_t* xh, float* xs, uint32_t k, ui
     return fail("miso_attn_gemm_input", kBadPtr);
   if (k == 0 || k % 256 != 0)
     return fail("miso_attn_gemm_input", "k must be a positive multiple of 256");
-  const k::QGemmActParams p{x, reinterpret_cast<_Float16*>(xh), xs, k, n_tok};
   // One thread per 8 elements (the kernel grid-strides, so the reference's one-thread-per-group
   // grid also works, with four passes per thread).
-  const unsigned quarters = n_tok * (k / 8);
-  k::qgemm_act_kernel<<<(quarters + 255) / 256, 256, 0, as_stream(stream)>>>(p);
+  k::layer::gemm_input(x, k, n_tok, reinterpret_cast<_Float16*>(xh), xs, as_stream(stream));
   return launched("miso_attn_gemm_input");
 }
 
@@ -563,6 +527,97 @@ int miso_attn_gemm(const uint8_t* w, int format, const uint16_t* xh, const float
   else
     return fail("miso_attn_gemm", "format must be 0 (Q4_K) or 1 (Q6_K)");
   return launched("miso_attn_gemm");
+}
+
+uint64_t miso_attn_layer_decode_ws(void) { return k::layer::decode_workspace_floats(); }
+
+uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok) {
+  return k::layer::prefill_workspace_floats(max_tok);
+}
+
+}  // extern "C"
+
+namespace {
+
+bool bad_matrix(const miso_attn_qmatrix& m) {
+  return bad_ptr(m.w) || (m.format != 0 && m.format != 1);
+}
+
+// The C description of a layer as the wiring's (rejects null or misaligned pointers and unknown
+// formats, then the shapes the projection layout needs).
+const char* layer_view(const miso_attn_layer* in, k::layer::Weights& w) {
+  if (in == nullptr)
+    return kBadPtr;
+  if (bad_matrix(in->q) || bad_matrix(in->k) || bad_matrix(in->v) || bad_matrix(in->o) ||
+      any_bad(in->attn_norm, in->q_norm, in->k_norm, in->inv_freq))
+    return "a layer pointer is NULL or not 16-byte aligned, or a format is not 0 or 1";
+  auto view = [](const miso_attn_qmatrix& m) {
+    return k::layer::Matrix{m.w, static_cast<k::layer::Format>(m.format), m.n_rows, m.k};
+  };
+  w = {view(in->q), view(in->k), view(in->v), view(in->o),
+       in->attn_norm, in->q_norm, in->k_norm, in->inv_freq};
+  return k::layer::check_weights(w);
+}
+
+int layer_result(const char* fn, const char* err) {
+  return err != nullptr ? fail(fn, err) : launched(fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int miso_attn_layer_decode(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                           uint32_t len, uint32_t max_ctx, float* h, const float* delta, float* y,
+                           float eps, float* ws, void* stream) {
+  constexpr const char* fn = "miso_attn_layer_decode";
+  k::layer::Weights w;
+  if (const char* err = layer_view(layer, w))
+    return fail(fn, err);
+  if (any_bad(k_cache, v_cache, h, y, ws) || (delta != nullptr && bad_ptr(delta)))
+    return fail(fn, kBadPtr);
+  return layer_result(fn, k::layer::decode_step(w, as_half(k_cache), as_half(v_cache), len,
+                                                max_ctx, h, delta, y, eps,
+                                                k::layer::decode_workspace(ws),
+                                                as_stream(stream)));
+}
+
+int miso_attn_layer_prefill(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                            uint32_t pos0, uint32_t n, uint32_t max_ctx, float* h,
+                            const float* delta, float* y, float eps, float* ws, uint32_t max_tok,
+                            void* stream) {
+  constexpr const char* fn = "miso_attn_layer_prefill";
+  if (n == 0)
+    return 0;
+  k::layer::Weights w;
+  if (const char* err = layer_view(layer, w))
+    return fail(fn, err);
+  if (any_bad(k_cache, v_cache, h, y, ws) || (delta != nullptr && bad_ptr(delta)))
+    return fail(fn, kBadPtr);
+  return layer_result(fn, k::layer::prefill_step(w, as_half(k_cache), as_half(v_cache), pos0, n,
+                                                 max_ctx, h, delta, y, eps,
+                                                 k::layer::prefill_workspace(ws, max_tok),
+                                                 max_tok, as_stream(stream)));
+}
+
+int miso_attn_layer_ingest(const miso_attn_layer* layer, uint16_t* k_cache, uint16_t* v_cache,
+                           uint32_t pos0, uint32_t n, uint32_t max_ctx, float* h,
+                           const float* delta, float* y, float eps, float* decode_ws,
+                           float* prefill_ws, uint32_t max_tok, uint32_t chunk, void* stream) {
+  constexpr const char* fn = "miso_attn_layer_ingest";
+  if (n == 0)
+    return 0;
+  k::layer::Weights w;
+  if (const char* err = layer_view(layer, w))
+    return fail(fn, err);
+  if (any_bad(k_cache, v_cache, h, y, decode_ws) || (delta != nullptr && bad_ptr(delta)) ||
+      (n >= k::layer::kPrefillMinTokens && bad_ptr(prefill_ws)))
+    return fail(fn, kBadPtr);
+  return layer_result(
+      fn, k::layer::ingest(w, as_half(k_cache), as_half(v_cache), pos0, n, max_ctx, h, delta, y,
+                           eps, k::layer::decode_workspace(decode_ws),
+                           k::layer::prefill_workspace(prefill_ws, max_tok), max_tok, chunk,
+                           as_stream(stream)));
 }
 
 }  // extern "C"

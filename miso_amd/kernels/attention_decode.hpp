@@ -1025,7 +1025,9 @@ __global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedPar
       (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
 }
 
-// One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's.
+// One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's. (A
+// template, so every translation unit including this header may instantiate it.)
+template <int = 0>
 __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParams p) {
   constexpr unsigned kGroup = attn::kQHeads / attn::kKvHeads, kTiles = attn::kDim / 64;
   const unsigned item = blockIdx.x;

@@ -103,6 +103,9 @@ __device__ inline void qgemm_act_op(const QGemmActParams& p, unsigned first, uns
   }
 }
 
+// A template with a defaulted parameter: launches keep the reference's qgemm_act_kernel<<<...>>>
+// form, and several translation units may include this header without clashing symbols.
+template <int = 0>
 __global__ void __launch_bounds__(256) qgemm_act_kernel(QGemmActParams p) {
   qgemm_act_op(p, 0, p.n_tok * (p.k / 32));
 }

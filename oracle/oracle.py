@@ -410,6 +410,48 @@ def prep_f64(qg, k, v, q_norm, k_norm, inv_freq_arr, pos: int, eps: float):
     return q_out, k_out, v_out
 
 
+def rmsnorm_f64(h, weight, eps: float) -> np.ndarray:
+    """The reference's residual RMSNorm (kernels/rmsnorm.hpp:2-4,40-47) in float64, per row:
+    h / sqrt(mean(h^2) + eps) * weight (the GGUF weight already stores 1 + w)."""
+    h = np.asarray(h, np.float64)
+    r = 1.0 / np.sqrt((h * h).mean(axis=-1, keepdims=True) + float(eps))
+    return h * r * np.asarray(weight, np.float64)
+
+
+def layer_f64(h, delta, wq, wk, wv, wo, attn_norm, q_norm, k_norm, inv_freq_arr, pos0: int,
+              max_ctx: int, eps: float, k16=None, v16=None):
+    """One gated attention layer over T consecutive tokens at pos0..pos0 + T - 1 (the engine's
+    attention_decode / attention_prefill, src/engine/attention.hip:76-148, token by token):
+    h += delta; xn = RMSNorm(h) attn_norm; [q + gate | k | v] = W xn with xn rounded to f16 (the
+    reference's GEMV and GEMM take f16 activations: kernels/q4k_gemv.hpp ActFormat::Fp16,
+    kernels/qgemm.hpp qgemm_act); per-head norms, RoPE and the f16 K/V append (prep_f64);
+    attention over the cache up to the token (decode_f64); y = W_o core with core rounded to f16.
+    w*: dequantized float matrices [rows][k]. k16 / v16: the f16 caches [2][max_ctx][256]
+    (updated; new zero caches when None). Returns (h, y [T][2048] float64, k16, v16)."""
+    h = np.asarray(h, np.float32).reshape(-1, 2048).copy()
+    if delta is not None:
+        h = (h + np.asarray(delta, np.float32).reshape(-1, 2048)).astype(np.float32)
+    n_tok = h.shape[0]
+    if k16 is None:
+        k16 = np.zeros((KV_HEADS, max_ctx, DIM), np.uint16)
+        v16 = np.zeros((KV_HEADS, max_ctx, DIM), np.uint16)
+    xn = rmsnorm_f64(h, attn_norm, eps).astype(np.float32).astype(np.float16).astype(np.float64)
+    proj = np.concatenate([xn @ np.asarray(w, np.float64).T for w in (wq, wk, wv)], axis=1)
+    proj = proj.astype(np.float32)
+    core = np.empty((n_tok, Q_HEADS * DIM), np.float64)
+    for t in range(n_tok):
+        pos = pos0 + t
+        qg, kk, vv = proj[t, :8192], proj[t, 8192:8704], proj[t, 8704:]
+        q, k_new, v_new = prep_f64(qg, kk, vv, q_norm, k_norm, inv_freq_arr, pos, eps)
+        k16[:, pos] = k_new
+        v16[:, pos] = v_new
+        core[t] = decode_f64(q.astype(np.float32), qg, k16.reshape(-1), v16.reshape(-1), pos + 1,
+                             max_ctx).reshape(-1)
+    core16 = core.astype(np.float32).astype(np.float16).astype(np.float64)
+    y = core16 @ np.asarray(wo, np.float64).T
+    return h, y, k16, v16
+
+
 def ref_n_splits(length: int, max_splits: int) -> int:
     return int(lib().oracle_ref_n_splits(length, max_splits))
 

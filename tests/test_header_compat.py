@@ -34,6 +34,11 @@ CALLERS = [
     ("tests/test_qgemm.hip", "qgemm.hpp"),
     ("src/engine/weights.hip", "qgemm.hpp"),
 ]
+
+# The engine drop-in (miso_amd/engine/attention.{hpp,hip}): the reference's src/engine/model.hip
+# compiles unchanged with it in place of src/engine/attention.hpp, and the drop-in's own source
+# compiles against the engine's headers.
+ENGINE = ROOT / "miso_amd"
 OURS = ("attention_decode.hpp", "attention_prefill.hpp", "q4k_gemv.hpp", "q6k_gemv.hpp",
         "mixed_gemv.hpp", "qgemm.hpp")
 
@@ -62,3 +67,27 @@ def test_reference_caller_compiles_against_our_headers(caller, direct, tmp_path)
             assert all(Path(p).resolve().as_posix().startswith(ours) for p in hits), hits
     if direct:
         assert any(p.endswith("/" + direct) for p in included)
+
+
+def _hipcc(src, tmp_path, includes):
+    cmd = [HIPCC, "-std=c++20", "-O1", "--offload-arch=gfx950", "-c", str(src),
+           "-o", str(tmp_path / "x.o"), "-H",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           *[a for inc in includes for a in ("-I", str(inc))],
+           "-isystem", str(REF / "third_party")]
+    return subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+
+
+def test_engine_model_compiles_with_the_attention_drop_in(tmp_path):
+    res = _hipcc(REF / "src/engine/model.hip", tmp_path,
+                 [ENGINE, ROOT / "miso_amd" / "kernels", REF / "kernels", REF / "src"])
+    assert res.returncode == 0, res.stderr[-4000:]
+    included = [l.lstrip(". ").strip() for l in res.stderr.splitlines() if l.startswith(".")]
+    hits = [p for p in included if p.endswith("engine/attention.hpp")]
+    assert hits and all(Path(p).resolve().as_posix().startswith(str(ENGINE)) for p in hits), hits
+
+
+def test_attention_drop_in_compiles_against_the_engine_headers(tmp_path):
+    res = _hipcc(ENGINE / "engine" / "attention.hip", tmp_path,
+                 [ENGINE, ROOT / "miso_amd" / "kernels", REF / "kernels", REF / "src"])
+    assert res.returncode == 0, res.stderr[-4000:]

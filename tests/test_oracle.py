@@ -283,3 +283,30 @@ def test_ragged_oracle_equals_decode_per_sequence(O):
         qg[:, D:] = r["gate"][s * H * D:(s + 1) * H * D].reshape(H, D)
         dec = O.decode_f64(r["q"][s * H * D:(s + 1) * H * D], qg.ravel(), k, v, L, L)
         np.testing.assert_array_equal(out[s], dec)
+
+
+def test_layer_oracle_single_token_closed_form():
+    """At position 0 the attention sees one key: softmax = 1, so head h's core is the f16 V row
+    of its KV head times sigmoid(gate), and y = W_o f16(core) -- independent of decode_f64. The
+    residual update and the cache row come out of the same call."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(5)
+    wq = rng.standard_normal((8192, 2048)) * 0.02
+    wk = rng.standard_normal((512, 2048)) * 0.02
+    wv = rng.standard_normal((512, 2048)) * 0.02
+    wo = rng.standard_normal((2048, 4096)) * 0.02
+    an, qn, kn = (1 + 0.1 * rng.standard_normal(n) for n in (2048, 256, 256))
+    h = rng.standard_normal((1, 2048)).astype(np.float32)
+    dl = rng.standard_normal((1, 2048)).astype(np.float32)
+    hh, y, k16, v16 = O.layer_f64(h, dl, wq, wk, wv, wo, an, qn, kn, O.inv_freq(1e7), 0, 4, 1e-6)
+    assert np.array_equal(hh, (h + dl).astype(np.float32))
+    hs = (h + dl).astype(np.float64)
+    xn = hs / np.sqrt((hs * hs).mean() + 1e-6) * an   # RMSNorm, restated from its definition
+    xn = xn.astype(np.float32).astype(np.float16).astype(np.float64)
+    proj = np.concatenate([xn @ w.T for w in (wq, wk, wv)], axis=1).astype(np.float32)[0]
+    v_rows = O.f16_to_f32(v16[:, 0]).astype(np.float64)          # [2][256], position 0
+    assert np.array_equal(v16[:, 0], O.f32_to_f16(proj[8704:].reshape(2, 256)))
+    gate = proj[:8192].reshape(16, 512)[:, 256:].astype(np.float64)
+    core = np.stack([v_rows[hd // 8] / (1 + np.exp(-gate[hd])) for hd in range(16)])
+    y_ref = core.reshape(-1).astype(np.float32).astype(np.float16).astype(np.float64) @ wo.T
+    assert np.allclose(y[0], y_ref, rtol=1e-9, atol=1e-9)
