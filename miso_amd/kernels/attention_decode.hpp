@@ -760,6 +760,500 @@ __device__ __attribute__((always_inline)) inline void split_partial(
                              base, sh, more);
 }
 
+// ------------------------------------------------------------------------------------------------
+// The f32-precision split on the matrix cores.
+//
+// Products: every key is f16 (exact in f32), the query and the softmax numerators are f32. Each
+// f32 operand x is carried as the f16 pair (hi, lo) = (f16(x), f16((x - hi) 2^11)), so x = hi +
+// 2^-11 lo to ~2^-22 relative, and hi * k, lo * k are exact f32 products. The 8 query heads of
+// a KV head times (hi, lo) are exactly the 16 columns of v_mfma_f32_16x16x32_f16: column h holds
+// head h's hi part, column 8 + h its lo part, so one MFMA computes both products of every head
+// and the two columns are joined as s = hi + 2^-11 lo (lane c and lane c ^ 8 of a row, one DPP
+// move). The same holds for O += V^T P^T with the numerators' (hi, lo) as the columns.
+//
+// Schedule per split workgroup (4 waves): 32-key tiles of K and V stream into a 4-stage LDS ring
+// by direct global -> LDS loads (each wave copies 8 rows of each tensor, 1 KiB per instruction),
+// one barrier per tile. Every wave computes each tile's scores and softmax decisions itself, so
+// the four waves hold identical (m, l) without exchanging anything, and each wave owns 64 of the
+// 256 value dimensions of O -- there is no cross-wave merge. The loop is software-pipelined:
+// iteration t issues the 16 score MFMAs of tile t + 1 and, between them, the VALU softmax of tile
+// t (whose scores the previous iteration produced), then the 4 P V MFMAs of tile t. Tiles t and
+// t + 1 are in use and t + 2, t + 3 in flight.
+//
+// LDS layouts (16-byte chunk c of tile row r at chunk position c ^ s(r) of the row):
+//   K: s(r) = r % 16. The A operand read (ds_read_b128) of 16 lanes takes one chunk of 16
+//      consecutive rows: 16 distinct positions mod 16.
+//   V: s(r) = 2 (r % 8). A transpose read (ds_read_b64_tr_b16) of 32 lanes takes 32 bytes (one
+//      16-dimension block) of 8 rows: 8 distinct 32-byte bank groups.
+// Operand layouts of the 16x16x32 MFMA (lane l, g = l / 16, c = l % 16; the k index 8 g + j):
+//   S^T = K Q^T: A = K rows 16 kb + c, dimensions 8 (4 s + g) + j at k-step s; B = column c of
+//     the query pairs over the same dimensions; the result holds keys 16 kb + 4 g + i, column c.
+//   O^T += V^T P^T: k-slot 8 g + j is key 4 g + j (j < 4) or 16 + 4 g + j - 4 (j >= 4) of the
+//     tile -- exactly the keys of the lane's two score results, so each lane's numerators are its
+//     own B operand; A = V^T of dimensions 16 blk + c over those keys (two transpose reads).
+// ------------------------------------------------------------------------------------------------
+
+constexpr unsigned kTileKeys = 32;
+constexpr unsigned kTileStages = 4;
+constexpr unsigned kTileBytes = kTileKeys * attn::kDim * 2;  // 16 KiB per K or V tile
+constexpr float kLoScale = 2048.0f;                          // 2^11: the lo half of a pair
+constexpr float kLoWeight = 1.0f / 2048.0f;
+
+// K tiles in the first 64 KiB (so a K operand address plus its stage offset stays under the
+// 16-bit instruction offset), V tiles in the next 64 KiB, then the KV head's 8 query rows.
+struct alignas(1024) TileShared {
+  unsigned char k[kTileStages][kTileBytes];
+  unsigned char v[kTileStages][kTileBytes];
+  float q[kGroup][attn::kDim];
+};
+
+__device__ inline unsigned tile_swz_k(unsigned row, unsigned chunk) { return chunk ^ (row & 15u); }
+__device__ inline unsigned tile_swz_v(unsigned row, unsigned chunk) {
+  return chunk ^ (2u * (row & 7u));
+}
+
+typedef cdna4::float4_t f32x4;
+
+__device__ __attribute__((always_inline)) inline f32x4 mfma16(const cdna4::half8_t& a,
+                                                             const cdna4::half8_t& b,
+                                                             const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __attribute__((always_inline)) inline cdna4::half8_t lds_b128(unsigned addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) cdna4::half8_t*>(addr);
+}
+
+typedef __fp16 tile_fp16x4 __attribute__((vector_size(8)));
+__device__ __attribute__((always_inline)) inline cdna4::half4_t lds_tr_b64(unsigned addr) {
+  const tile_fp16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+      reinterpret_cast<__attribute__((address_space(3))) tile_fp16x4*>(addr));
+  return __builtin_bit_cast(cdna4::half4_t, raw);
+}
+
+// A workgroup barrier that waits only for this wave's LDS reads: the tiles in flight (direct LDS
+// loads, counted by vmcnt) stay in flight across it. A compiler memory barrier on both sides.
+__device__ __attribute__((always_inline)) inline void tile_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Wait until this wave's copy of the tile followed by `after` (< 3) more tile copies has landed
+// (8 instructions per tile copy).
+__device__ __attribute__((always_inline)) inline void wait_tiles_after(unsigned after) {
+  switch (after) {
+    case 0: cdna4::wait_vmcnt<0>(); break;
+    case 1: cdna4::wait_vmcnt<8>(); break;
+    default: cdna4::wait_vmcnt<16>(); break;
+  }
+}
+
+// Copy of this wave's 8 rows of a K and a V tile whose rows all exist: instruction i moves rows
+// 8 w + 2 i + lane / 32 of the tile, LDS chunk position lane % 32 <- the row's chunk at that
+// position's swizzle. kt / vt: the wave's first row (wave-uniform); koff[i] / voff[i]: the lane's
+// byte offset from it minus 1024 i, since the instruction offset (1024 i) moves the global and the
+// LDS address alike. The loads carry the non-temporal hint (the cache is streamed once per call).
+// M0 is saved and restored.
+__device__ __attribute__((always_inline)) inline void issue_rows8(const void* kt, const void* vt,
+                                                                 const unsigned (&koff)[4],
+                                                                 const unsigned (&voff)[4],
+                                                                 unsigned k_lds, unsigned v_lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %11\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %9 nt\n\t"
+      "global_load_lds_dwordx4 %2, %9 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %3, %9 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %4, %9 offset:3072 nt\n\t"
+      "s_mov_b32 m0, %12\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %5, %10 nt\n\t"
+      "global_load_lds_dwordx4 %6, %10 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %7, %10 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %8, %10 offset:3072 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(koff[0]), "v"(koff[1]), "v"(koff[2]), "v"(koff[3]), "v"(voff[0]), "v"(voff[1]),
+        "v"(voff[2]), "v"(voff[3]), "s"(kt), "s"(vt), "s"(k_lds), "s"(v_lds)
+      : "memory");
+}
+
+// Where the rows of a split lie, for the tile copies: k_at(row) / v_at(row) is the address of K /
+// V row `row`, valid for the 8-row group (aligned to 8) that holds it.
+struct LinearTiles {
+  const attn::half_t* K;
+  const attn::half_t* V;
+  __device__ const attn::half_t* k_at(unsigned row) const { return K + std::size_t{row} * attn::kDim; }
+  __device__ const attn::half_t* v_at(unsigned row) const { return V + std::size_t{row} * attn::kDim; }
+};
+// Paged rows: the pages of the split's rows, one per lane from page0 (at most 64; a page past
+// them is read from the table), read with a uniform readlane.
+struct PagedTiles {
+  PagedRows rows;
+  int tab;
+  unsigned page0;
+  __device__ std::size_t at(unsigned row) const {
+    const unsigned j = (row >> rows.log2_page) - page0;  // wave-uniform
+    const int page = j < 64 ? __builtin_amdgcn_readlane(tab, j) : rows.table[page0 + j];
+    return std::size_t(static_cast<unsigned>(page)) * rows.page_halves + rows.head_off +
+           std::size_t{row & ((1u << rows.log2_page) - 1u)} * attn::kDim;
+  }
+  __device__ const attn::half_t* k_at(unsigned row) const { return rows.k_pages + at(row); }
+  __device__ const attn::half_t* v_at(unsigned row) const { return rows.v_pages + at(row); }
+};
+
+// A wave-uniform address, in scalar registers (the copies take their base there).
+__device__ __attribute__((always_inline)) inline const attn::half_t* uniform(const attn::half_t* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return reinterpret_cast<const attn::half_t*>((uint64_t{hi} << 32) | lo);
+}
+
+// This wave's 8 rows of the tile at key k0 into the K and V slots k_lds / v_lds (this wave's 4 KiB
+// of each): rows past last_row read last_row instead (they are masked at use), so no load
+// leaves the split's rows. Always 8 vector-memory instructions.
+template <class Tiles>
+__device__ __attribute__((always_inline)) inline void issue_tile(
+    const Tiles& tl, unsigned k0, unsigned last_row, unsigned k_lds, unsigned v_lds,
+    const unsigned (&koff)[4], const unsigned (&voff)[4], unsigned wave, unsigned lane) {
+  const unsigned gs = k0 + 8 * wave;  // the group's first row (wave-uniform)
+  if (gs + 7 <= last_row) {
+    issue_rows8(uniform(tl.k_at(gs)), uniform(tl.v_at(gs)), koff, voff, k_lds, v_lds);
+  } else {
+    const unsigned row0 = gs <= last_row ? gs : last_row;
+    const unsigned lim = last_row - row0;  // rows of the group past last_row read row0 + lim
+    const attn::half_t* K = tl.k_at(row0);
+    const attn::half_t* V = tl.v_at(row0);
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i) {
+      const unsigned j = 2 * i + (lane >> 5), r = 8 * wave + j, p = lane & 31u;
+      const std::size_t at = std::size_t{j < lim ? j : lim} * attn::kDim;
+      cdna4::lds_load16_nt(K + at + 8 * tile_swz_k(r, p), k_lds + 1024 * i);
+      cdna4::lds_load16_nt(V + at + 8 * tile_swz_v(r, p), v_lds + 1024 * i);
+    }
+  }
+}
+
+// Per-lane state of a wave over its split (lane l, g = l / 16, c = l % 16, head h = c % 8).
+//   q[s]: B operand of k-step s: head h's query x log2(e)/16, dimensions 8 (4 s + g) + j, as
+//         its hi (c < 8) or lo (c >= 8) f16 half.
+//   m: the reference max of head h (log2 units, -inf before the first tile), moved lazily;
+//   mt: the true max; l: the sum of this lane's numerators (keys 4 g + i and 16 + 4 g + i of
+//   every tile, relative to m).
+//   o[b]: O^T of dimensions 64 w + 16 b + 4 g + i, column c, relative to m.
+struct TileState {
+  cdna4::half8_t q[8];
+  float m, mt, l;
+  f32x4 o[4];
+};
+
+// The K operands of one tile (both 16-key blocks, 8 k-steps): ka[kb][s] at (kaddr + 8192 kb) ^
+// 64 s, kaddr = the tile's K slot + the lane's offset.
+__device__ __attribute__((always_inline)) inline void read_k(cdna4::half8_t (&ka)[2][8],
+                                                            unsigned kaddr) {
+#pragma unroll
+  for (unsigned s = 0; s < 8; ++s)
+#pragma unroll
+    for (unsigned kb = 0; kb < 2; ++kb)
+      ka[kb][s] = lds_b128((kaddr + 8192u * kb) ^ (64u * s));
+}
+
+// The V^T operands of this wave's 4 dimension blocks (two transpose reads each: rows 4 g + r and
+// 16 + 4 g + r).
+__device__ __attribute__((always_inline)) inline void read_v(cdna4::half8_t (&va)[4],
+                                                            unsigned vslot,
+                                                            const unsigned (&vl)[4]) {
+#pragma unroll
+  for (unsigned b = 0; b < 4; ++b) {
+    const cdna4::half4_t lo = lds_tr_b64(vslot + vl[b]);
+    const cdna4::half4_t up = lds_tr_b64(vslot + vl[b] + 8192u);
+    va[b] = cdna4::half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+  }
+}
+
+// Score MFMA k-step s of both key blocks.
+__device__ __attribute__((always_inline)) inline void score_step(f32x4 (&s)[2],
+                                                                const cdna4::half8_t (&ka)[2][8],
+                                                                const cdna4::half8_t& q,
+                                                                unsigned step) {
+  if (step == 0) {
+    s[0] = mfma16(ka[0][0], q, f32x4{});
+    s[1] = mfma16(ka[1][0], q, f32x4{});
+  } else {
+    s[0] = mfma16(ka[0][step], q, s[0]);
+    s[1] = mfma16(ka[1][step], q, s[1]);
+  }
+}
+
+// The softmax update of one tile from its raw score accumulators `s`, speculating that the
+// reference max stays: joins the (hi, lo) columns (lane c and lane c ^ 8 both form hi + 2^-11 lo
+// of head c % 8), masks keys k0 + key >= lim when kMasked, forms the numerators 2^(x - m) with the
+// current m, their sum and this lane's half of each as the P^T operand. Returns whether the
+// reference max must move (the tile's head max exceeds m by more than the slack, in any lane;
+// always on the first tile, m = -inf); then the caller runs tile_rescale before using them.
+struct TileSoftmax {
+  float x[8];
+  float mx, lt;
+  cdna4::half8_t pb;
+};
+
+__device__ __attribute__((always_inline)) inline void tile_numerators(TileSoftmax& sm, float m,
+                                                                     bool is_hi) {
+  _Float16 ph[8];
+  float lt = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = __builtin_amdgcn_exp2f(sm.x[i] - m);  // 0 if masked
+    lt += p;
+    const _Float16 hi = static_cast<_Float16>(p);
+    const _Float16 lo = static_cast<_Float16>((p - static_cast<float>(hi)) * kLoScale);
+    ph[i] = is_hi ? hi : lo;
+  }
+  sm.lt = lt;
+  sm.pb = cdna4::half8_t{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+}
+
+template <bool kMasked>
+__device__ __attribute__((always_inline)) inline void tile_scores_joined(
+    TileSoftmax& sm, const f32x4 (&s)[2], unsigned k0, unsigned lim, unsigned lane) {
+  const unsigned g = lane >> 4, c = lane & 15u;
+  const bool is_hi = c < 8;
+  const float w_own = is_hi ? 1.0f : kLoWeight, w_other = is_hi ? kLoWeight : 1.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float own = s[i / 4][i % 4];
+    sm.x[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(own), w_other, own * w_own);
+  }
+  if constexpr (kMasked) {
+#pragma unroll
+    for (unsigned i = 0; i < 8; ++i) {
+      const unsigned key = k0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4));
+      sm.x[i] = key < lim ? sm.x[i] : -__builtin_inff();
+    }
+  }
+}
+
+// Head max over the tile (the lane's 8 keys, then the 4 lanes g of its column; every tile has a
+// key in the split, so it is finite), the true max, and the speculative numerators.
+__device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& sm, TileState& st,
+                                                                 unsigned lane) {
+  const float* x = sm.x;
+  float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                   fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+  mx = cdna4::max_xor32(cdna4::max_xor16(mx));
+  sm.mx = mx;
+  st.mt = fmaxf(st.mt, mx);
+  tile_numerators(sm, st.m, (lane & 15u) < 8);
+  return __builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack) != 0;
+}
+
+// The rare path: move the reference max to max(m, tile max), rescale l and O, and redo the
+// numerators.
+__device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& sm, TileState& st,
+                                                                  unsigned lane) {
+  const float mn = fmaxf(st.m, sm.mx);
+  const float corr = __builtin_amdgcn_exp2f(st.m - mn);  // 0 on the first tile (m = -inf)
+  st.m = mn;
+  st.l *= corr;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    st.o[b] *= corr;
+  tile_numerators(sm, st.m, (lane & 15u) < 8);
+}
+
+// Partial (m, l, o) of KV head kvh over keys [span.begin, span.end) (span.end <= len), written at
+// `base` (= kvh * n_splits + split, or the batched paths' index) in the reference's partial
+// layout: m in natural-log units, l and o relative to the split's true max (an empty span
+// writes m = -inf, l = 0, o = 0). Every vector-memory load of the stream is a direct LDS load
+// with an explicit wait. `more` says whether the workgroup runs another item afterwards (its LDS
+// is then reused).
+template <class Tiles>
+__device__ __attribute__((always_inline)) inline void split_partial_tiles(
+    const float* __restrict__ q, const Tiles& tl, AttnSpan span, unsigned kvh, float* part_m,
+    float* part_l, float* part_o, std::size_t base, TileShared& sh, bool more) {
+  using cdna4::half8_t;
+  const unsigned t = threadIdx.x, lane = t & 63u, g = lane >> 4, c = lane & 15u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const unsigned n_tiles = (span.end - span.begin + kTileKeys - 1) / kTileKeys;
+  const unsigned last_row = span.end - 1;  // unused when n_tiles == 0
+  const unsigned k_lds0 = cdna4::lds_offset(sh.k[0]) + 4096 * wave;
+  const unsigned v_lds0 = cdna4::lds_offset(sh.v[0]) + 4096 * wave;
+
+  // Copy offsets: instruction i moves tile row r = 8 w + 2 i + lane / 32 (row j = r - 8 w of the
+  // wave's group), LDS chunk position lane % 32.
+  unsigned koff[4], voff[4];
+#pragma unroll
+  for (unsigned i = 0; i < 4; ++i) {
+    const unsigned j = 2 * i + (lane >> 5), r = 8 * wave + j, p = lane & 31u;
+    koff[i] = j * 512 + 16 * tile_swz_k(r, p) - 1024 * i;
+    voff[i] = j * 512 + 16 * tile_swz_v(r, p) - 1024 * i;
+  }
+  auto issue = [&](unsigned ti) __attribute__((always_inline)) {
+    const unsigned stage = ti % kTileStages;
+    issue_tile(tl, span.begin + ti * kTileKeys, last_row, k_lds0 + stage * kTileBytes,
+               v_lds0 + stage * kTileBytes, koff, voff, wave, lane);
+  };
+
+  // The KV head's 8 query rows (wave w: rows 2 w, 2 w + 1), then the first three tiles.
+#pragma unroll
+  for (unsigned i = 0; i < 2; ++i) {
+    const unsigned h = 2 * wave + i;
+    cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
+                      cdna4::lds_offset(sh.q[h]));
+  }
+#pragma unroll
+  for (unsigned ti = 0; ti < kTileStages - 1; ++ti)
+    if (ti < n_tiles)
+      issue(ti);
+
+  // Operand offsets. K: row 16 kb + c, chunk 4 s + g at position (4 s + g) ^ c, i.e. byte
+  // 512 c + 16 (g ^ c % 4) + 64 (s ^ c / 4) = kl ^ 64 s (+ 8192 kb; the slot base has no bits
+  // below 14). V^T: lane 16 g + 4 r + e reads row 4 g + r, dimensions 16 blk + 4 e .. + 3 (blk =
+  // 4 w + b): chunk 2 blk + e / 2 at position 2 (blk ^ row % 8) + e / 2.
+  const unsigned kl = 512 * c + 16 * (g ^ (c & 3u)) + 64 * (c >> 2);
+  unsigned vl[4];
+  {
+    const unsigned r = (lane >> 2) & 3u, e = lane & 3u, row = 4 * g + r;
+#pragma unroll
+    for (unsigned b = 0; b < 4; ++b)
+      vl[b] = 512 * row + 32 * ((4 * wave + b) ^ (row & 7u)) + 8 * e;
+  }
+  auto kslot = [&](unsigned ti) __attribute__((always_inline)) {
+    return cdna4::lds_offset(sh.k[ti % kTileStages]) + kl;
+  };
+  auto vslot = [&](unsigned ti) __attribute__((always_inline)) {
+    return cdna4::lds_offset(sh.v[ti % kTileStages]);
+  };
+
+  TileState st;
+  st.m = -__builtin_inff();
+  st.mt = -__builtin_inff();
+  st.l = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    st.o[b] = f32x4{};
+  f32x4 s_cur[2] = {f32x4{}, f32x4{}};
+
+  if (n_tiles > 0) {
+    wait_tiles_after(n_tiles - 1 < 2 ? n_tiles - 1 : 2);  // tile 0 and the queries landed
+    tile_barrier();
+    // Query pairs: head c % 8, dimensions 8 (4 s + g) .. + 7, x log2(e)/16 (1/sqrt(256) in
+    // log2 units), hi half in columns 0-7, lo half in columns 8-15.
+    const float* qrow = sh.q[c & 7u];
+    constexpr float kScale = kLog2e / 16.0f;
+#pragma unroll
+    for (unsigned s = 0; s < 8; ++s) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s + g));
+      const float4 x1 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s + g) + 4);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      _Float16 hv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = xs[j] * kScale;
+        const _Float16 hi = static_cast<_Float16>(v);
+        const _Float16 lo = static_cast<_Float16>((v - static_cast<float>(hi)) * kLoScale);
+        hv[j] = c < 8 ? hi : lo;
+      }
+      st.q[s] = half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
+    }
+    half8_t ka[2][8];
+    read_k(ka, kslot(0));
+#pragma unroll
+    for (unsigned s = 0; s < 8; ++s)
+      score_step(s_cur, ka, st.q[s], s);
+  }
+
+  // Iteration ti: tile ti + 1 lands (this wave's copy by vmcnt, every wave's by the barrier, which
+  // also says that every wave is done with tile ti - 1, whose stage then receives tile ti + 3).
+  // The 16 score MFMAs of tile ti + 1 (of tile ti again on the last iteration, discarded) go to
+  // the matrix cores interleaved with the VALU softmax of tile ti, whose scores the previous
+  // iteration produced; then O += V^T P^T of tile ti.
+  for (unsigned ti = 0; ti < n_tiles; ++ti) {
+    const bool next = ti + 1 < n_tiles;  // uniform
+    if (next) {
+      const unsigned ahead = n_tiles - 2 - ti;  // copies issued after tile ti + 1's
+      wait_tiles_after(ahead < 1 ? ahead : 1);
+      tile_barrier();
+      if (ti + kTileStages - 1 < n_tiles)
+        issue(ti + kTileStages - 1);  // into tile ti - 1's stage
+    }
+    const unsigned k0 = span.begin + ti * kTileKeys;
+    TileSoftmax sm;
+    if (k0 + kTileKeys > span.end)  // uniform: only the last tile
+      tile_scores_joined<true>(sm, s_cur, k0, span.end, lane);
+    else
+      tile_scores_joined<false>(sm, s_cur, k0, span.end, lane);
+    half8_t ka[2][8], va[4];
+    read_k(ka, kslot(next ? ti + 1 : ti));
+    read_v(va, vslot(ti), vl);
+    __builtin_amdgcn_sched_barrier(0);  // every operand read in flight before the MFMAs
+    f32x4 s_next[2];
+#pragma unroll
+    for (unsigned s = 0; s < 8; ++s)
+      score_step(s_next, ka, st.q[s], s);
+    const bool moved = tile_decide(sm, st, lane);
+    // The speculative numerators are computed here, between the MFMAs, not sunk past the branch.
+    asm volatile("" : "+v"(sm.lt), "+v"(sm.pb));
+    // 16 MFMAs, each followed by up to 6 VALU instructions of the softmax.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    if (moved)
+      tile_rescale(sm, st, lane);
+    st.l += sm.lt;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
+    s_cur[0] = s_next[0];
+    s_cur[1] = s_next[1];
+  }
+
+  // Relative to the true max; l summed over the lanes g of the column; the (hi, lo) columns of
+  // O joined in the lanes c < 8, which store this wave's 64 dimensions of head c.
+  const bool empty = n_tiles == 0;
+  const float f = empty ? 1.0f : __builtin_amdgcn_exp2f(st.m - st.mt);
+  const float L = cdna4::sum_xor32(cdna4::sum_xor16(st.l)) * f;
+  const unsigned h = c & 7u;
+#pragma unroll
+  for (unsigned b = 0; b < 4; ++b) {
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = st.o[b][i] * f;
+      o[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
+    }
+    if (c < 8) {
+      float4* dst = reinterpret_cast<float4*>(part_o + (base * kGroup + h) * attn::kDim +
+                                              64 * wave + 16 * b + 4 * g);
+      *dst = float4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  if (wave == 0 && lane < 8) {
+    part_m[base * kGroup + h] = st.mt * kLn2;  // -inf stays -inf for an empty span
+    part_l[base * kGroup + h] = L;
+  }
+  if (more)
+    tile_barrier();  // LDS is reused by the next item
+}
+
+// PagedTiles of a split: the pages of its rows [span.begin, span.end), one per lane (at most 64
+// pages; further ones are read from the table at use). The page-table slice is waited for here,
+// before any tile copy is in flight.
+__device__ __attribute__((always_inline)) inline PagedTiles paged_tiles(const PagedRows& rows,
+                                                                        AttnSpan span) {
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned page0 = span.begin >> rows.log2_page;
+  const unsigned npages =
+      span.end > span.begin ? ((span.end - 1) >> rows.log2_page) - page0 + 1 : 0;
+  int tab = lane < npages ? rows.table[page0 + lane] : 0;
+  asm volatile("" : "+v"(tab));  // the load completes before the copies are issued
+  return PagedTiles{rows, tab, page0};
+}
+
 }  // namespace decode_detail
 
 namespace decode_detail {
@@ -787,22 +1281,52 @@ __device__ __attribute__((always_inline)) inline void split_items(const AttnSpli
 
 }  // namespace decode_detail
 
-// Split-K flash decoding on wave64 VALU (no MFMA), in the reference's arithmetic: f32 query, f32
-// scores and numerators, f32 accumulation over f16 K/V (kernels/attention_decode.hpp:150-221).
-// Each split's keys are streamed in 8-row units through per-wave LDS rings (direct global -> LDS
-// loads, 1 KiB coalesced per wave instruction); scores are v_fma_mix_f32 products of the lane's
-// f32 query slice and f16 K, summed by a DPP/crossbar reduce-scatter; the online softmax runs in
-// log2 units; P V is v_fma_mix_f32 of f32 numerators and f16 V. Output: the reference's partial
-// layout, m in natural-log units.
+namespace decode_detail {
+
+// Items [first, first + count) of a split launch on the matrix cores (split_partial_tiles).
+__device__ __attribute__((always_inline)) inline void split_items_mfma(const AttnSplitParams& p,
+                                                                       unsigned first,
+                                                                       unsigned count) {
+  __shared__ TileShared sh;
+  for (unsigned item = first + blockIdx.y * gridDim.x + blockIdx.x; item < first + count;
+       item += gridDim.x * gridDim.y) {
+    const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
+    const std::size_t head = std::size_t{kvh} * p.max_ctx * attn::kDim;
+    split_partial_tiles(p.q, LinearTiles{p.k_cache + head, p.v_cache + head},
+                        attn_split_span(p.len, p.n_splits, split), kvh, p.part_m, p.part_l,
+                        p.part_o, std::size_t{kvh} * p.n_splits + split, sh,
+                        item + gridDim.x * gridDim.y < first + count);
+  }
+}
+
+}  // namespace decode_detail
+
+// Split-K flash decoding in the reference's precision (kernels/attention_decode.hpp:150-221: f32
+// query, f32 scores and numerators, f32 accumulation over f16 K/V) on the matrix cores: each
+// f32 operand is an exact f16 (hi, lo) pair, and the 8 heads x (hi, lo) fill the 16 columns of
+// v_mfma_f32_16x16x32_f16 (split_partial_tiles). The KV cache streams through a 4-stage LDS ring
+// of 32-key tiles; the max/sum reductions are DPP and lane-crossbar moves. Output: the
+// reference's partial layout, m in natural-log units.
 template <int kBlock>
 __device__ void attn_split_op(const AttnSplitParams& p, unsigned first, unsigned count) {
   static_assert(kBlock == 256, "four waves per split workgroup");
-  decode_detail::split_items<decode_detail::DecodeArith::kF32>(p, first, count);
+  decode_detail::split_items_mfma(p, first, count);
 }
 
 template <int kBlock>
-__global__ void __launch_bounds__(kBlock) attn_split_kernel(AttnSplitParams p) {
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_split_kernel(AttnSplitParams p) {
   attn_split_op<kBlock>(p, 0, attn::kKvHeads * p.n_splits);
+}
+
+// The same split and arithmetic on wave64 VALU (no reference counterpart; same launch shape and
+// partial layout). Each split's keys are streamed in 8-row units through per-wave LDS rings;
+// scores are v_fma_mix_f32 products of the lane's f32 query slice and f16 K, summed by a
+// DPP/crossbar reduce-scatter; P V is v_fma_mix_f32 of f32 numerators and f16 V: 512 products per
+// key and head, one per instruction, which on MI355X is most of the HBM time of the same bytes.
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_split_valu_kernel(AttnSplitParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  decode_detail::split_items<decode_detail::DecodeArith::kF32>(p, 0, attn::kKvHeads * p.n_splits);
 }
 
 // The same split with an f16 query and f16 numerators through v_dot2_f32_f16 (two products per
@@ -1006,9 +1530,9 @@ __host__ __device__ inline unsigned attn_ragged_seq_splits(unsigned len, unsigne
 
 // One workgroup per (sequence, KV head, split slot); slots past the sequence's split count exit.
 template <int kBlock>
-__global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedParams p) {
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_ragged_split_kernel(AttnRaggedParams p) {
   static_assert(kBlock == 256, "four waves per split workgroup");
-  __shared__ decode_detail::SplitShared sh;
+  __shared__ decode_detail::TileShared sh;
   const unsigned item = blockIdx.x;
   const unsigned split = item % p.s_max, kvh = (item / p.s_max) % attn::kKvHeads;
   const unsigned seq = item / (p.s_max * attn::kKvHeads);
@@ -1019,9 +1543,10 @@ __global__ void __launch_bounds__(kBlock) attn_ragged_split_kernel(AttnRaggedPar
   if (split >= n_splits)
     return;
   const std::size_t kv0 = p.kv_offsets[seq] + std::size_t{kvh} * len * attn::kDim;
-  decode_detail::split_partial<decode_detail::DecodeArith::kF32>(
-      p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, p.k_cache + kv0, p.v_cache + kv0, len,
-      attn_split_span(len, n_splits, split), kAttnSubChunk, kvh, p.part_m, p.part_l, p.part_o,
+  decode_detail::split_partial_tiles(
+      p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
+      decode_detail::LinearTiles{p.k_cache + kv0, p.v_cache + kv0},
+      attn_split_span(len, n_splits, split), kvh, p.part_m, p.part_l, p.part_o,
       (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
 }
 
@@ -1080,9 +1605,9 @@ __host__ __device__ inline unsigned attn_paged_len_cap(unsigned max_pages, unsig
 
 // One workgroup per (sequence, KV head, split slot), as attn_ragged_split_kernel.
 template <int kBlock>
-__global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParams p) {
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_paged_split_kernel(AttnPagedParams p) {
   static_assert(kBlock == 256, "four waves per split workgroup");
-  __shared__ decode_detail::SplitShared sh;
+  __shared__ decode_detail::TileShared sh;
   const unsigned item = blockIdx.x;
   const unsigned split = item % p.s_max, kvh = (item / p.s_max) % attn::kKvHeads;
   const unsigned seq = item / (p.s_max * attn::kKvHeads);
@@ -1097,10 +1622,12 @@ __global__ void __launch_bounds__(kBlock) attn_paged_split_kernel(AttnPagedParam
       p.k_pages, p.v_pages, p.page_table + std::size_t{seq} * p.max_pages, p.log2_page,
       std::size_t{2} * attn::kDim << p.log2_page,
       std::size_t{kvh} * attn::kDim << p.log2_page};
-  decode_detail::split_partial_rows<decode_detail::DecodeArith::kF32>(
-      p.q + std::size_t{seq} * attn::kQHeads * attn::kDim, rows, len,
-      attn_split_span(len, n_splits, split), kAttnSubChunk, kvh, p.part_m, p.part_l, p.part_o,
-      (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
+  const AttnSpan span = attn_split_span(len, n_splits, split);
+  decode_detail::split_partial_tiles(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
+                                     decode_detail::paged_tiles(rows, span), span, kvh, p.part_m,
+                                     p.part_l, p.part_o,
+                                     (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
+                                     sh, false);
 }
 
 }  // namespace miso::kernels
