@@ -30,9 +30,12 @@ Also reported:
                 shapes (us, GB/s of weights).
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
 
-Launches are recorded once into HIP graphs and replayed in the timed regions, so the host's
-per-launch cost does not throttle a ~10 us step; the kernels are the same ones the C ABI
-launches eagerly.
+Decode steps are timed the way the reference's own bench times them (bench/attention/
+bench_attention.hip:24-33): back-to-back eager calls of the C ABI on one stream between two HIP
+events, from a native loop (miso_amd/lib/libmiso_bench.so), since a Python caller's per-call cost
+is of the order of a step. The same calls recorded into a HIP graph and replayed are reported
+beside them (`graph_*`): on this ROCm each graph kernel node costs ~1-2.5 us more than an eager
+launch. Without the native loop the graph figures are the measurement.
 
     python bench.py [--gpus 1] [--steps 60] [--warmup 12]
 """
@@ -181,6 +184,36 @@ def decode_caches(torch, args):
     return q, qg, caches
 
 
+def eager_loop():
+    """The native eager timing loop (libmiso_bench.so), or None if it is not built."""
+    import ctypes
+    path = ROOT / "miso_amd" / "lib" / "libmiso_bench.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    vp, u32, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int
+    lib.miso_bench_decode.restype = ctypes.c_double
+    lib.miso_bench_decode.argtypes = [i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i32,
+                                      vp, vp, vp, vp, u32, u32, u32, i32, i32, vp]
+    return lib
+
+
+def eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits, warmup, iters):
+    """ms per call of `iters` eager calls (mode: 0 decode, 1 split, 2 combine, 3 decode f16q)."""
+    import ctypes
+    R = len(caches)
+    ks = (ctypes.c_void_p * R)(*[k.data_ptr() for k, _ in caches])
+    vs = (ctypes.c_void_p * R)(*[v.data_ptr() for _, v in caches])
+    torch.cuda.synchronize()
+    ms = lib.miso_bench_decode(mode, q.data_ptr(), qg.data_ptr(), ks, vs, R, core.data_ptr(),
+                               sc.part_m.data_ptr(), sc.part_l.data_ptr(), sc.part_o.data_ptr(),
+                               L, L, n_splits, warmup, iters,
+                               torch.cuda.current_stream().cuda_stream)
+    if ms < 0:
+        raise RuntimeError(f"eager timing loop failed ({ms})")
+    return ms
+
+
 def bench_decode(torch, A, args, inputs, max_splits, f16_query=False, label="C2"):
     """One decode call per step over rotated caches: step (split + combine), split alone and
     combine alone, each as a graph of `buffers` calls replayed; per-call times in ms. Returns
@@ -218,17 +251,32 @@ def bench_decode(torch, A, args, inputs, max_splits, f16_query=False, label="C2"
     ms_step, wall_step = time_replays(torch, g_step, reps)
     ms_split, _ = time_replays(torch, g_split, reps)
     ms_comb, _ = time_replays(torch, g_comb, reps)
-    t_step = ms_step / steps
-    t_split = ms_split / steps
-    t_comb = ms_comb / steps
+    g_step_t = ms_step / steps
+    g_split_t = ms_split / steps
+    g_comb_t = ms_comb / steps
     if f16_query:
-        t_split -= t_comb  # the f16q graph above times split + combine
-    log(f"decode {label}: step {t_step * 1e3:.2f} us (wall {wall_step / steps * 1e3:.2f} us), "
-        f"split {t_split * 1e3:.2f} us, combine {t_comb * 1e3:.2f} us, n_splits {n_splits}")
+        g_split_t -= g_comb_t  # the f16q graph above times split + combine
+    log(f"decode {label} (graph): step {g_step_t * 1e3:.2f} us (wall "
+        f"{wall_step / steps * 1e3:.2f} us), split {g_split_t * 1e3:.2f} us, combine "
+        f"{g_comb_t * 1e3:.2f} us, n_splits {n_splits}")
+    timing = "graph"
+    t_step, t_split, t_comb = g_step_t, g_split_t, g_comb_t
+    lib = eager_loop()
+    if lib is not None:
+        timing = "eager"
+        ev = lambda mode: eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits,
+                                       args.warmup, steps)
+        t_step = ev(3 if f16_query else 0)
+        t_comb = ev(2)
+        t_split = ev(1) if not f16_query else t_step - t_comb
+        log(f"decode {label} (eager): step {t_step * 1e3:.2f} us, split {t_split * 1e3:.2f} us, "
+            f"combine {t_comb * 1e3:.2f} us")
     step(0)
     torch.cuda.synchronize()
     return {
         "steps": steps, "t_step_ms": t_step, "t_split_ms": t_split, "t_comb_ms": t_comb,
+        "graph_ms": {"step": g_step_t, "split": g_split_t, "combine": g_comb_t},
+        "timing": timing,
         "kv_bytes": kv_bytes, "n_splits": n_splits, "L": L, "core0": core.cpu().numpy(),
     }
 
@@ -238,6 +286,8 @@ def decode_line(dec, workload):
     return {"workload": workload, "us_per_step": round(dec["t_step_ms"] * 1e3, 3),
             "split_us": round(dec["t_split_ms"] * 1e3, 3),
             "combine_us": round(dec["t_comb_ms"] * 1e3, 3), "n_splits": dec["n_splits"],
+            "timing": dec["timing"],
+            "graph_us_per_step": round(dec["graph_ms"]["step"] * 1e3, 3),
             "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
@@ -610,6 +660,21 @@ def main():
         other["C2_f16q"] = decode_line(
             d16, "C2 with an f16 query and f16 numerators (v_dot2_f32_f16; miso_attn_decode_f16q):"
                  " half the VALU work, per-head rel-L2 ~3e-4 -- not the reference's arithmetic")
+        lib = eager_loop()
+        if lib is not None:
+            q, qg, caches = inputs
+            sc = A.DecodeScratch(args.max_splits)
+            core = torch.empty(H * D, device="cuda")
+            t_valu = eager_decode(torch, lib, 4, q, qg, caches, core, sc, args.ctx,
+                                  dec["n_splits"], args.warmup, dec["steps"])
+            log(f"decode C2 split on VALU (eager): {t_valu * 1e3:.2f} us")
+            other["C2_split_valu"] = {
+                "workload": "the C2 split alone computed on wave64 VALU (v_fma_mix_f32, one f32 "
+                            "product per instruction; miso_attn_split_valu) instead of the matrix "
+                            "cores, same precision and partials: the measured alternative",
+                "split_us": round(t_valu * 1e3, 3),
+                "mfma_split_us": round(dec["t_split_ms"] * 1e3, 3),
+                "gbs": round(dec["kv_bytes"] / (t_valu * 1e-3) / 1e9, 1)}
         d60 = bench_decode(torch, A, args, inputs, 60, label="C2 engine cap 60")
         other["C2_engine_cap60"] = decode_line(
             d60, "C2 at the engine's shipped partial capacity kMaxSplits = 60 "
@@ -644,9 +709,14 @@ def main():
                         "head_dim 256, f16 KV [2][32768][256], split-K + LSE merge x sigmoid gate",
             "ctx": dec["L"], "n_splits": dec["n_splits"], "kv_buffers_rotated": args.buffers,
             "step": "split kernel + combine kernel (one decode call)",
-            "arithmetic": "f32 query, scores, softmax numerators and accumulation over the f16 "
-                          "KV cache (the reference's, kernels/attention_decode.hpp:150-221); "
-                          "storage f16",
+            "timing": dec["timing"] + (" (native loop of eager C ABI calls between two HIP "
+                                       "events, as bench/attention/bench_attention.hip)"
+                                       if dec["timing"] == "eager" else " (HIP graph replays)"),
+            "graph_us_per_step": round(dec["graph_ms"]["step"] * 1e3, 3),
+            "arithmetic": "the reference's precision (kernels/attention_decode.hpp:150-221): f32 "
+                          "query and softmax numerators, each carried as an exact f16 (hi, lo) "
+                          "pair into v_mfma_f32_16x16x32_f16 against the f16 KV cache, f32 "
+                          "scores and accumulation; storage f16",
             "algorithmic_bytes_per_step": dec["kv_bytes"],
         },
         "roofline": {

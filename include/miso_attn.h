@@ -69,12 +69,20 @@ int miso_attn_prep_batch(const float* qg, const float* k, const float* v, const 
 /* Split-K partials: replaces attn_split_kernel<256><<<dim3(n_splits, 2), 256, 0, stream>>>(
  * AttnSplitParams{...}), src/engine/attention.hip:103-106 and tests/test_attn_splitk.hip:125-134
  * (kernels/attention_decode.hpp:117-236). Writes part_m/part_l [2][n_splits][8] and part_o
- * [2][n_splits][8][256] for keys [0, len), in the reference's arithmetic (f32 query, scores,
- * numerators and accumulation over the f16 cache). Rejects len == 0, len > max_ctx,
- * n_splits == 0. */
+ * [2][n_splits][8][256] for keys [0, len), at the reference's precision (f32 query, scores,
+ * numerators and accumulation over the f16 cache), on the matrix cores: each f32 operand as an
+ * exact f16 (hi, lo) pair. Rejects len == 0, len > max_ctx, n_splits == 0. */
 int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     float* part_m, float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                     uint32_t n_splits, void* stream);
+
+/* The same split and partials computed on wave64 VALU instead (attn_split_valu_kernel<256>,
+ * v_fma_mix_f32: one f32 product per instruction). No reference counterpart: the measured
+ * alternative to the matrix-core split, kept for comparison. Same arguments and rejections as
+ * miso_attn_split. */
+int miso_attn_split_valu(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         float* part_m, float* part_l, float* part_o, uint32_t len,
+                         uint32_t max_ctx, uint32_t n_splits, void* stream);
 
 /* LSE merge x sigmoid gate: replaces attn_combine_kernel<64, true, 4><<<64, 64, 0, stream>>>(
  * AttnCombineParams{...}), src/engine/attention.hip:107-109 (kernels/attention_decode.hpp:

@@ -22,6 +22,7 @@ SIGNATURES = {
     "miso_attn_prep_batch": (c_int, [P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_float,
                                      c_uint32, c_uint32, P]),
     "miso_attn_split": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
+    "miso_attn_split_valu": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_combine": (c_int, [P, P, P, P, P, c_uint32, P]),
     "miso_attn_combine_variant": (c_int, [c_int, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                           c_uint32, P]),

@@ -93,7 +93,8 @@ def attn_prep_batch(qg, k, v, q_norm, k_norm, inv_freq, k_cache, v_cache, q, pos
 
 
 def attn_split(q, k_cache, v_cache, part_m, part_l, part_o, length: int, max_ctx: int,
-               n_splits: int, stream=None) -> None:
+               n_splits: int, stream=None, valu: bool = False) -> None:
+    """Split-K partials (miso_attn_split; with valu, the VALU form miso_attn_split_valu)."""
     f32 = torch.float32
     _need(q, "q", f32, Q_HEADS * DIM)
     _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
@@ -101,7 +102,9 @@ def attn_split(q, k_cache, v_cache, part_m, part_l, part_o, length: int, max_ctx
     _need(part_m, "part_m", f32, KV_HEADS * n_splits * GROUP)
     _need(part_l, "part_l", f32, KV_HEADS * n_splits * GROUP)
     _need(part_o, "part_o", f32, KV_HEADS * n_splits * GROUP * DIM)
-    _lib.check(_lib.load().miso_attn_split(
+    lib = _lib.load()
+    fn = lib.miso_attn_split_valu if valu else lib.miso_attn_split
+    _lib.check(fn(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(part_m), _ptr(part_l), _ptr(part_o), length,
         max_ctx, n_splits, _stream(stream)))
 

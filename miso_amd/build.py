@@ -19,6 +19,9 @@ ROOT = PKG.parent
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libmiso_attn.so"
 SOURCES = [PKG / "csrc" / "miso_attn_capi.hip"]
+# bench.py's eager timing loops (host code over the C ABI above); not part of the product.
+BENCH_LIB = LIB_DIR / "libmiso_bench.so"
+BENCH_SOURCES = [PKG / "csrc" / "miso_bench.cpp"]
 HEADERS = sorted((PKG / "kernels").glob("*.hpp")) + [ROOT / "include" / "miso_attn.h"]
 
 # Packed FP32 VALU forms are disabled for all device code built here.
@@ -43,16 +46,18 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile libmiso_attn.so for gfx950 (always recompiles)."""
+    """Compile libmiso_attn.so for gfx950, then libmiso_bench.so over it (always recompiles)."""
     _compile(SOURCES, LIB, verbose)
+    _compile(BENCH_SOURCES, BENCH_LIB, verbose,
+             ["-L", str(LIB_DIR), "-lmiso_attn", "-Wl,-rpath,$ORIGIN"])
     return LIB
 
 
-def _compile(sources, lib: Path, verbose: bool) -> None:
+def _compile(sources, lib: Path, verbose: bool, extra=()) -> None:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), *HIP_FLAGS, "-I", str(PKG / "kernels"), "-I", str(ROOT / "include"),
-           *map(str, sources), "-o", str(tmp)]
+           *map(str, sources), *extra, "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

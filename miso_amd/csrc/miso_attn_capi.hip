@@ -176,6 +176,24 @@ int miso_attn_split(const float* q, const uint16_t* k_cache, const uint16_t* v_c
   return launched("miso_attn_split");
 }
 
+int miso_attn_split_valu(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         float* part_m, float* part_l, float* part_o, uint32_t len,
+                         uint32_t max_ctx, uint32_t n_splits, void* stream) {
+  constexpr const char* fn = "miso_attn_split_valu";
+  if (any_bad(q, k_cache, v_cache, part_o) || bad_scalars(part_m) || bad_scalars(part_l))
+    return fail(fn, kBadPtr);
+  if (len == 0)
+    return fail(fn, "len must be >= 1");
+  if (len > max_ctx)
+    return fail(fn, "len exceeds max_ctx");
+  if (n_splits == 0)
+    return fail(fn, "n_splits must be >= 1");
+  const k::AttnSplitParams p{q,      as_half(k_cache), as_half(v_cache), part_m, part_l,
+                             part_o, len,              max_ctx,          n_splits};
+  k::attn_split_valu_kernel<256><<<dim3(n_splits, 2), 256, 0, as_stream(stream)>>>(p);
+  return launched(fn);
+}
+
 int miso_attn_combine(const float* part_m, const float* part_l, const float* part_o,
                       const float* qg, float* core, uint32_t n_splits, void* stream) {
   if (any_bad(part_o, qg, core) || bad_scalars(part_m) || bad_scalars(part_l))

@@ -68,6 +68,26 @@ def test_decode_baseline_configs(O, attn, torch_mod, length):
           name="baseline")
 
 
+@pytest.mark.parametrize("length,n_splits", [(1, 1), (33, 2), (1000, 31), (32768, 128)])
+def test_valu_split_matches_oracle(O, attn, torch_mod, length, n_splits):
+    """miso_attn_split_valu (the split on VALU, kept as the measured alternative to the
+    matrix-core split): combined by miso_attn_combine, held to the same gates as the f32 path."""
+    torch = torch_mod
+    d = O.decode_inputs(length, length, length, q_scale=1.0)
+    q, qg = to_dev(torch, d["q"]), to_dev(torch, d["qg"])
+    k, v = to_dev(torch, d["k"]), to_dev(torch, d["v"])
+    sc = attn.DecodeScratch(n_splits)
+    core = torch.full((H * D,), CANARY, dtype=torch.float32, device="cuda")
+    attn.attn_split(q, k, v, sc.part_m, sc.part_l, sc.part_o, length, length, n_splits, valu=True)
+    attn.attn_combine(sc.part_m, sc.part_l, sc.part_o, qg, core, n_splits)
+    torch.cuda.synchronize()
+    got = to_host(core).reshape(H, D)
+    ref = O.decode_f64(d["q"], d["qg"], d["k"], d["v"], length, length)
+    st = O.compare(got, ref)
+    report(f"valu split len={length} splits={n_splits}", st)
+    assert st["ok"] and st["rel_l2_head"] <= REF_REL_L2, st
+
+
 @pytest.mark.parametrize("length", [1, 33, 1000, 32768])
 def test_decode_f16_query_variant(O, attn, torch_mod, length):
     """miso_attn_decode_f16q (f16 query and numerators): the north star's elementwise tolerance,
