@@ -1165,28 +1165,37 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
       score_step(s_cur, ka, st.q[s], s);
   }
 
-  // Iteration ti: tile ti + 1 lands (this wave's copy by vmcnt, every wave's by the barrier, which
-  // also says that every wave is done with tile ti - 1, whose stage then receives tile ti + 3).
-  // The 16 score MFMAs of tile ti + 1 (of tile ti again on the last iteration, discarded) go to
-  // the matrix cores interleaved with the VALU softmax of tile ti, whose scores the previous
-  // iteration produced; then O += V^T P^T of tile ti.
-  for (unsigned ti = 0; ti < n_tiles; ++ti) {
-    const bool next = ti + 1 < n_tiles;  // uniform
-    if (next) {
-      const unsigned ahead = n_tiles - 2 - ti;  // copies issued after tile ti + 1's
-      wait_tiles_after(ahead < 1 ? ahead : 1);
-      tile_barrier();
-      if (ti + kTileStages - 1 < n_tiles)
-        issue(ti + kTileStages - 1);  // into tile ti - 1's stage
-    }
+  // Iteration ti < n_tiles - 1: tile ti + 1 lands (this wave's copy by vmcnt, every wave's by the
+  // barrier, which also says that every wave is done with tile ti - 1, whose stage then receives
+  // tile ti + 3). The 16 score MFMAs of tile ti + 1 go to the matrix cores interleaved with the
+  // VALU softmax of tile ti, whose scores the previous iteration produced; then O += V^T P^T of
+  // tile ti. The last tile has no successor: its softmax and P V alone.
+  auto softmax_pv = [&](const half8_t (&va)[4], TileSoftmax& sm, bool moved)
+      __attribute__((always_inline)) {
+    if (moved)
+      tile_rescale(sm, st, lane);
+    st.l += sm.lt;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
+  };
+  auto join = [&](unsigned ti, TileSoftmax& sm) __attribute__((always_inline)) {
     const unsigned k0 = span.begin + ti * kTileKeys;
-    TileSoftmax sm;
     if (k0 + kTileKeys > span.end)  // uniform: only the last tile
       tile_scores_joined<true>(sm, s_cur, k0, span.end, lane);
     else
       tile_scores_joined<false>(sm, s_cur, k0, span.end, lane);
+  };
+  for (unsigned ti = 0; ti + 1 < n_tiles; ++ti) {
+    const unsigned ahead = n_tiles - 2 - ti;  // copies issued after tile ti + 1's
+    wait_tiles_after(ahead < 1 ? ahead : 1);
+    tile_barrier();
+    if (ti + kTileStages - 1 < n_tiles)
+      issue(ti + kTileStages - 1);  // into tile ti - 1's stage
+    TileSoftmax sm;
+    join(ti, sm);
     half8_t ka[2][8], va[4];
-    read_k(ka, kslot(next ? ti + 1 : ti));
+    read_k(ka, kslot(ti + 1));
     read_v(va, vslot(ti), vl);
     __builtin_amdgcn_sched_barrier(0);  // every operand read in flight before the MFMAs
     f32x4 s_next[2];
@@ -1202,14 +1211,18 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
-    if (moved)
-      tile_rescale(sm, st, lane);
-    st.l += sm.lt;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
+    softmax_pv(va, sm, moved);
     s_cur[0] = s_next[0];
     s_cur[1] = s_next[1];
+  }
+  if (n_tiles > 0) {
+    const unsigned ti = n_tiles - 1;
+    TileSoftmax sm;
+    join(ti, sm);
+    half8_t va[4];
+    read_v(va, vslot(ti), vl);
+    const bool moved = tile_decide(sm, st, lane);
+    softmax_pv(va, sm, moved);
   }
 
   // Relative to the true max; l summed over the lanes g of the column; the (hi, lo) columns of
