@@ -26,6 +26,7 @@ Also reported:
                 TFLOP/s), C5 (ragged decode, 64 sequences: GB/s of K/V), as in the survey's table,
                 and C5 over a pool of 16-row KV pages (the paged entry point); C2 over an fp8
                 (e4m3 rows) KV cache: us per decode step and GB/s of codes + row scales.
+                F4_qgemm: the prefill projection GEMMs at a 4096-token chunk (TFLOP/s).
                 F4_q4k_gemv / F4_q6k_gemv: the Q4_K and Q6_K GEMVs at the attention's projection
                 shapes (us, GB/s of weights).
   device        clock / temperature / power readings (rocm-smi or amd-smi) right after the runs.
@@ -521,6 +522,30 @@ def bench_other(torch, A, args):
                           "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p),
                           "attn_q_k_v_one_launch": line(w4b + w6b + 512 * 2048 // 256 * 144, tq,
                                                         copies_p)}
+    # Prefill projection GEMMs (row f4, kernels/qgemm.hpp) at a 4096-token chunk (the layer's
+    # retuned prefill chunk): TFLOP/s of 2 n_tok n k over the dequantized product.
+    n_tok = 4096
+    gemm = {}
+    for name, fmt, k, n in (("attn_q", "q4_k", 2048, 8192), ("attn_k", "q4_k", 2048, 512),
+                            ("attn_v", "q6_k", 2048, 512), ("attn_output", "q4_k", 4096, 2048)):
+        xa = torch.randn(n_tok * k, generator=gen, device="cuda")
+        inp = A.GemmInput(n_tok, k)
+        A.gemm_input(xa, k, n_tok, inp)
+        wg = (synthetic_q4k(torch, gen, 1, n, k) if fmt == "q4_k"
+              else synthetic_q6k(torch, gen, 1, n, k))[0]
+        ya = torch.empty(n_tok * n, device="cuda")
+        tg = timed(lambda i: A.gemm(wg, fmt, n, k, inp, ya, n), 4)
+        ta = timed(lambda i: A.gemm_input(xa, k, n_tok, inp), 4)
+        fl = 2.0 * n_tok * n * k
+        gemm[name] = {"format": fmt, "k": k, "n_rows": n, "us_per_call": round(tg * 1e3, 2),
+                      "tflops": round(fl / (tg * 1e-3) / 1e12, 1),
+                      "frac": round(fl / (tg * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                      "gemm_input_us": round(ta * 1e3, 2)}
+        del xa, inp, wg, ya
+    out["F4_qgemm"] = {"workload": f"prefill projection GEMMs over Q4_K / Q6_K r1 weights, "
+                                   f"{n_tok} tokens, f16 activations (gemm_input) and f16 MFMA "
+                                   f"with f32 accumulation; TFLOP/s of 2 n_tok n k",
+                       "tokens": n_tok, **gemm}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
@@ -528,7 +553,9 @@ def bench_other(torch, A, args):
                     for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
         + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "
         f"{out['F4_q6k_gemv']['attn_q_plus_attn_v_pair']['us_per_call']} us, q+k+v "
-        f"{out['F4_q6k_gemv']['attn_q_k_v_one_launch']['us_per_call']} us")
+        f"{out['F4_q6k_gemv']['attn_q_k_v_one_launch']['us_per_call']} us, qgemm "
+        + ", ".join(f"{k_} {v['tflops']} TFLOP/s" for k_, v in out['F4_qgemm'].items()
+                    if isinstance(v, dict)))
     return out
 
 
