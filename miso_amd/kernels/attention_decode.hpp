@@ -939,7 +939,7 @@ __device__ __attribute__((always_inline)) inline void issue_tile(
 // Per-lane state of a wave over its split (lane l, g = l / 16, c = l % 16, head h = c % 8).
 //   q[s]: B operand of k-step s: head h's query x log2(e)/16, dimensions 8 (4 s + g) + j, as
 //         its hi (c < 8) or lo (c >= 8) f16 half.
-//   m: the reference max of head h (log2 units, -inf before the first tile), moved lazily;
+//   m: the reference max of head h (log2 units, 0 before the first tile), moved lazily;
 //   mt: the true max; l: the sum of this lane's numerators (keys 4 g + i and 16 + 4 g + i of
 //   every tile, relative to m).
 //   o[b]: O^T of dimensions 64 w + 16 b + 4 g + i, column c, relative to m.
@@ -987,46 +987,81 @@ __device__ __attribute__((always_inline)) inline void score_step(f32x4 (&s)[2],
   }
 }
 
-// The softmax update of one tile from its raw score accumulators `s`, speculating that the
-// reference max stays: joins the (hi, lo) columns (lane c and lane c ^ 8 both form hi + 2^-11 lo
-// of head c % 8), masks keys k0 + key >= lim when kMasked, forms the numerators 2^(x - m) with the
-// current m, their sum and this lane's half of each as the P^T operand. Returns whether the
-// reference max must move (the tile's head max exceeds m by more than the slack, in any lane;
-// always on the first tile, m = -inf); then the caller runs tile_rescale before using them.
+// The softmax of one tile, in log2 units relative to the reference max m of the lane's head.
+// The (hi, lo) columns are joined in every lane (lane c and lane c ^ 8 both form hi + 2^-11 lo
+// of head c % 8) with m subtracted in the same instructions; keys k0 + key >= lim are masked when
+// kMasked. The numerators 2^x are speculated with the current m; the reference max moves (the
+// caller runs tile_rescale before using them) when the tile's head max exceeds m by more than
+// the slack in any lane, and always on the split's first tile, whose max becomes m.
 struct TileSoftmax {
-  float x[8];
-  float mx, lt;
+  float x[8];    // scores minus m, -inf where masked
+  float mx, lt;  // the tile's head max of x; the sum of the numerators
   cdna4::half8_t pb;
 };
 
-__device__ __attribute__((always_inline)) inline void tile_numerators(TileSoftmax& sm, float m,
-                                                                     bool is_hi) {
-  _Float16 ph[8];
-  float lt = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float p = __builtin_amdgcn_exp2f(sm.x[i] - m);  // 0 if masked
-    lt += p;
-    const _Float16 hi = static_cast<_Float16>(p);
-    const _Float16 lo = static_cast<_Float16>((p - static_cast<float>(hi)) * kLoScale);
-    ph[i] = is_hi ? hi : lo;
-  }
-  sm.lt = lt;
-  sm.pb = cdna4::half8_t{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+// Per-lane constants of the pair columns: the join weights (hi lanes 1 and 2^-11 for their own
+// and the partner's accumulator, lo lanes the reverse) and the numerator split r = f16(hi nsb +
+// p sa), which is hi = f16(p) in the hi lanes (sa = 1, nsb = 0) and the lo half f16((p - hi)
+// 2^11) in the lo lanes (sa = 2^11, nsb = -2^11): one expression, no select.
+struct TileLane {
+  float w_own, w_other, sa, nsb;
+};
+__device__ __attribute__((always_inline)) inline TileLane tile_lane(unsigned lane) {
+  const bool is_hi = (lane & 15u) < 8;
+  return is_hi ? TileLane{1.0f, kLoWeight, 1.0f, 0.0f}
+               : TileLane{kLoWeight, 1.0f, kLoScale, -kLoScale};
 }
 
-template <bool kMasked>
+// max(a, b) and max(a, b, c) without canonicalising the inputs (scores are never NaN).
+__device__ __attribute__((always_inline)) inline float tile_max(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __attribute__((always_inline)) inline float tile_max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// x = (own w_own + partner w_other) kscale - m. own w_own is exact (a power of two), and one
+// v_fmac adds the partner (lane ^ 8) read through DPP, so both lanes of a pair round the same
+// exact sum hi + 2^-11 lo once and hold identical x: the pair's hi and lo halves of each
+// numerator are then cut from the same value. kscale: the keys' K row scales (kKScale), else 1.
+// The leading s_nop gives the DPP source reads the two wait states they need after a VALU write.
+template <bool kMasked, bool kKScale = false>
 __device__ __attribute__((always_inline)) inline void tile_scores_joined(
-    TileSoftmax& sm, const f32x4 (&s)[2], unsigned k0, unsigned lim, unsigned lane) {
-  const unsigned g = lane >> 4, c = lane & 15u;
-  const bool is_hi = c < 8;
-  const float w_own = is_hi ? 1.0f : kLoWeight, w_other = is_hi ? kLoWeight : 1.0f;
+    TileSoftmax& sm, const f32x4 (&s)[2], float m, unsigned k0, unsigned lim, unsigned lane,
+    const TileLane& tl, const float* kscale = nullptr) {
+  float own[8], t[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float own = s[i / 4][i % 4];
-    sm.x[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(own), w_other, own * w_own);
+    own[i] = s[i / 4][i % 4];
+    t[i] = own[i] * tl.w_own;
+  }
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %8, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %9, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %10, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %11, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %4, %12, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %5, %13, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %6, %14, %16 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %7, %15, %16 row_ror:8 row_mask:0xf bank_mask:0xf"
+      : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]),
+        "+v"(t[7])
+      : "v"(own[0]), "v"(own[1]), "v"(own[2]), "v"(own[3]), "v"(own[4]), "v"(own[5]),
+        "v"(own[6]), "v"(own[7]), "v"(tl.w_other));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (kKScale)
+      sm.x[i] = __builtin_fmaf(t[i], kscale[i], -m);
+    else
+      sm.x[i] = t[i] - m;
   }
   if constexpr (kMasked) {
+    const unsigned g = lane >> 4;
 #pragma unroll
     for (unsigned i = 0; i < 8; ++i) {
       const unsigned key = k0 + (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4));
@@ -1035,32 +1070,89 @@ __device__ __attribute__((always_inline)) inline void tile_scores_joined(
   }
 }
 
-// Head max over the tile (the lane's 8 keys, then the 4 lanes g of its column; every tile has a
-// key in the split, so it is finite), the true max, and the speculative numerators.
-__device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& sm, TileState& st,
-                                                                 unsigned lane) {
-  const float* x = sm.x;
-  float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                   fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-  mx = cdna4::max_xor32(cdna4::max_xor16(mx));
-  sm.mx = mx;
-  st.mt = fmaxf(st.mt, mx);
-  tile_numerators(sm, st.m, (lane & 15u) < 8);
-  return __builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack) != 0;
+// The numerators p = 2^(x - shift) (times vr, the V row scale ratios, when kV), their sum (of the
+// unscaled p) and this lane's half of each as the P^T operand.
+template <bool kV>
+__device__ __attribute__((always_inline)) inline void tile_numerators(TileSoftmax& sm, float shift,
+                                                                     const TileLane& tl,
+                                                                     const float* vr) {
+  _Float16 ph[8];
+  float lt = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float p0 = __builtin_amdgcn_exp2f(sm.x[i] - shift);  // 0 if masked
+    float p1 = __builtin_amdgcn_exp2f(sm.x[i + 1] - shift);
+    lt += p0;
+    lt += p1;
+    if constexpr (kV) {
+      p0 *= vr[i];
+      p1 *= vr[i + 1];
+    }
+    const cdna4::half2_t h{static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
+    ph[i] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[0]), tl.nsb, p0 * tl.sa));
+    ph[i + 1] =
+        static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[1]), tl.nsb, p1 * tl.sa));
+  }
+  sm.lt = lt;
+  sm.pb = cdna4::half8_t{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
 }
 
-// The rare path: move the reference max to max(m, tile max), rescale l and O, and redo the
-// numerators.
-__device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& sm, TileState& st,
-                                                                  unsigned lane) {
-  const float mn = fmaxf(st.m, sm.mx);
-  const float corr = __builtin_amdgcn_exp2f(st.m - mn);  // 0 on the first tile (m = -inf)
-  st.m = mn;
-  st.l *= corr;
+// Head max over the tile (the lane's 8 keys, then the 4 lanes g of its column; every tile has a
+// key in the split, so it is finite), the true max, and the speculative numerators. `first`:
+// the split's first tile (wave-uniform).
+template <bool kV = false>
+__device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& sm, TileState& st,
+                                                                 bool first, const TileLane& tl,
+                                                                 const float* vr = nullptr) {
+  const float* x = sm.x;
+  float mx = tile_max3(tile_max3(x[0], x[1], x[2]), tile_max3(x[3], x[4], x[5]),
+                       tile_max(x[6], x[7]));
+  {
+    const cdna4::Pair a = cdna4::swap16(mx, mx);
+    mx = tile_max(a.a, a.b);
+    const cdna4::Pair b = cdna4::swap32(mx, mx);
+    mx = tile_max(b.a, b.b);
+  }
+  sm.mx = mx;
+  st.mt = fmaxf(st.mt, mx + st.m);
+  tile_numerators<kV>(sm, 0.0f, tl, vr);
+  return first || __builtin_amdgcn_ballot_w64(mx > kRescaleSlack) != 0;
+}
+
+// O *= c for accumulators in AGPRs, in place (the copies through a VGPR stay inside the rarely
+// taken branch; as C++, the compiler hoists copies of O out of it to every iteration). The
+// leading no-ops let the last P V MFMA's results settle; the trailing ones separate the AGPR
+// writes from the next MFMA reading them.
+__device__ __attribute__((always_inline)) inline void tile_scale_o(f32x4 (&o)[4], float c) {
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
   for (int b = 0; b < 4; ++b)
-    st.o[b] *= corr;
-  tile_numerators(sm, st.m, (lane & 15u) < 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = o[b][i], tmp;
+      asm volatile(
+          "v_accvgpr_read_b32 %1, %0\n\t"
+          "v_mul_f32 %1, %1, %2\n\t"
+          "v_accvgpr_write_b32 %0, %1"
+          : "+a"(x), "=&v"(tmp)
+          : "v"(c));
+      o[b][i] = x;
+    }
+  asm volatile("s_nop 3" ::: "memory");
+}
+
+// The rare path: move the reference max of each head by d = max(0, tile max) (the tile max on
+// the first tile), rescale l and O, and redo the numerators.
+template <bool kV = false>
+__device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& sm, TileState& st,
+                                                                  bool first, const TileLane& tl,
+                                                                  const float* vr = nullptr) {
+  const float d = first ? sm.mx : fmaxf(sm.mx, 0.0f);
+  const float corr = first ? 0.0f : __builtin_amdgcn_exp2f(-d);  // l and O are 0 on the first
+  st.m += d;
+  st.l *= corr;
+  tile_scale_o(st.o, corr);
+  tile_numerators<kV>(sm, d, tl, vr);
 }
 
 // Partial (m, l, o) of KV head kvh over keys [span.begin, span.end) (span.end <= len), written at
@@ -1128,13 +1220,14 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
   };
 
   TileState st;
-  st.m = -__builtin_inff();
+  st.m = 0.0f;
   st.mt = -__builtin_inff();
   st.l = 0.0f;
 #pragma unroll
   for (int b = 0; b < 4; ++b)
     st.o[b] = f32x4{};
   f32x4 s_cur[2] = {f32x4{}, f32x4{}};
+  const TileLane tln = tile_lane(lane);
 
   if (n_tiles > 0) {
     wait_tiles_after(n_tiles - 1 < 2 ? n_tiles - 1 : 2);  // tile 0 and the queries landed
@@ -1170,10 +1263,10 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
   // tile ti + 3). The 16 score MFMAs of tile ti + 1 go to the matrix cores interleaved with the
   // VALU softmax of tile ti, whose scores the previous iteration produced; then O += V^T P^T of
   // tile ti. The last tile has no successor: its softmax and P V alone.
-  auto softmax_pv = [&](const half8_t (&va)[4], TileSoftmax& sm, bool moved)
+  auto softmax_pv = [&](const half8_t (&va)[4], TileSoftmax& sm, bool moved, bool first)
       __attribute__((always_inline)) {
     if (moved)
-      tile_rescale(sm, st, lane);
+      tile_rescale(sm, st, first, tln);
     st.l += sm.lt;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
@@ -1182,9 +1275,9 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
   auto join = [&](unsigned ti, TileSoftmax& sm) __attribute__((always_inline)) {
     const unsigned k0 = span.begin + ti * kTileKeys;
     if (k0 + kTileKeys > span.end)  // uniform: only the last tile
-      tile_scores_joined<true>(sm, s_cur, k0, span.end, lane);
+      tile_scores_joined<true>(sm, s_cur, st.m, k0, span.end, lane, tln);
     else
-      tile_scores_joined<false>(sm, s_cur, k0, span.end, lane);
+      tile_scores_joined<false>(sm, s_cur, st.m, k0, span.end, lane, tln);
   };
   for (unsigned ti = 0; ti + 1 < n_tiles; ++ti) {
     const unsigned ahead = n_tiles - 2 - ti;  // copies issued after tile ti + 1's
@@ -1202,7 +1295,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
 #pragma unroll
     for (unsigned s = 0; s < 8; ++s)
       score_step(s_next, ka, st.q[s], s);
-    const bool moved = tile_decide(sm, st, lane);
+    const bool moved = tile_decide(sm, st, ti == 0, tln);
     // The speculative numerators are computed here, between the MFMAs, not sunk past the branch.
     asm volatile("" : "+v"(sm.lt), "+v"(sm.pb));
     // 16 MFMAs, each followed by up to 6 VALU instructions of the softmax.
@@ -1211,7 +1304,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
-    softmax_pv(va, sm, moved);
+    softmax_pv(va, sm, moved, ti == 0);
     s_cur[0] = s_next[0];
     s_cur[1] = s_next[1];
   }
@@ -1221,8 +1314,8 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
     join(ti, sm);
     half8_t va[4];
     read_v(va, vslot(ti), vl);
-    const bool moved = tile_decide(sm, st, lane);
-    softmax_pv(va, sm, moved);
+    const bool moved = tile_decide(sm, st, ti == 0, tln);
+    softmax_pv(va, sm, moved, ti == 0);
   }
 
   // Relative to the true max; l summed over the lanes g of the column; the (hi, lo) columns of

@@ -491,9 +491,10 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
     if (kNext && j == 1)
       corr[0] = decide_block<kMaskNext>(s[0], rw.m[0], rw.l[0], next[0], k0_next, lim[0], hi,
                                         moved[0]);
-    if (kNext && kBlocks == 2 && j == 5)
-      corr[1] = decide_block<kMaskNext>(s[1], rw.m[1], rw.l[1], next[1], k0_next, lim[1], hi,
-                                        moved[1]);
+    if constexpr (kBlocks == 2)
+      if (kNext && j == 5)
+        corr[1] = decide_block<kMaskNext>(s[1], rw.m[1], rw.l[1], next[1], k0_next, lim[1], hi,
+                                          moved[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
   drain_pv();
