@@ -466,6 +466,31 @@ def bench_other(torch, A, args):
                      "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
                      "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del caches8
+    # C4 over an e4m3-row cache: the 16384 rows widened to f16 into a workspace each call, then
+    # the f16 prefill (attn_prefill_fp8).
+    if not args.no_prefill:
+        pos0, n = 8192, 8192
+        m4 = pos0 + n
+        gen.manual_seed(m4 + 1)
+        q4 = torch.randn(n * H * D, generator=gen, device="cuda")
+        qg4 = torch.randn(n * H * 2 * D, generator=gen, device="cuda")
+        c8 = A.Fp8Cache(m4)
+        A.attn_kv_encode_fp8(torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
+                             torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
+                             c8, 0, m4)
+        ws4 = A.Fp8PrefillScratch(m4)
+        core4 = torch.empty(n * H * D, device="cuda")
+        g = graph_of(torch, lambda _: A.attn_prefill_fp8(q4, qg4, c8, core4, pos0, n, ws4), 1)
+        time_replays(torch, g, 1)
+        t4 = sorted(time_replays(torch, g, args.prefill_steps)[0]
+                    for _ in range(3))[1] / args.prefill_steps
+        flop4 = 4.0 * H * D * (n * pos0 + n * (n + 1) // 2)
+        out["C4_fp8"] = {"workload": "C4 (causal prefill, 8192 tokens after an 8192-token prefix) "
+                                     "over an e4m3-row cache: rows widened to f16, then the f16 "
+                                     "prefill",
+                         "ms_per_call": round(t4, 4),
+                         "tflops": round(flop4 / (t4 * 1e-3) / 1e12, 1)}
+        del c8, ws4, q4, qg4, core4
     # The projection GEMVs (row f4), f16 activations as the engine; weights rotated over >= 512 MB
     # of copies so they stream from HBM as a model's layers do.
     def rotated(nbytes):
@@ -548,7 +573,8 @@ def bench_other(torch, A, args):
                        "tokens": n_tok, **gemm}
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
-        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, q4k gemv "
+        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, "
+        f"C4 fp8 {out.get('C4_fp8', {}).get('tflops')} TFLOP/s, q4k gemv "
         + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
                     for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
         + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "

@@ -208,6 +208,25 @@ int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, con
                          float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
                          uint32_t n_splits, void* stream);
 
+/* miso_attn_prep_batch with the tokens' K / V appended as e4m3 rows at positions pos0 .. pos0 +
+ * n - 1 (q output, layouts and rejections as miso_attn_prep_batch; every row equals the one
+ * miso_attn_prep_fp8 writes for its token). n == 0 is a no-op. */
+int miso_attn_prep_batch_fp8(const float* qg, const float* k, const float* v, const float* q_norm,
+                             const float* k_norm, const float* inv_freq, uint8_t* k8, uint8_t* v8,
+                             float* k_scale, float* v_scale, float* q, uint32_t pos0,
+                             uint32_t max_ctx, float eps, uint32_t n, uint32_t proj_stride,
+                             void* stream);
+
+/* miso_attn_prefill over e4m3 rows: rows [0, pos0 + n) of both KV heads are widened to f16
+ * (value = scale * e4m3(code), rounded to nearest even after saturating at +-65504) into the
+ * caller's workspaces k_ws / v_ws, each 2 * (pos0 + n) * 256 binary16 values ([2][pos0 + n][256],
+ * 16-byte aligned), then the f16 causal prefill runs over them. Layouts of q, qg, core and the
+ * rejections as miso_attn_prefill. */
+int miso_attn_prefill_fp8(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
+                          const float* k_scale, const float* v_scale, uint16_t* k_ws,
+                          uint16_t* v_ws, float* core, uint32_t pos0, uint32_t n,
+                          uint32_t max_ctx, uint32_t qg_stride, void* stream);
+
 /* Q4_K GEMV y = W x (the attention's Q4_K projections attn_q, attn_k, attn_output). Replaces the
  * launches of q4k_gemv_kernel<ActFormat, K, 256, R> in gemv() (src/engine/weights.hip:248-275,
  * kernels/q4k_gemv.hpp:196-239). w: n_rows rows of k / 256 Q4_K blocks in the r1 layout

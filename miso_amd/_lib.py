@@ -40,6 +40,10 @@ SIGNATURES = {
                                    P]),
     "miso_attn_decode_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                      P]),
+    "miso_attn_prep_batch_fp8": (c_int, [P, P, P, P, P, P, P, P, P, P, P, c_uint32, c_uint32,
+                                         c_float, c_uint32, c_uint32, P]),
+    "miso_attn_prefill_fp8": (c_int, [P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
+                                      c_uint32, P]),
     "miso_attn_q4k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, c_int, P]),
     "miso_attn_q6k_gemv": (c_int, [P, P, P, c_uint32, c_uint32, P]),
     "miso_attn_q4k_q6k_gemv_pair": (c_int, [P, c_uint32, P, P, c_uint32, P, P, P]),

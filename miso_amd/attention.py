@@ -298,6 +298,53 @@ def attn_prep_fp8(qg, k, v, q_norm, k_norm, inv_freq, cache: Fp8Cache, q, pos: i
         *(_ptr(b) for b in cache.buffers()), _ptr(q), pos, cache.max_ctx, eps, _stream(stream)))
 
 
+def attn_prep_batch_fp8(qg, k, v, q_norm, k_norm, inv_freq, cache: Fp8Cache, q, pos0: int,
+                        n: int, proj_stride: int, eps: float = 1e-6, stream=None) -> None:
+    """attn_prep_batch appending the tokens' K / V to `cache` as e4m3 rows at pos0 .. pos0 + n - 1;
+    qg / k / v are views into a token-major projection buffer, rows proj_stride floats apart."""
+    f32 = torch.float32
+    for name, t in (("qg", qg), ("k", k), ("v", v)):
+        if not t.is_cuda or t.dtype != f32:
+            raise ValueError(f"{name} must be a float32 device tensor")
+    for name, t, m in (("q_norm", q_norm, DIM), ("k_norm", k_norm, DIM),
+                       ("inv_freq", inv_freq, 32), ("q", q, n * Q_HEADS * DIM)):
+        _need(t, name, f32, m)
+    _need_fp8(cache)
+    _lib.check(_lib.load().miso_attn_prep_batch_fp8(
+        _ptr(qg), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(inv_freq),
+        *(_ptr(b) for b in cache.buffers()), _ptr(q), pos0, cache.max_ctx, eps, n, proj_stride,
+        _stream(stream)))
+
+
+class Fp8PrefillScratch:
+    """f16 workspaces for attn_prefill_fp8 over up to max_rows cache rows (pos0 + n)."""
+
+    def __init__(self, max_rows: int, device="cuda"):
+        self.max_rows = max_rows
+        self.k = torch.empty(KV_HEADS * max_rows * DIM, dtype=torch.float16, device=device)
+        self.v = torch.empty(KV_HEADS * max_rows * DIM, dtype=torch.float16, device=device)
+
+
+def attn_prefill_fp8(q, qg, cache: Fp8Cache, core, pos0: int, n: int,
+                     scratch: Optional[Fp8PrefillScratch] = None, qg_stride: int = QG_STRIDE,
+                     stream=None) -> Fp8PrefillScratch:
+    """attn_prefill over an e4m3 cache: rows [0, pos0 + n) widened to f16 into `scratch` (made
+    here when None), then the f16 causal prefill over them. Returns the scratch used."""
+    if scratch is None:
+        scratch = Fp8PrefillScratch(pos0 + n, device=q.device)
+    if pos0 + n > scratch.max_rows:
+        raise ValueError("pos0 + n exceeds the scratch capacity")
+    f32 = torch.float32
+    _need(q, "q", f32, n * Q_HEADS * DIM)
+    _need(qg, "qg", f32, (n - 1) * qg_stride + Q_HEADS * 2 * DIM if n else 0)
+    _need(core, "core", f32, n * Q_HEADS * DIM)
+    _need_fp8(cache)
+    _lib.check(_lib.load().miso_attn_prefill_fp8(
+        _ptr(q), _ptr(qg), *(_ptr(b) for b in cache.buffers()), _ptr(scratch.k), _ptr(scratch.v),
+        _ptr(core), pos0, n, cache.max_ctx, qg_stride, _stream(stream)))
+    return scratch
+
+
 def attn_decode_fp8(q, qg, cache: Fp8Cache, core, scratch: DecodeScratch, length: int,
                     n_splits: Optional[int] = None, stream=None) -> int:
     """attn_decode over an e4m3 cache: split + combine over keys [0, length)."""

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
@@ -439,6 +440,55 @@ int miso_attn_decode_fp8(const float* q, const float* qg, const uint8_t* k8, con
   if (rc != 0)
     return rc;
   return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
+}
+
+int miso_attn_prep_batch_fp8(const float* qg, const float* kp, const float* v,
+                             const float* q_norm, const float* k_norm, const float* inv_freq,
+                             uint8_t* k8, uint8_t* v8, float* k_scale, float* v_scale, float* q,
+                             uint32_t pos0, uint32_t max_ctx, float eps, uint32_t n,
+                             uint32_t proj_stride, void* stream) {
+  if (n == 0)
+    return 0;
+  if (any_bad(qg, kp, v, q_norm, k_norm, inv_freq, k8, v8, q) || bad_scalars(k_scale) ||
+      bad_scalars(v_scale))
+    return fail("miso_attn_prep_batch_fp8", kBadPtr);
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail("miso_attn_prep_batch_fp8", "KV cache is full (pos0 + n > max_ctx)");
+  if (proj_stride < 8192 + 1024)
+    return fail("miso_attn_prep_batch_fp8",
+                "proj_stride must cover [q+gate 8192 | k 512 | v 512]");
+  const k::AttnPrepBatchFp8Params p{
+      {qg, kp, v, q_norm, k_norm, inv_freq, k8, v8, k_scale, v_scale, q, pos0, max_ctx, eps},
+      n,
+      proj_stride};
+  k::attn_prep_batch_fp8_kernel<256><<<n * 18, 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prep_batch_fp8");
+}
+
+int miso_attn_prefill_fp8(const float* q, const float* qg, const uint8_t* k8, const uint8_t* v8,
+                          const float* k_scale, const float* v_scale, uint16_t* k_ws,
+                          uint16_t* v_ws, float* core, uint32_t pos0, uint32_t n,
+                          uint32_t max_ctx, uint32_t qg_stride, void* stream) {
+  if (any_bad(q, qg, k8, v8, k_ws, v_ws, core) || bad_scalars(k_scale) || bad_scalars(v_scale))
+    return fail("miso_attn_prefill_fp8", kBadPtr);
+  if (n == 0)
+    return fail("miso_attn_prefill_fp8", "n must be >= 1");
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail("miso_attn_prefill_fp8", "KV cache is full (pos0 + n > max_ctx)");
+  if (qg_stride < 8192 || qg_stride % 4 != 0)
+    return fail("miso_attn_prefill_fp8", "qg_stride must be >= 8192 and a multiple of 4");
+  const uint32_t rows = pos0 + n;
+  const k::AttnKvFp8WidenParams w{k8,           v8, k_scale, v_scale, as_half(k_ws),
+                                  as_half(v_ws), rows, max_ctx};
+  const uint32_t wgrid = std::min<uint32_t>(rows, 4096);  // 4 rows per workgroup, grid-stride
+  k::attn_kv_fp8_widen_kernel<256><<<wgrid, 256, 0, as_stream(stream)>>>(w);
+  const int rc = launched("miso_attn_prefill_fp8");
+  if (rc != 0)
+    return rc;
+  const k::AttnPrefillParams p{q, qg, as_half(k_ws), as_half(v_ws), core, pos0, n, rows,
+                               qg_stride};
+  k::attn_prefill_kernel<256><<<k::attn_prefill_items(n), 256, 0, as_stream(stream)>>>(p);
+  return launched("miso_attn_prefill_fp8");
 }
 
 int miso_attn_q4k_gemv(const uint8_t* w, const float* x, float* y, uint32_t n_rows, uint32_t k,

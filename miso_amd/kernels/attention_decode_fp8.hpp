@@ -15,6 +15,8 @@
 // Kernels:
 //   attn_kv_fp8_encode_kernel<256>  f16 cache rows [pos0, pos0 + n) of both KV heads -> e4m3 rows
 //   attn_prep_fp8_kernel<256>       attn_prep (RMSNorm + RoPE) appending the token as e4m3 rows
+//   attn_prep_batch_fp8_kernel<256> the same for a batch of tokens (attn_prep_batch's layout)
+//   attn_kv_fp8_widen_kernel<256>   e4m3 rows -> f16 rows, for the f16 prefill over an e4m3 cache
 //   attn_split_fp8_kernel<256>      split-K partials over e4m3 rows, in the reference's partial
 //                                   layout; attn_combine_kernel merges them unchanged.
 
@@ -172,6 +174,84 @@ template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_prep_fp8_kernel(AttnPrepFp8Params p) {
   for (unsigned head = blockIdx.x; head < attn::kQHeads + attn::kKvHeads; head += gridDim.x)
     attn_prep_fp8_head<kBlock>(p, head);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Batched prep with an e4m3 append (the counterpart of attn_prep_batch_kernel,
+// kernels/attention_prefill.hpp:20-40)
+// ------------------------------------------------------------------------------------------------
+
+// Token t of the batch: tok0 with qg / k / v advanced by t proj_stride floats, q by t 16 x 256
+// floats and the position by t (AttnPrepBatchParams over e4m3 rows).
+struct AttnPrepBatchFp8Params {
+  AttnPrepFp8Params tok0;
+  unsigned n, proj_stride;
+};
+
+// Items [0, 18 n) token-major, one workgroup each (grid-stride): attn_prep_fp8_head of token
+// item / 18, head item % 18, so every row equals the one attn_prep_fp8_kernel writes for it.
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_prep_batch_fp8_kernel(AttnPrepBatchFp8Params p) {
+  constexpr unsigned kHeads = attn::kQHeads + attn::kKvHeads;
+  for (unsigned item = blockIdx.x; item < p.n * kHeads; item += gridDim.x) {
+    const unsigned t = item / kHeads, head = item % kHeads;
+    AttnPrepFp8Params one = p.tok0;
+    one.qg += std::size_t{t} * p.proj_stride;
+    one.k += std::size_t{t} * p.proj_stride;
+    one.v += std::size_t{t} * p.proj_stride;
+    one.q += std::size_t{t} * attn::kQHeads * attn::kDim;
+    one.pos += t;
+    attn_prep_fp8_head<kBlock>(one, head);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Widening e4m3 rows to f16 (prefill over an e4m3 cache)
+// ------------------------------------------------------------------------------------------------
+
+// The causal prefill is bound by its MFMAs, which take f16 operands: over an e4m3 cache the
+// rows a chunk attends to are widened once into an f16 workspace and the f16 prefill runs on it
+// (the widening moves 3 bytes per element, microseconds against the milliseconds of the MFMAs).
+// Rows [0, n) of both KV heads of the e4m3 cache (head stride max_ctx rows) go to the workspace
+// [2][n][256] f16 (head stride n rows): value = scale e4m3(code), exact in f32, rounded to f16
+// (RNE) after saturating at +-65504 -- only a row whose largest magnitude rounds to 2^16 at
+// encoding (max |x| >= 63488) reaches that bound.
+struct AttnKvFp8WidenParams {
+  const uint8_t* k8;  // [2][max_ctx][256]
+  const uint8_t* v8;
+  const float* k_scale;  // [2][max_ctx]
+  const float* v_scale;
+  attn::half_t* k_out;  // [2][n][256]
+  attn::half_t* v_out;
+  unsigned n, max_ctx;
+};
+
+// One wave per row (4 per workgroup), lane i widening dimensions 4 i .. 4 i + 3; row r of the 4 n
+// is (position r / 4, KV head r / 2 % 2, K if r is even else V). Grid-stride.
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_kv_fp8_widen_kernel(AttnKvFp8WidenParams p) {
+  static_assert(kBlock == 256, "four rows per workgroup");
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (unsigned r = 4 * blockIdx.x + wave; r < 4 * p.n; r += 4 * gridDim.x) {
+    const bool is_v = r & 1u;
+    const unsigned kvh = (r >> 1) & 1u, pos = r >> 2;
+    const std::size_t src = std::size_t{kvh} * p.max_ctx + pos;
+    const std::size_t dst = std::size_t{kvh} * p.n + pos;
+    const unsigned w = *reinterpret_cast<const unsigned*>((is_v ? p.v8 : p.k8) +
+                                                          src * attn::kDim + 4 * lane);
+    const float sc = (is_v ? p.v_scale : p.k_scale)[src];
+    const cdna4::half2_t a = cdna4::as_half2(fp8kv::pair_lo(w));
+    const cdna4::half2_t b = cdna4::as_half2(fp8kv::pair_hi(w));
+    const float e[4] = {static_cast<float>(a[0]), static_cast<float>(a[1]),
+                        static_cast<float>(b[0]), static_cast<float>(b[1])};
+    _Float16 h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      h[i] = static_cast<_Float16>(fminf(fmaxf(e[i] * sc, -65504.0f), 65504.0f));
+    *reinterpret_cast<uint2*>((is_v ? p.v_out : p.k_out) + dst * attn::kDim + 4 * lane) =
+        __builtin_bit_cast(uint2, h);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------

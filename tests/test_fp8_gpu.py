@@ -8,7 +8,10 @@
   * prep: the q output bit-identical to attn_prep's, V codes bit-identical to the oracle's, K
     within half a code step of the oracle's normalised, rotated row;
   * the format's own error against the f16 cache (reported, bounded loosely): it is a property
-    of e4m3 storage, not of the kernels.
+    of e4m3 storage, not of the kernels;
+  * prefill over e4m3 rows: the f16 workspace rows bit-identical to f16(scale e4m3(code)) with
+    saturation at 65504, the prefill against the FP64 prefill oracle over those rows (same
+    gate), and the batched e4m3 prep bit-identical to the single-token one.
 """
 from __future__ import annotations
 
@@ -226,3 +229,117 @@ def test_prep_fp8_and_engine_sequence(O, attn, torch_mod):
         st = O.compare(to_host(out).reshape(H, D), ref)
         report(f"fp8 engine decode len={pos + 1}", st)
         assert st["ok"], st
+
+
+def widen_host(O, codes, scales):
+    """Rows as attn_prefill_fp8 widens them: f16(clamp(scale * e4m3(code), +-65504)), RNE. The
+    product is exact in f32, so the float64 dequant rounded once to f16 is the same value."""
+    val = np.clip(O.fp8_dequant(codes, scales), -65504.0, 65504.0).astype(np.float32)
+    return O.f32_to_f16(val)
+
+
+def run_prefill_fp8(attn, torch, p, cache):
+    n, S = p["n"], p["qg_stride"]
+    core = torch.full((n * H * D,), CANARY, dtype=torch.float32, device="cuda")
+    ws = attn.attn_prefill_fp8(to_dev(torch, p["q"]), to_dev(torch, p["qg"]), cache, core,
+                               p["pos0"], n, qg_stride=S)
+    torch.cuda.synchronize()
+    out = to_host(core).reshape(n, H, D)
+    assert not (out == CANARY).any(), "unwritten outputs"
+    return out, ws
+
+
+def test_prefill_fp8_widening_bit_exact(O, attn, torch_mod):
+    """The f16 workspace rows equal f16(scale * e4m3(code)) for every finite code, scales from
+    2^-107 to 2^8, and saturate at 65504 where a code of 256 meets the largest scale."""
+    torch = torch_mod
+    rows = 300
+    max_ctx = rows + 3
+    rng = np.random.default_rng(31)
+    finite = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=np.uint8)
+    k8 = rng.choice(finite, size=(KV, max_ctx, D)).astype(np.uint8)
+    v8 = rng.choice(finite, size=(KV, max_ctx, D)).astype(np.uint8)
+    k8[:, :2, :len(finite)] = finite  # every finite code at least once
+    ks = (2.0 ** rng.integers(-107, 9, size=(KV, max_ctx))).astype(np.float32)
+    vs = (2.0 ** rng.integers(-107, 9, size=(KV, max_ctx))).astype(np.float32)
+    ks[:, 5] = vs[:, 5] = 256.0
+    k8[:, 5, :4] = v8[:, 5, :4] = [0x78, 0xF8, 0x77, 0x70]  # 256, -256, 240, 128 at scale 2^8
+    cache = upload(attn, torch, k8, ks, v8, vs, max_ctx)
+    p = O.prefill_inputs(5, rows - 1, 1, max_ctx)
+    out, ws = run_prefill_fp8(attn, torch, p, cache)
+    assert np.isfinite(out).all()
+    gk = to_host(ws.k).view(np.uint16).reshape(KV, rows, D)
+    gv = to_host(ws.v).view(np.uint16).reshape(KV, rows, D)
+    assert np.array_equal(gk, widen_host(O, k8[:, :rows], ks[:, :rows]))
+    assert np.array_equal(gv, widen_host(O, v8[:, :rows], vs[:, :rows]))
+    assert O.f16_to_f32(gk[:, 5, :2]).tolist() == [[65504.0, -65504.0]] * KV
+
+
+@pytest.mark.parametrize("pos0,n", [(0, 1), (0, 33), (40, 17), (100, 128), (1000, 77)])
+def test_prefill_fp8_matches_oracle(O, attn, torch_mod, pos0, n):
+    """Prefill over e4m3 rows against the FP64 prefill oracle over the same rows widened to f16
+    (the kernel's f16 operands), every row, gate |got - ref| <= 2e-3 + 1e-2 |ref|."""
+    torch = torch_mod
+    max_ctx = pos0 + n + 5
+    p = O.prefill_inputs(3000 + pos0 + n, pos0, n, max_ctx, q_scale=2.0)
+    k8, ks, v8, vs = encode_host(O, p["k"], p["v"], max_ctx)
+    cache = upload(attn, torch, k8, ks, v8, vs, max_ctx)
+    got, _ = run_prefill_fp8(attn, torch, p, cache)
+    kw = widen_host(O, k8, ks).reshape(-1)
+    vw = widen_host(O, v8, vs).reshape(-1)
+    ref = O.prefill_f64(p["q"], p["qg"], p["qg_stride"], kw, vw, pos0, max_ctx, np.arange(n))
+    st = O.compare(got, ref)
+    report(f"fp8 prefill pos0={pos0} n={n}", st)
+    assert st["ok"], st
+
+
+def test_prep_batch_fp8_equals_single_token_prep(O, attn, torch_mod):
+    """prep_batch_fp8 over 37 tokens writes the same e4m3 rows, scales and q as 37 calls of
+    prep_fp8, bit for bit."""
+    torch = torch_mod
+    PROJ, EPS, n, pos0, max_ctx = 9216, 1e-6, 37, 5, 64
+    rng = np.random.default_rng(41)
+    q_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    k_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    w = [to_dev(torch, a) for a in (q_norm, k_norm, O.inv_freq(10_000_000.0))]
+    proj = to_dev(torch, O.normal(4242, n * PROJ))
+    a, b = attn.Fp8Cache(max_ctx), attn.Fp8Cache(max_ctx)
+    qa = torch.empty(n * H * D, device="cuda")
+    qb = torch.empty(n * H * D, device="cuda")
+    attn.attn_prep_batch_fp8(proj, proj[8192:], proj[8704:], *w, a, qa, pos0, n, PROJ, EPS)
+    for t in range(n):
+        r = proj[t * PROJ:(t + 1) * PROJ]
+        attn.attn_prep_fp8(r[:8192], r[8192:8704], r[8704:], *w, b, qb[t * H * D:(t + 1) * H * D],
+                           pos0 + t, EPS)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(qa), to_host(qb))
+    for x, y in zip(a.buffers(), b.buffers()):
+        assert np.array_equal(to_host(x), to_host(y))
+
+
+def test_prep_batch_fp8_then_prefill_fp8(O, attn, torch_mod):
+    """The engine's prefill over an e4m3 cache: a 300-token prompt prepped in one batch, then
+    the prefill over the cache it built, against the oracle over the widened rows."""
+    torch = torch_mod
+    PROJ, EPS, n, max_ctx = 9216, 1e-6, 300, 320
+    rng = np.random.default_rng(43)
+    q_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    k_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    w = [to_dev(torch, a) for a in (q_norm, k_norm, O.inv_freq(10_000_000.0))]
+    proj_h = O.normal(4343, n * PROJ)
+    proj = to_dev(torch, proj_h)
+    cache = attn.Fp8Cache(max_ctx)
+    q = torch.empty(n * H * D, device="cuda")
+    attn.attn_prep_batch_fp8(proj, proj[8192:], proj[8704:], *w, cache, q, 0, n, PROJ, EPS)
+    core = torch.full((n * H * D,), CANARY, dtype=torch.float32, device="cuda")
+    attn.attn_prefill_fp8(q, proj, cache, core, 0, n, qg_stride=PROJ)
+    torch.cuda.synchronize()
+    got = to_host(core).reshape(n, H, D)
+    kw = widen_host(O, to_host(cache.k8).reshape(KV, max_ctx, D),
+                    to_host(cache.k_scale).reshape(KV, max_ctx)).reshape(-1)
+    vw = widen_host(O, to_host(cache.v8).reshape(KV, max_ctx, D),
+                    to_host(cache.v_scale).reshape(KV, max_ctx)).reshape(-1)
+    ref = O.prefill_f64(to_host(q), proj_h, PROJ, kw, vw, 0, max_ctx, np.arange(n))
+    st = O.compare(got, ref)
+    report(f"fp8 prep_batch + prefill n={n}", st)
+    assert st["ok"], st
