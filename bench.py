@@ -571,10 +571,48 @@ def bench_other(torch, A, args):
                                    f"{n_tok} tokens, f16 activations (gemm_input) and f16 MFMA "
                                    f"with f32 accumulation; TFLOP/s of 2 n_tok n k",
                        "tokens": n_tok, **gemm}
+    # Row f3: one attention layer step through the engine wiring (miso_attn_layer_*), synthetic
+    # Q4_K (q, k, o) and Q6_K (v) weights of the engine's shapes.
+    gen.manual_seed(33)
+    layer = A.Layer((synthetic_q4k(torch, gen, 1, 8192, 2048)[0], "q4_k"),
+                    (synthetic_q4k(torch, gen, 1, 512, 2048)[0], "q4_k"),
+                    (synthetic_q6k(torch, gen, 1, 512, 2048)[0], "q6_k"),
+                    (synthetic_q4k(torch, gen, 1, 2048, 4096)[0], "q4_k"),
+                    torch.ones(2048, device="cuda"), torch.ones(D, device="cuda"),
+                    torch.ones(D, device="cuda"),
+                    (1e7 ** (-torch.arange(32, device="cuda") / 32.0)).float())
+    lws = A.LayerWorkspace(4096)
+    Ld = 32768
+    lk = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
+    lv = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
+    h = torch.randn(2048, generator=gen, device="cuda")
+    dl = torch.randn(2048, generator=gen, device="cuda") * 0.1
+    y = torch.empty(2048, device="cuda")
+    g = graph_of(torch, lambda _: A.layer_decode(layer, lk, lv, Ld, Ld - 1, h, dl, y, 1e-6, lws),
+                 1)
+    time_replays(torch, g, 2)
+    tl = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1] / 20
+    ntk, p0 = 4096, 8192
+    hp = torch.randn(ntk * 2048, generator=gen, device="cuda")
+    yp = torch.empty(ntk * 2048, device="cuda")
+    g = graph_of(torch, lambda _: A.layer_prefill(layer, lk, lv, Ld, p0, ntk, hp, None, yp, 1e-6,
+                                                  lws), 1)
+    time_replays(torch, g, 1)
+    tp = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / 3
+    out["F3_layer"] = {"workload": "one attention layer step through the engine wiring "
+                                   "(miso_attn_layer_decode / _prefill): residual + RMSNorm, "
+                                   "q/k/v projections, prep, attention, output projection; "
+                                   "synthetic Q4_K / Q6_K weights of the engine's shapes",
+                       "decode_ctx": Ld, "decode_us_per_step": round(tl * 1e3, 2),
+                       "prefill_tokens": ntk, "prefill_pos0": p0,
+                       "prefill_ms_per_chunk": round(tp, 3)}
+    del layer, lws, lk, lv, hp, yp
     log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
         f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
         f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, "
-        f"C4 fp8 {out.get('C4_fp8', {}).get('tflops')} TFLOP/s, q4k gemv "
+        f"C4 fp8 {out.get('C4_fp8', {}).get('tflops')} TFLOP/s, layer decode "
+        f"{out['F3_layer']['decode_us_per_step']} us, layer prefill chunk "
+        f"{out['F3_layer']['prefill_ms_per_chunk']} ms, q4k gemv "
         + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
                     for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
         + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "
