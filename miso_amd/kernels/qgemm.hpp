@@ -26,8 +26,9 @@
 //         is one MFMA whose result the lane scales by d sc (d sc / 16 for the high set).
 // LDS tiles are double-buffered by stage (one barrier per stage) and their 16-byte chunks are
 // XOR-swizzled by row, so the 32 rows an MFMA operand read touches spread over the banks.
-// Workgroups are mapped to tiles so that the token tiles of one row tile run on the same XCD
-// (weights are read from HBM once and shared through that XCD's L2).
+// Workgroups are mapped to tiles in groups of 8 token tiles swept across the row tiles, each XCD
+// a contiguous part of that order, so an XCD's activations and weights are read from the memory
+// side about once and reused through its L2.
 
 #include <hip/hip_runtime.h>
 
@@ -293,12 +294,29 @@ __device__ __attribute__((always_inline)) inline float16_t mfma(half8_t a, half8
 }
 
 // Tile index for workgroup b of a launch of `count` workgroups: workgroups are dealt round-robin
-// to the 8 XCDs, so XCD x's workgroups b = x, x + 8, ... take the contiguous tile range
-// [x q + min(x, r), ...) (q = count / 8, r = count % 8) -- consecutive tiles, token tile fastest,
-// share one row tile.
+// to the 8 XCDs, so XCD x's workgroups b = x, x + 8, ... take the contiguous range
+// [x q + min(x, r), ...) (q = count / 8, r = count % 8) of the tile order below.
 __device__ __attribute__((always_inline)) inline unsigned xcd_tile(unsigned b, unsigned count) {
   const unsigned q = count / 8, r = count % 8, x = b % 8;
   return x * q + (x < r ? x : r) + b / 8;
+}
+
+// The tile order: groups of kGroupTok token tiles, and inside a group the row tiles in order, the
+// group's token tiles fastest. The ~64 workgroups an XCD runs at once then cover 8 token tiles x 8
+// row tiles, and a group's activations (8 x 64 tokens x k f16: 2 MiB at k = 2048) stay in that
+// XCD's L2 while its row tiles pass -- each XCD reads its activations once and each weight row
+// once per group, where a row tile swept across all token tiles would re-read the whole activation
+// matrix from the memory side for every row tile.
+constexpr unsigned kGroupTok = 8;
+__device__ __attribute__((always_inline)) inline void grouped_tile(unsigned t, unsigned n_ttiles,
+                                                                  unsigned n_rtiles,
+                                                                  unsigned& ttile,
+                                                                  unsigned& rtile) {
+  const unsigned per_group = kGroupTok * n_rtiles;
+  const unsigned first_tok = t / per_group * kGroupTok, in = t % per_group;
+  const unsigned width = n_ttiles - first_tok < kGroupTok ? n_ttiles - first_tok : kGroupTok;
+  ttile = first_tok + in % width;
+  rtile = in / width;
 }
 
 }  // namespace qgemm_detail
@@ -375,15 +393,17 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const QGemmParam
 
 }  // namespace qgemm_detail
 
-// Output tiles [first, first + count) of 64 tokens x 64 rows, token tiles fastest.
+// Output tiles [first, first + count) of 64 tokens x 64 rows, in grouped_tile's order.
 template <QFormat F>
 __device__ void qgemm_op(const QGemmParams& p, unsigned first, unsigned count) {
   using namespace qgemm_detail;
   __shared__ Lds sm;
-  const unsigned n_ttiles = (p.n_tok + kBM - 1) / kBM;
+  const unsigned n_ttiles = (p.n_tok + kBM - 1) / kBM, n_rtiles = (p.n_rows + kBN - 1) / kBN;
   for (unsigned i = blockIdx.x; i < count; i += gridDim.x) {
     const unsigned tile = first + (gridDim.x == count ? xcd_tile(i, count) : i);
-    const unsigned m0 = tile % n_ttiles * kBM, n0 = tile / n_ttiles * kBN;
+    unsigned ttile, rtile;
+    grouped_tile(tile, n_ttiles, n_rtiles, ttile, rtile);
+    const unsigned m0 = ttile * kBM, n0 = rtile * kBN;
     gemm_tile<F, 0>(p, sm, m0, n0);
     __syncthreads();  // the next tile's first stores reuse buffer 0
   }
