@@ -1000,16 +1000,24 @@ struct TileSoftmax {
 };
 
 // Per-lane constants of the pair columns: the join weights (hi lanes 1 and 2^-11 for their own
-// and the partner's accumulator, lo lanes the reverse) and the numerator split r = f16(hi nsb +
-// p sa), which is hi = f16(p) in the hi lanes (sa = 1, nsb = 0) and the lo half f16((p - hi)
-// 2^11) in the lo lanes (sa = 2^11, nsb = -2^11): one expression, no select.
+// and the partner's accumulator, lo lanes the reverse) and the split of a value x with hi =
+// f16(x) into this lane's half r = f16(hi a + x b): hi itself in the hi lanes (a = 1, b = 0: hi 1
+// + 0 is exact, so the hi lanes return the very value the lo lanes subtract, however the compiler
+// rounded it), the lo half f16((x - hi) 2^11) in the lo lanes (a = -2^11, b = 2^11): one
+// expression, no select.
 struct TileLane {
-  float w_own, w_other, sa, nsb;
+  float w_own, w_other, a, b;
 };
 __device__ __attribute__((always_inline)) inline TileLane tile_lane(unsigned lane) {
   const bool is_hi = (lane & 15u) < 8;
   return is_hi ? TileLane{1.0f, kLoWeight, 1.0f, 0.0f}
-               : TileLane{kLoWeight, 1.0f, kLoScale, -kLoScale};
+               : TileLane{kLoWeight, 1.0f, -kLoScale, kLoScale};
+}
+
+// This lane's half of the pair of x, given hi = f16(x).
+__device__ __attribute__((always_inline)) inline _Float16 pair_half(_Float16 hi, float x,
+                                                                   const TileLane& tl) {
+  return static_cast<_Float16>(__builtin_fmaf(static_cast<float>(hi), tl.a, x * tl.b));
 }
 
 // max(a, b) and max(a, b, c) without canonicalising the inputs (scores are never NaN).
@@ -1089,9 +1097,8 @@ __device__ __attribute__((always_inline)) inline void tile_numerators(TileSoftma
       p1 *= vr[i + 1];
     }
     const cdna4::half2_t h{static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
-    ph[i] = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[0]), tl.nsb, p0 * tl.sa));
-    ph[i + 1] =
-        static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[1]), tl.nsb, p1 * tl.sa));
+    ph[i] = pair_half(h[0], p0, tl);
+    ph[i + 1] = pair_half(h[1], p1, tl);
   }
   sm.lt = lt;
   sm.pb = cdna4::half8_t{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
@@ -1233,7 +1240,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
     wait_tiles_after(n_tiles - 1 < 2 ? n_tiles - 1 : 2);  // tile 0 and the queries landed
     tile_barrier();
     // Query pairs: head c % 8, dimensions 8 (4 s + g) .. + 7, x log2(e)/16 (1/sqrt(256) in
-    // log2 units), hi half in columns 0-7, lo half in columns 8-15.
+    // log2 units), hi half in columns 0-7, lo half in columns 8-15 (pair_half's split).
     const float* qrow = sh.q[c & 7u];
     constexpr float kScale = kLog2e / 16.0f;
 #pragma unroll
@@ -1245,9 +1252,7 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float v = xs[j] * kScale;
-        const _Float16 hi = static_cast<_Float16>(v);
-        const _Float16 lo = static_cast<_Float16>((v - static_cast<float>(hi)) * kLoScale);
-        hv[j] = c < 8 ? hi : lo;
+        hv[j] = pair_half(static_cast<_Float16>(v), v, tln);
       }
       st.q[s] = half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
     }
