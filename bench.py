@@ -378,15 +378,23 @@ def bench_other(torch, A, args):
     k = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
     v = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
     core = torch.empty(n3 * H * D, device="cuda")
-    g = graph_of(torch, lambda i: A.attn_prefill(q, qg, k, v, core, 0, n3, n3), 1)
-    time_replays(torch, g, 2)
-    ms = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1]
-    t3 = ms / 20
     flop3 = 4.0 * H * D * (n3 * (n3 + 1) // 2)
-    out["C3"] = {"workload": "causal prefill, 2048 tokens, empty cache",
-                 "ms_per_call": round(t3, 4), "tflops": round(flop3 / (t3 * 1e-3) / 1e12, 1),
-                 "frac": round(flop3 / (t3 * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
-    del q, qg, k, v, core
+    # Ten calls per graph (one call per replay is bound by the replay launch, ~89 us here), the
+    # balanced form (miso_attn_prefill_ws) and the one-workgroup-per-block form side by side.
+    scratch = A.PrefillScratch(n3)
+    t3 = {}
+    for form, sc in (("balanced", scratch), ("one_block", None)):
+        g = graph_of(torch, lambda i: A.attn_prefill(q, qg, k, v, core, 0, n3, n3, scratch=sc), 10)
+        time_replays(torch, g, 1)
+        t3[form] = sorted(time_replays(torch, g, 2)[0] for _ in range(3))[1] / 20
+        del g
+    out["C3"] = {"workload": "causal prefill, 2048 tokens, empty cache (balanced form)",
+                 "ms_per_call": round(t3["balanced"], 4),
+                 "tflops": round(flop3 / (t3["balanced"] * 1e-3) / 1e12, 1),
+                 "frac": round(flop3 / (t3["balanced"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                 "one_block_ms_per_call": round(t3["one_block"], 4),
+                 "one_block_tflops": round(flop3 / (t3["one_block"] * 1e-3) / 1e12, 1)}
+    del q, qg, k, v, core, scratch
     # C5: ragged decode, 64 sequences, lengths uniform in [1024, 16384] (numpy, seed 64).
     lens = np.random.default_rng(64).integers(1024, 16385, 64).astype(np.int64)
     offs = np.zeros(64, dtype=np.int64)

@@ -144,6 +144,24 @@ int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
                       const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
                       uint32_t max_ctx, uint32_t qg_stride, void* stream);
 
+/* Balanced causal prefill (no reference counterpart: the reference launches one workgroup per
+ * 16-token block, kernels/attention_prefill.hpp:42-161, so under the causal mask the last block
+ * sets the time). Same arguments, contract and output as miso_attn_prefill (within the prefill
+ * tolerance, not bitwise: the heavy blocks' keys are summed in two parts; bit-equal from call to
+ * call). For n <= 2048 token block B-1-j of the n / 16 blocks is paired with block j and the
+ * pair's tiles are shared by two workgroups (at most 256, one per CU); the two parts of a split
+ * block meet in `workspace`: miso_attn_prefill_workspace_bytes(n) bytes of device memory,
+ * 16-byte aligned, zero-filled once before its first use (every call leaves it reusable; one
+ * workspace of miso_attn_prefill_workspace_bytes(2048) bytes serves every n). Calls that overlap
+ * on one workspace race. For larger n it runs miso_attn_prefill and the workspace is not used
+ * (miso_attn_prefill_workspace_bytes returns 0). Rejects what miso_attn_prefill rejects and, for
+ * n <= 2048, a NULL or misaligned workspace or one smaller than required. */
+uint64_t miso_attn_prefill_workspace_bytes(uint32_t n);
+int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cache,
+                         const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
+                         uint32_t max_ctx, uint32_t qg_stride, void* workspace,
+                         uint64_t workspace_bytes, void* stream);
+
 /* Ragged batched decode (no reference counterpart: the reference is batch-1,
  * docs/decisions/ADR_002-build-scope-numerics-ops.md:14-18). batch sequences, one new token each:
  * q [batch][16][256] (unscaled), gate [batch][16][256], core [batch][16][256] = per-sequence

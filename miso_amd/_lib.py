@@ -30,6 +30,9 @@ SIGNATURES = {
     "miso_attn_decode_f16q": (c_int, [P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_decode_noalloc": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_prefill": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P]),
+    "miso_attn_prefill_workspace_bytes": (c_uint64, [c_uint32]),
+    "miso_attn_prefill_ws": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P,
+                                     c_uint64, P]),
     "miso_attn_ragged_splits": (c_uint32, [c_uint32]),
     "miso_attn_ragged_partials": (c_uint64, [c_uint32, c_uint32]),
     "miso_attn_decode_ragged": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, P, P, P, P, P]),

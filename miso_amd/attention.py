@@ -173,17 +173,38 @@ def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: i
     return n_splits
 
 
+def prefill_workspace_bytes(n: int) -> int:
+    return int(_lib.load().miso_attn_prefill_workspace_bytes(n))
+
+
+class PrefillScratch:
+    """Workspace of the balanced prefill (miso_attn_prefill_ws) for launches of up to max_n
+    tokens (the form covers n <= 2048), zero-filled once; every call leaves it reusable."""
+
+    def __init__(self, max_n: int = 2048, device="cuda"):
+        nbytes = prefill_workspace_bytes(min(max_n, 2048))
+        self.buf = torch.zeros(max((nbytes + 3) // 4, 4), dtype=torch.int32, device=device)
+        self.nbytes = self.buf.numel() * 4
+
+
 def attn_prefill(q, qg, k_cache, v_cache, core, pos0: int, n: int, max_ctx: int,
-                 qg_stride: int = QG_STRIDE, stream=None) -> None:
+                 qg_stride: int = QG_STRIDE, stream=None, scratch: PrefillScratch = None) -> None:
+    """Causal prefill of tokens pos0 .. pos0 + n - 1; with `scratch`, the balanced form
+    (miso_attn_prefill_ws)."""
     f32 = torch.float32
     _need(q, "q", f32, n * Q_HEADS * DIM)
     _need(qg, "qg", f32, (n - 1) * qg_stride + Q_HEADS * 2 * DIM if n else 0)
     _need(k_cache, "k_cache", _cache_dtype(k_cache), KV_HEADS * max_ctx * DIM)
     _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
     _need(core, "core", f32, n * Q_HEADS * DIM)
-    _lib.check(_lib.load().miso_attn_prefill(
-        _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), pos0, n, max_ctx, qg_stride,
-        _stream(stream)))
+    if scratch is None:
+        _lib.check(_lib.load().miso_attn_prefill(
+            _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), pos0, n, max_ctx,
+            qg_stride, _stream(stream)))
+    else:
+        _lib.check(_lib.load().miso_attn_prefill_ws(
+            _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), pos0, n, max_ctx,
+            qg_stride, _ptr(scratch.buf), scratch.nbytes, _stream(stream)))
 
 
 def ragged_partials(batch: int, max_len: int) -> int:

@@ -296,21 +296,62 @@ int miso_attn_decode_noalloc(const float* q, const float* qg, const uint16_t* k_
                           n_splits, stream);
 }
 
+// The argument checks of the prefill entry points (0 if the arguments are good).
+static int prefill_args(const char* fn, const float* q, const float* qg, const uint16_t* k_cache,
+                        const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
+                        uint32_t max_ctx, uint32_t qg_stride) {
+  if (any_bad(q, qg, k_cache, v_cache, core))
+    return fail(fn, kBadPtr);
+  if (n == 0)
+    return fail(fn, "n must be >= 1");
+  if (static_cast<uint64_t>(pos0) + n > max_ctx)
+    return fail(fn, "KV cache is full (pos0 + n > max_ctx)");
+  if (qg_stride < 8192 || qg_stride % 4 != 0)
+    return fail(fn, "qg_stride must be >= 8192 and a multiple of 4");
+  return 0;
+}
+
 int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
                       const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
                       uint32_t max_ctx, uint32_t qg_stride, void* stream) {
-  if (any_bad(q, qg, k_cache, v_cache, core))
-    return fail("miso_attn_prefill", kBadPtr);
-  if (n == 0)
-    return fail("miso_attn_prefill", "n must be >= 1");
-  if (static_cast<uint64_t>(pos0) + n > max_ctx)
-    return fail("miso_attn_prefill", "KV cache is full (pos0 + n > max_ctx)");
-  if (qg_stride < 8192 || qg_stride % 4 != 0)
-    return fail("miso_attn_prefill", "qg_stride must be >= 8192 and a multiple of 4");
+  if (const int rc = prefill_args("miso_attn_prefill", q, qg, k_cache, v_cache, core, pos0, n,
+                                  max_ctx, qg_stride))
+    return rc;
   const k::AttnPrefillParams p{q,    qg, as_half(k_cache), as_half(v_cache), core, pos0,
                                n,    max_ctx, qg_stride};
   k::attn_prefill_kernel<256><<<k::attn_prefill_items(n), 256, 0, as_stream(stream)>>>(p);
   return launched("miso_attn_prefill");
+}
+
+uint64_t miso_attn_prefill_workspace_bytes(uint32_t n) {
+  return k::attn_prefill_balanced(n) ? k::attn_prefill_split_workspace_bytes(n) : 0;
+}
+
+int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cache,
+                         const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
+                         uint32_t max_ctx, uint32_t qg_stride, void* workspace,
+                         uint64_t workspace_bytes, void* stream) {
+  static const char* fn = "miso_attn_prefill_ws";
+  if (const int rc =
+          prefill_args(fn, q, qg, k_cache, v_cache, core, pos0, n, max_ctx, qg_stride))
+    return rc;
+  const k::AttnPrefillParams a{q,    qg, as_half(k_cache), as_half(v_cache), core, pos0,
+                               n,    max_ctx, qg_stride};
+  if (!k::attn_prefill_balanced(n)) {  // the one-block-per-workgroup layout
+    k::attn_prefill_kernel<256><<<k::attn_prefill_items(n), 256, 0, as_stream(stream)>>>(a);
+    return launched(fn);
+  }
+  if (bad_ptr(workspace))
+    return fail(fn, "workspace must be a non-null, 16-byte aligned device pointer");
+  if (workspace_bytes < k::attn_prefill_split_workspace_bytes(n))
+    return fail(fn, "workspace smaller than miso_attn_prefill_workspace_bytes(n)");
+  char* const ws = static_cast<char*>(workspace);
+  float* const part_ml = reinterpret_cast<float*>(ws + k::kAttnSplitCounterBytes);
+  float* const part_o = part_ml + std::size_t{k::attn_prefill_split_pairs(n)} * 2 * 128 * 2;
+  const k::AttnPrefillSplitParams p{a, part_o, part_ml, reinterpret_cast<unsigned*>(ws)};
+  k::attn_prefill_split_kernel<256><<<k::attn_prefill_split_items(n), 256, 0,
+                                      as_stream(stream)>>>(p);
+  return launched(fn);
 }
 
 uint32_t miso_attn_ragged_splits(uint32_t max_len) { return k::attn_ragged_splits(max_len); }

@@ -82,6 +82,62 @@ __host__ __device__ inline unsigned attn_prefill_items(unsigned n) {
   return 8 * ((blocks + 3) / 4);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Balanced causal prefill (no reference counterpart; the reference launches one workgroup per
+// token block). Under a causal mask block b of a launch sees ~b tiles of keys, so with one
+// workgroup per block the last block sets the time at about twice the mean. For launches of one
+// row block per wave (n < kAttnWideMin) the balanced form pairs block B-1-j with block j (their
+// tile counts sum to a near constant) and gives the pair two workgroups: A takes the heavy
+// block's first S = ceil(pair tiles / 2) tiles, B its remaining tiles and then the light block.
+// Both parts of a split block write their partial (m, l, O) to a workspace; whichever finishes
+// second (an agent-scope counter per pair) merges the other's partial into its own and stores
+// the output. Pairs whose heavy block would save fewer than kAttnSplitMinTiles tiles run
+// unsplit (A: the heavy block, B: the light one). The pairing pays while its grid fits the chip
+// at one workgroup per CU (attn_prefill_balanced: n <= 2048 on the 256 CUs of an MI355X);
+// beyond that the one-block layout's extra rounds already even out the load (measured: 3072
+// tokens after a 1024-token prefix, 175 us one-block against 202 us paired).
+// ------------------------------------------------------------------------------------------------
+
+constexpr unsigned kAttnSplitMinTiles = 4;
+constexpr unsigned kAttnBalancedMaxItems = 256;  // CUs of an MI355X
+
+// Workspace of the balanced form, for launches of n < kAttnWideMin: one counter per pair (a
+// fixed region of kAttnSplitMaxPairs, so one workspace serves every n), then (m, l) (f32
+// [slot][128 rows][2]) and O (f32 [slot][128][256]) of the two parts (slots 2 pair, 2 pair + 1)
+// of each pair. The counters must be zero before the first launch over a workspace; every launch
+// leaves them zero. Launches that overlap on one workspace race.
+struct AttnPrefillSplitParams {
+  AttnPrefillParams a;
+  float* part_o;
+  float* part_ml;
+  unsigned* counters;
+};
+
+__host__ __device__ constexpr unsigned attn_prefill_split_pairs(unsigned n) {
+  return attn::kKvHeads * (((n + kAttnQBlock - 1) / kAttnQBlock) / 2);
+}
+constexpr unsigned kAttnSplitMaxPairs = attn::kKvHeads * (kAttnWideMin / kAttnQBlock / 2);
+constexpr std::size_t kAttnSplitCounterBytes = kAttnSplitMaxPairs * sizeof(unsigned);
+
+// Grid size: per KV head one slot per pair (and one for the middle block of an odd count),
+// groups of 4 slots per XCD pair round (XCD = item % 8 as in attn_prefill_items), the two
+// workgroups of a slot in consecutive rounds on the same XCD.
+__host__ __device__ constexpr unsigned attn_prefill_split_items(unsigned n) {
+  const unsigned blocks = (n + kAttnQBlock - 1) / kAttnQBlock;
+  const unsigned slots = blocks / 2 + blocks % 2;
+  return 16 * ((slots + 3) / 4);
+}
+
+// Whether a launch of n tokens takes the balanced form.
+__host__ __device__ constexpr bool attn_prefill_balanced(unsigned n) {
+  return n > 0 && n < kAttnWideMin && attn_prefill_split_items(n) <= kAttnBalancedMaxItems;
+}
+
+__host__ __device__ constexpr std::size_t attn_prefill_split_workspace_bytes(unsigned n) {
+  return kAttnSplitCounterBytes +
+         std::size_t{attn_prefill_split_pairs(n)} * 2 * 128 * (attn::kDim + 2) * sizeof(float);
+}
+
 namespace prefill_detail {
 
 using cdna4::float16_t;
@@ -525,10 +581,69 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
 // only in the diagonal tiles of a wave; the gate and 1/l are applied at the store.
 namespace prefill_detail {
 
-template <int kBlocks>
-__device__ __attribute__((always_inline)) inline void prefill_items(const AttnPrefillParams& p,
-                                                                    unsigned first,
-                                                                    unsigned count, Shared& sh) {
+// A workgroup's run over one token block: tiles [tb, te) of its keys; `part` says the tiles are
+// one of two parts of a split block (partial to workspace slot `slot`, merge by the later part).
+struct PrefillJob {
+  unsigned kvh, blk, tb, te, slot;
+  bool part;
+};
+
+// Tiles of keys block b of kTokens tokens sees (its last token's causal limit).
+template <unsigned kTokens>
+__device__ __attribute__((always_inline)) inline unsigned block_tiles(const AttnPrefillParams& p,
+                                                                      unsigned b) {
+  return (p.pos0 + min((b + 1) * kTokens, p.n) + kKeys - 1) / kKeys;
+}
+
+// The jobs of item `item` (wave-uniform): one for the one-block-per-workgroup layout of
+// attn_prefill_items, up to two for the balanced layout of attn_prefill_split_items.
+template <unsigned kTokens, bool kSplit>
+__device__ __attribute__((always_inline)) inline unsigned item_jobs(const AttnPrefillParams& p,
+                                                                    unsigned item,
+                                                                    unsigned blocks,
+                                                                    PrefillJob (&jobs)[2]) {
+  const unsigned xcd = item % 8, kvh = xcd / 4;
+  if constexpr (!kSplit) {
+    const unsigned rank = (item / 8) * 4 + xcd % 4;
+    if (rank >= blocks)
+      return 0;
+    const unsigned blk = blocks - 1 - rank;
+    jobs[0] = PrefillJob{kvh, blk, 0, block_tiles<kTokens>(p, blk), 0, false};
+    return 1;
+  } else {
+    const unsigned role = (item / 8) % 2, pair = (item / 16) * 4 + xcd % 4;
+    const unsigned pairs = blocks / 2;
+    if (pair >= pairs) {  // the middle block of an odd count (workgroup A), or nothing
+      if (pair > pairs || blocks % 2 == 0 || role == 1)
+        return 0;
+      jobs[0] = PrefillJob{kvh, pair, 0, block_tiles<kTokens>(p, pair), 0, false};
+      return 1;
+    }
+    const unsigned hb = blocks - 1 - pair, lb = pair;
+    const unsigned th = block_tiles<kTokens>(p, hb), tl = block_tiles<kTokens>(p, lb);
+    const unsigned cut = (th + tl + 1) / 2;
+    // Tiles every row of the heavy block sees in full: the split point stays among them.
+    const unsigned full = (p.pos0 + hb * kTokens + 1) / kKeys;
+    if (cut + kAttnSplitMinTiles > th || cut > full) {
+      jobs[0] = role == 0 ? PrefillJob{kvh, hb, 0, th, 0, false}
+                          : PrefillJob{kvh, lb, 0, tl, 0, false};
+      return 1;
+    }
+    const unsigned slot = 2 * (kvh * pairs + pair) + role;
+    if (role == 0) {
+      jobs[0] = PrefillJob{kvh, hb, 0, cut, slot, true};
+      return 1;
+    }
+    jobs[0] = PrefillJob{kvh, hb, cut, th, slot, true};
+    jobs[1] = PrefillJob{kvh, lb, 0, tl, 0, false};
+    return 2;
+  }
+}
+
+template <int kBlocks, bool kSplit = false>
+__device__ __attribute__((always_inline)) inline void prefill_items(
+    const AttnPrefillParams& p, const AttnPrefillSplitParams* sp, unsigned first, unsigned count,
+    Shared& sh) {
   using attn::kDim;
   constexpr int kGroup = attn::kQHeads / attn::kKvHeads;
   constexpr unsigned kItemTokens = kAttnQBlock * kBlocks;
@@ -567,195 +682,361 @@ __device__ __attribute__((always_inline)) inline void prefill_items(const AttnPr
   }
 
   for (unsigned item = first + blockIdx.x; item < first + count; item += gridDim.x) {
-    const unsigned slot = item % 8, kvh = slot / 4;
-    const unsigned rank = (item / 8) * 4 + slot % 4;
-    if (rank >= blocks)
-      continue;  // uniform across the workgroup
-    const unsigned blk = blocks - 1 - rank;
-    const unsigned t0 = blk * kItemTokens;
-    const unsigned t_end = min(t0 + kItemTokens, p.n);
-    const unsigned kv_end = p.pos0 + t_end;
-    const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * kDim;
-    const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * kDim;
-    const unsigned tiles = (kv_end + kKeys - 1) / kKeys;
-    // Ring slots as byte offsets, rotated once per tile: tile ti is in `cur`, ti + 1 in `next`,
-    // ti + 2 goes to `spare`.
-    unsigned slot_cur = 0, slot_next = kTileBytes, slot_spare = 2 * kTileBytes;
-    auto rotate = [&]() __attribute__((always_inline)) {
-      const unsigned tmp = slot_cur;
-      slot_cur = slot_next;
-      slot_next = slot_spare;
-      slot_spare = tmp;
-    };
-    auto full_tile = [&](unsigned ti) __attribute__((always_inline)) {
-      return (ti + 1) * kKeys <= kv_end;
-    };
-    auto dest = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
-      return TileCopy{K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
-                      lds0 + slot + wave * 4096, lds0 + kVBase + slot + wave * 4096};
-    };
-    // A whole tile copy at once (the first two tiles, and the last one when it crosses kv_end).
-    auto copy = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
-      const TileCopy d = dest(ti, slot);
-      if (full_tile(ti))
-        copy_tile(d.kt, d.vt, copy_koff, copy_voff, d.k_lds, d.v_lds);
-      else
-        copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, d.k_lds - wave * 4096,
-                          d.v_lds - wave * 4096, wave, lane);
-    };
-
-    // Start streaming before anything else: tiles 0 and 1.
-    copy(0, slot_cur);
-    if (tiles > 1)
-      copy(1, slot_next);
-
-    // This wave's rows: block c, token tw + 4 c + col / 8, head kvh * 8 + col % 8.
-    const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
-    unsigned tq[2] = {0, 0}, lim[2] = {0, 0};
-    bool q_valid[2] = {false, false};
-#pragma unroll
-    for (int c = 0; c < kBlocks; ++c) {
-      const unsigned raw_t = tw + 4 * c + col / kGroup;
-      q_valid[c] = raw_t < p.n;
-      tq[c] = q_valid[c] ? raw_t : p.n - 1;
-      lim[c] = p.pos0 + tq[c];  // last visible key
-    }
-    const bool wave_active = tw < p.n;
-    // Tiles this wave needs, and how many of them every row of the wave sees in full (always
-    // fewer: the last tile of a wave is a diagonal one).
-    const unsigned wave_tiles =
-        wave_active ? (p.pos0 + min(tw + kWaveTokens - 1, p.n - 1)) / kKeys + 1 : 0;
-    const unsigned full_tiles = wave_active ? (p.pos0 + tw + 1) / kKeys : 0;
-
-    Rows2 rw;
-    rw.q1 = cdna4::lds_offset(sh.q1[wave]) + 16 * lane;
-    {
-      constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
-#pragma unroll
-      for (int c = 0; c < kBlocks; ++c) {
-        const float* src =
-            p.q + (std::size_t{tq[c]} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
-        const float z = q_valid[c] ? kScale : 0.0f;
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
-          const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
-          const half8_t v =
-              half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
-                      static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
-                      static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
-                      static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
-          if (c == 0)
-            rw.q0[st] = v;
-          else  // this wave's own region: its later reads are ordered after these writes
-            *reinterpret_cast<__attribute__((address_space(3))) half8_t*>(rw.q1 + 1024u * st) = v;
-        }
-        rw.m[c] = -__builtin_inff();
-        rw.l[c] = 0.0f;
-      }
-    }
-    float16_t oacc[kBlocks][8];
-#pragma unroll
-    for (int c = 0; c < kBlocks; ++c)
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        oacc[c][b] = float16_t{};
-
-    // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (its
-    // copy was the last one issued), every wave's by the barrier, which also says that all waves
-    // are done with tile ti - 1, whose slot then receives tile ti + 2 during the step.
-    auto sync = [&](unsigned ti) __attribute__((always_inline)) {
-      if (ti + 1 < tiles) {
-        cdna4::wait_vmcnt<0>();
-        __syncthreads();
-      }
-    };
-    // The step's copy of tile ti + 2: spread inside the step for a full tile, else at once.
-    auto next_copy = [&](unsigned ti) __attribute__((always_inline)) {
-      const bool spread = ti + 2 < tiles && full_tile(ti + 2);
-      if (ti + 2 < tiles && !spread)
-        copy(ti + 2, slot_spare);
-      return spread;
-    };
-
-    cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
-    __syncthreads();
-    // cur: the decided numerators of tile ti at the top of iteration ti (tile 0: here; O is
-    // still 0, so the first decision needs no rescale).
-    Numer cur;
-    if (wave_active) {
-      float16_t s0[kBlocks];
-      scores2<kBlocks>(rw, kb, s0);
-      bool mv;
-#pragma unroll
-      for (int c = 0; c < kBlocks; ++c) {
-        if (full_tiles > 0)
-          decide_block<false>(s0[c], rw.m[c], rw.l[c], cur.p[c], 0, lim[c], hi, mv);
+    PrefillJob jobs[2];
+    const unsigned njobs = item_jobs<kItemTokens, kSplit>(p, item, blocks, jobs);
+    for (unsigned j = 0; j < njobs; ++j) {  // uniform across the workgroup
+      const PrefillJob jb = j == 0 ? jobs[0] : jobs[1];
+      const unsigned kvh = jb.kvh, blk = jb.blk, tb = jb.tb;
+      const unsigned t0 = blk * kItemTokens;
+      const unsigned t_end = min(t0 + kItemTokens, p.n);
+      const unsigned kv_end = p.pos0 + t_end;
+      const attn::half_t* K = p.k_cache + std::size_t{kvh} * p.max_ctx * kDim;
+      const attn::half_t* V = p.v_cache + std::size_t{kvh} * p.max_ctx * kDim;
+      const unsigned tiles = jb.te;  // this job's tiles: [tb, tiles)
+      // Ring slots as byte offsets, rotated once per tile: tile ti is in `cur`, ti + 1 in `next`,
+      // ti + 2 goes to `spare`.
+      unsigned slot_cur = 0, slot_next = kTileBytes, slot_spare = 2 * kTileBytes;
+      auto rotate = [&]() __attribute__((always_inline)) {
+        const unsigned tmp = slot_cur;
+        slot_cur = slot_next;
+        slot_next = slot_spare;
+        slot_spare = tmp;
+      };
+      auto full_tile = [&](unsigned ti) __attribute__((always_inline)) {
+        return (ti + 1) * kKeys <= kv_end;
+      };
+      auto dest = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
+        return TileCopy{K + std::size_t{ti} * kKeys * kDim, V + std::size_t{ti} * kKeys * kDim,
+                        lds0 + slot + wave * 4096, lds0 + kVBase + slot + wave * 4096};
+      };
+      // A whole tile copy at once (the first two tiles, and the last one when it crosses kv_end).
+      auto copy = [&](unsigned ti, unsigned slot) __attribute__((always_inline)) {
+        const TileCopy d = dest(ti, slot);
+        if (full_tile(ti))
+          copy_tile(d.kt, d.vt, copy_koff, copy_voff, d.k_lds, d.v_lds);
         else
-          decide_block<true>(s0[c], rw.m[c], rw.l[c], cur.p[c], 0, lim[c], hi, mv);
-      }
-    }
-    // One pass over the workgroup's tiles in phases per wave, each a loop with a single body
-    // (the per-wave bounds differ; every wave still runs sync once per tile, in order): tiles
-    // whose successor the wave's rows see in full, tiles whose successor is diagonal, the last
-    // tile (no successor), then the tiles the wave does not need.
-    unsigned ti = 0;
-    auto step = [&](auto mask_next, auto has_next) __attribute__((always_inline)) {
-      sync(ti);
-      const bool spread = next_copy(ti);
-      tile_step2<kBlocks, decltype(mask_next)::value, decltype(has_next)::value>(
-          cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim, hi, spread,
-          dest(ti + 2, slot_spare), copy_koff, copy_voff);
-    };
-    using F = std::false_type;
-    using T = std::true_type;
-    for (; ti + 1 < full_tiles; ++ti, rotate())
-      step(F{}, T{});
-    for (; ti + 1 < wave_tiles; ++ti, rotate())
-      step(T{}, T{});
-    if (ti < wave_tiles) {
-      step(F{}, F{});
-      ++ti;
-      rotate();
-    }
-    for (; ti < tiles; ++ti, rotate()) {
-      sync(ti);
-      if (ti + 2 < tiles)
-        copy(ti + 2, slot_spare);
-    }
-    __syncthreads();  // the ring is reused by the next item
-    drain_pv();
+          copy_tile_clamped(K, V, ti * kKeys, kv_end - 1, d.k_lds - wave * 4096,
+                            d.v_lds - wave * 4096, wave, lane);
+      };
 
+      // Start streaming before anything else: the job's first two tiles.
+      copy(tb, slot_cur);
+      if (tiles > tb + 1)
+        copy(tb + 1, slot_next);
+
+      // This wave's rows: block c, token tw + 4 c + col / 8, head kvh * 8 + col % 8.
+      const unsigned tw = t0 + kWaveTokens * wave, hq = col % kGroup;
+      unsigned tq[2] = {0, 0}, lim[2] = {0, 0};
+      bool q_valid[2] = {false, false};
 #pragma unroll
-    for (int c = 0; c < kBlocks; ++c) {
-      // Row total: each column's keys per tile were split between the lane halves.
-      const float l_tot = cdna4::sum_xor32(rw.l[c]);
-      if (q_valid[c]) {
-        const unsigned head = kvh * kGroup + hq;
-        const float inv_l = __builtin_amdgcn_rcpf(l_tot);
-        const float* gate = p.qg + std::size_t{tq[c]} * p.qg_stride + head * 2 * kDim + kDim;
-        float* out = p.core + (std::size_t{tq[c]} * attn::kQHeads + head) * kDim;
-        // The gate loads of a 32-dimension block before its stores: the compiler cannot tell qg
-        // from core apart, so interleaved, each load would wait behind the previous store.
+      for (int c = 0; c < kBlocks; ++c) {
+        const unsigned raw_t = tw + 4 * c + col / kGroup;
+        q_valid[c] = raw_t < p.n;
+        tq[c] = q_valid[c] ? raw_t : p.n - 1;
+        lim[c] = p.pos0 + tq[c];  // last visible key
+      }
+      const bool wave_active = tw < p.n;
+      // Tiles this wave needs, and how many of them every row of the wave sees in full (always
+      // fewer: the last tile of a wave is a diagonal one).
+      const unsigned wave_tiles =
+          wave_active ? (p.pos0 + min(tw + kWaveTokens - 1, p.n - 1)) / kKeys + 1 : 0;
+      const unsigned full_tiles = wave_active ? (p.pos0 + tw + 1) / kKeys : 0;
+
+      Rows2 rw;
+      rw.q1 = cdna4::lds_offset(sh.q1[wave]) + 16 * lane;
+      constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
+      if constexpr (kBlocks == 1) {
+        // Q^T B operands: lane (col, hi) needs row col, one row per lane, which as global loads
+        // would take the address unit one lane per cycle. Instead each load moves one row (1 KiB,
+        // lane l: dimensions 4 l .. 4 l + 3), the f16 rows go to this wave's Q^T area (unused
+        // with one block: 32 rows x 512 bytes, 16-byte chunk c of row r at position c ^ (r % 16),
+        // so the writes of a row and the reads of 16 rows at one chunk hit distinct banks), and
+        // each lane reads its operands back. Rows of tokens >= n are zero (they are not stored).
+        const unsigned qa = cdna4::lds_offset(sh.q1[wave]);
+        float4 x[32];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          float4 gv[4];
+        for (int r = 0; r < 32; ++r) {
+          const unsigned tk = min(tw + r / 8, p.n - 1);
+          x[r] = *reinterpret_cast<const float4*>(
+              p.q + (std::size_t{tk} * attn::kQHeads + kvh * kGroup + r % 8) * kDim + 4 * lane);
+        }
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4)
-            gv[r4] = *reinterpret_cast<const float4*>(gate + 32 * b + 8 * r4 + 4 * hi);
+        for (int r = 0; r < 32; ++r) {
+          const float z = tw + r / 8 < p.n ? kScale : 0.0f;
+          const half4_t h = {static_cast<_Float16>(x[r].x * z), static_cast<_Float16>(x[r].y * z),
+                             static_cast<_Float16>(x[r].z * z), static_cast<_Float16>(x[r].w * z)};
+          *reinterpret_cast<__attribute__((address_space(3))) half4_t*>(
+              qa + 512 * r + 16 * ((lane / 2) ^ (r & 15)) + 8 * (lane & 1)) = h;
+        }
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+          rw.q0[st] = *reinterpret_cast<const __attribute__((address_space(3))) half8_t*>(
+              qa + 512 * col + 16 * ((2 * st + hi) ^ (col & 15)));
+        rw.m[0] = -__builtin_inff();
+        rw.l[0] = 0.0f;
+      } else {
+#pragma unroll
+        for (int c = 0; c < kBlocks; ++c) {
+          const float* src =
+              p.q + (std::size_t{tq[c]} * attn::kQHeads + kvh * kGroup + hq) * kDim + 8 * hi;
+          const float z = q_valid[c] ? kScale : 0.0f;
+#pragma unroll
+          for (int st = 0; st < 16; ++st) {
+            const float4 x0 = *reinterpret_cast<const float4*>(src + 16 * st);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
+            const half8_t v =
+                half8_t{static_cast<_Float16>(x0.x * z), static_cast<_Float16>(x0.y * z),
+                        static_cast<_Float16>(x0.z * z), static_cast<_Float16>(x0.w * z),
+                        static_cast<_Float16>(x1.x * z), static_cast<_Float16>(x1.y * z),
+                        static_cast<_Float16>(x1.z * z), static_cast<_Float16>(x1.w * z)};
+            if (c == 0)
+              rw.q0[st] = v;
+            else  // this wave's own region: its later reads are ordered after these writes
+              *reinterpret_cast<__attribute__((address_space(3))) half8_t*>(rw.q1 + 1024u * st) =
+                  v;
+          }
+          rw.m[c] = -__builtin_inff();
+          rw.l[c] = 0.0f;
+        }
+      }
+      float16_t oacc[kBlocks][8];
+#pragma unroll
+      for (int c = 0; c < kBlocks; ++c)
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          oacc[c][b] = float16_t{};
+
+      // Start of iteration ti: tile ti + 1 complete in LDS -- this wave's share by vmcnt (its
+      // copy was the last one issued), every wave's by the barrier, which also says that all waves
+      // are done with tile ti - 1, whose slot then receives tile ti + 2 during the step.
+      auto sync = [&](unsigned ti) __attribute__((always_inline)) {
+        if (ti + 1 < tiles) {
+          cdna4::wait_vmcnt<0>();
+          __syncthreads();
+        }
+      };
+      // The step's copy of tile ti + 2: spread inside the step for a full tile, else at once.
+      auto next_copy = [&](unsigned ti) __attribute__((always_inline)) {
+        const bool spread = ti + 2 < tiles && full_tile(ti + 2);
+        if (ti + 2 < tiles && !spread)
+          copy(ti + 2, slot_spare);
+        return spread;
+      };
+
+      cdna4::wait_vmcnt<0>();  // tiles 0 (and 1) and the queries are in
+      __syncthreads();
+      // cur: the decided numerators of tile ti at the top of iteration ti (tile 0: here; O is
+      // still 0, so the first decision needs no rescale).
+      Numer cur;
+      if (wave_active) {
+        float16_t s0[kBlocks];
+        scores2<kBlocks>(rw, kb, s0);
+        bool mv;
+#pragma unroll
+        for (int c = 0; c < kBlocks; ++c) {
+          if (full_tiles > tb)
+            decide_block<false>(s0[c], rw.m[c], rw.l[c], cur.p[c], tb * kKeys, lim[c], hi, mv);
+          else
+            decide_block<true>(s0[c], rw.m[c], rw.l[c], cur.p[c], tb * kKeys, lim[c], hi, mv);
+        }
+      }
+      // One pass over the workgroup's tiles in phases per wave, each a loop with a single body
+      // (the per-wave bounds differ; every wave still runs sync once per tile, in order): tiles
+      // whose successor the wave's rows see in full, tiles whose successor is diagonal, the last
+      // tile (no successor), then the tiles the wave does not need.
+      unsigned ti = tb;
+      auto step = [&](auto mask_next, auto has_next) __attribute__((always_inline)) {
+        sync(ti);
+        const bool spread = next_copy(ti);
+        tile_step2<kBlocks, decltype(mask_next)::value, decltype(has_next)::value>(
+            cur, rw, oacc, kb, slot_next, vb, slot_cur, (ti + 1) * kKeys, lim, hi, spread,
+            dest(ti + 2, slot_spare), copy_koff, copy_voff);
+      };
+      using F = std::false_type;
+      using T = std::true_type;
+      const unsigned full_end = min(full_tiles, tiles), wave_end = min(wave_tiles, tiles);
+      for (; ti + 1 < full_end; ++ti, rotate())
+        step(F{}, T{});
+      for (; ti + 1 < wave_end; ++ti, rotate())
+        step(T{}, T{});
+      if (ti < wave_end) {
+        step(F{}, F{});
+        ++ti;
+        rotate();
+      }
+      for (; ti < tiles; ++ti, rotate()) {
+        sync(ti);
+        if (ti + 2 < tiles)
+          copy(ti + 2, slot_spare);
+      }
+      __syncthreads();  // the ring is reused by the next item
+      drain_pv();
+
+      // Output: core = O / l * sigmoid(gate). In the accumulator layout a lane holds one row
+      // (its column), so a global access of a wave would touch 32 rows 1 KiB apart, 16 bytes
+      // each, and the address unit handles such an access one lane per cycle. O / l therefore
+      // goes through this wave's LDS (the ring and the Q^T area are free after the barrier
+      // above): row r at byte kStageRow r, padded by one 16-byte chunk so the 16 lanes of a write
+      // (16 rows, one chunk) and of a read (one row, 16 chunks) hit distinct banks; every address
+      // is one register plus an immediate. Then each gate load and core store moves one whole
+      // row (1 KiB, lane l: dimensions 4 l .. 4 l + 3).
+      constexpr unsigned kStageRow = 1024 + 16;
+      static_assert(4 * 32 * kStageRow <= sizeof(Shared));
+      const unsigned stage = lds0 + wave * 32 * kStageRow;
+      auto stage_o = [&](int c, float f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
-            const unsigned d0 = 32 * b + 8 * r4 + 4 * hi;
-            const float4 g = gv[r4];
-            float4 o;
-            o.x = oacc[c][b][4 * r4 + 0] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
-            o.y = oacc[c][b][4 * r4 + 1] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.y));
-            o.z = oacc[c][b][4 * r4 + 2] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.z));
-            o.w = oacc[c][b][4 * r4 + 3] * inv_l * __builtin_amdgcn_rcpf(1.0f + __expf(-g.w));
-            *reinterpret_cast<float4*>(out + d0) = o;
+            const unsigned k = 8 * b + 2 * r4 + hi;
+            const cdna4::float4_t o = {oacc[c][b][4 * r4 + 0] * f, oacc[c][b][4 * r4 + 1] * f,
+                                       oacc[c][b][4 * r4 + 2] * f, oacc[c][b][4 * r4 + 3] * f};
+            *reinterpret_cast<__attribute__((address_space(3))) cdna4::float4_t*>(
+                stage + kStageRow * col + 16 * k) = o;
+          }
+      };
+      auto staged_row = [&](int r) __attribute__((always_inline)) {
+        return *reinterpret_cast<const __attribute__((address_space(3))) cdna4::float4_t*>(
+            stage + kStageRow * r + 16 * lane);
+      };
+      // Row total: each column's keys per tile were split between the lane halves.
+      float l_row[kBlocks];
+#pragma unroll
+      for (int c = 0; c < kBlocks; ++c)
+        l_row[c] = cdna4::sum_xor32(rw.l[c]);
+      // A part of a split block: its partial to the workspace (rows of O relative to 2^m, and
+      // (m, l) per row), then the agent-scope counter of the pair; the part that arrives second
+      // merges. Merged rows: O = O_A f_A + O_B f_B, f_X = 2^(m_X - M) / (l_A 2^(m_A - M) +
+      // l_B 2^(m_B - M)), M the larger m, evaluated in this order whichever part merges (the
+      // output does not depend on which part arrives second).
+      //
+      // The partials move with agent-coherent buffer accesses (cache policy sc1, what a relaxed
+      // agent-scope atomic access compiles to on gfx950): they are not left dirty in, nor read
+      // stale from, an XCD's L2. Each wave waits for its partial stores to complete, the
+      // barrier orders them before thread 0's counter increment, and the merging part's loads
+      // are issued after it has read the count. An agent-scope release fence would instead write
+      // back every dirty line of the L2 (the other workgroups' output included), which stalls
+      // the XCD for microseconds.
+      bool store = true, merge = false;
+      float f_a = 0.0f, f_b = 0.0f;
+      bool own_a = true;
+      unsigned oth_off = 0;  // byte offset of the other part's rows (this wave's first)
+      constexpr int kSc1 = 16;  // cache-policy operand of the buffer builtins: sc1
+      const auto part_rsrc = [&](float* base, unsigned floats) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(4 * floats),
+                                                 0x00020000);
+      };
+      const unsigned slots = 2 * attn_prefill_split_pairs(p.n);
+      if constexpr (kSplit) {
+        static_assert(kBlocks == 1, "the balanced form runs one row block per wave");
+        if (jb.part) {
+          const auto o_rsrc = part_rsrc(sp->part_o, slots * 128 * kDim);
+          const auto ml_rsrc = part_rsrc(sp->part_ml, slots * 128 * 2);
+          const unsigned row0 = jb.slot * 128 + 32 * wave;
+          stage_o(0, 1.0f);
+          if (hi == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                __builtin_bit_cast(cdna4::u32x2_t, float2{rw.m[0], l_row[0]}), ml_rsrc,
+                (row0 + col) * 8, 0, kSc1);
+#pragma unroll
+          for (int r = 0; r < 32; ++r)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(cdna4::u32x4_t, staged_row(r)), o_rsrc,
+                (row0 + r) * 1024 + 16 * lane, 0, kSc1);
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+          const unsigned flag = lds0 + 4 * 32 * kStageRow;  // past every wave's staging
+          unsigned* counter = sp->counters + jb.slot / 2;
+          if (t == 0)
+            *reinterpret_cast<__attribute__((address_space(3))) unsigned*>(flag) =
+                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __syncthreads();
+          store = *reinterpret_cast<const __attribute__((address_space(3))) unsigned*>(flag) != 0;
+          if (store) {  // uniform: the other part's partial is complete
+            if (t == 0)  // every launch leaves the counters zero
+              __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned orow0 = (jb.slot ^ 1u) * 128 + 32 * wave;
+            const float2 oml = __builtin_bit_cast(
+                float2, __builtin_amdgcn_raw_buffer_load_b64(ml_rsrc, (orow0 + col) * 8, 0, kSc1));
+            own_a = (jb.slot & 1u) == 0;
+            const float m_a = own_a ? rw.m[0] : oml.x, m_b = own_a ? oml.x : rw.m[0];
+            const float l_a = own_a ? l_row[0] : oml.y, l_b = own_a ? oml.y : l_row[0];
+            const float m_max = fmaxf(m_a, m_b);
+            const float e_a = __builtin_amdgcn_exp2f(m_a - m_max);
+            const float e_b = __builtin_amdgcn_exp2f(m_b - m_max);
+            const float inv_l = __builtin_amdgcn_rcpf(l_a * e_a + l_b * e_b);
+            f_a = e_a * inv_l;
+            f_b = e_b * inv_l;
+            merge = true;
+            oth_off = orow0 * 1024 + 16 * lane;
           }
         }
       }
+      if (store) {
+#pragma unroll
+        for (int c = 0; c < kBlocks; ++c) {
+          if (!merge)  // a merging part's raw O is still staged from its partial
+            stage_o(c, __builtin_amdgcn_rcpf(l_row[c]));
+          // Rows 8 j + h of the block: token tw + 4 c + j, head kvh * 8 + h; tokens >= n are not
+          // stored (their gate loads read token n - 1).
+          const unsigned tok0 = tw + 4 * c;
+          const float* gate = p.qg + std::size_t{kvh} * kGroup * 2 * kDim + kDim + 4 * lane;
+          float* out = p.core + std::size_t{kvh} * kGroup * kDim + 4 * lane;
+          // Rows in flight: all 32 of the block with one block of O in the AGPRs; with two, or
+          // with the other part's rows to add, 16 at a time (the loads of the second half then
+          // wait behind the stores of the first).
+          constexpr int kGateRows = kBlocks == 1 && !kSplit ? 32 : 16;
+#pragma unroll
+          for (int r0 = 0; r0 < 32; r0 += kGateRows) {
+            float4 gv[kGateRows], ov[kSplit ? kGateRows : 1];
+#pragma unroll
+            for (int r = r0; r < r0 + kGateRows; ++r) {
+              const unsigned tk = min(tok0 + r / 8, p.n - 1);
+              gv[r - r0] = *reinterpret_cast<const float4*>(gate + std::size_t{tk} * p.qg_stride +
+                                                            (r % 8) * 2 * kDim);
+            }
+            if constexpr (kSplit)
+              if (merge) {
+                const auto o_rsrc = part_rsrc(sp->part_o, slots * 128 * kDim);
+#pragma unroll
+                for (int r = r0; r < r0 + kGateRows; ++r)
+                  ov[r - r0] = __builtin_bit_cast(
+                      float4, __builtin_amdgcn_raw_buffer_load_b128(o_rsrc, oth_off + r * 1024,
+                                                                    0, kSc1));
+              }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = r0; r < r0 + kGateRows; ++r) {
+              cdna4::float4_t v = staged_row(r);
+              if constexpr (kSplit)
+                if (merge) {  // row r's factors from lane r (column r)
+                  const float fa = __builtin_bit_cast(
+                      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f_a), r));
+                  const float fb = __builtin_bit_cast(
+                      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f_b), r));
+                  const cdna4::float4_t w = {ov[r - r0].x, ov[r - r0].y, ov[r - r0].z,
+                                             ov[r - r0].w};
+                  const cdna4::float4_t oa = own_a ? v : w, ob = own_a ? w : v;
+                  v = cdna4::float4_t{__builtin_fmaf(ob[0], fb, oa[0] * fa),
+                                      __builtin_fmaf(ob[1], fb, oa[1] * fa),
+                                      __builtin_fmaf(ob[2], fb, oa[2] * fa),
+                                      __builtin_fmaf(ob[3], fb, oa[3] * fa)};
+                }
+              const float4 g = gv[r - r0];
+              float4 o;
+              o.x = v[0] * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
+              o.y = v[1] * __builtin_amdgcn_rcpf(1.0f + __expf(-g.y));
+              o.z = v[2] * __builtin_amdgcn_rcpf(1.0f + __expf(-g.z));
+              o.w = v[3] * __builtin_amdgcn_rcpf(1.0f + __expf(-g.w));
+              if (tok0 + r / 8 < p.n)  // uniform
+                *reinterpret_cast<float4*>(out + (std::size_t{tok0 + r / 8} * attn::kQHeads +
+                                                  r % 8) * kDim) = o;
+            }
+          }
+        }
+      }
+      if (j + 1 < njobs || item + gridDim.x < first + count)
+        __syncthreads();  // the next job's copies overwrite the staging
     }
   }
 }
@@ -767,14 +1048,22 @@ __device__ void attn_prefill_op(const AttnPrefillParams& p, unsigned first, unsi
   static_assert(kBlock == 256, "four waves per prefill workgroup");
   __shared__ prefill_detail::Shared sh;
   if (attn_prefill_row_blocks(p.n) == 2)  // uniform: the item size follows n
-    prefill_detail::prefill_items<2>(p, first, count, sh);
+    prefill_detail::prefill_items<2>(p, nullptr, first, count, sh);
   else
-    prefill_detail::prefill_items<1>(p, first, count, sh);
+    prefill_detail::prefill_items<1>(p, nullptr, first, count, sh);
 }
 
 template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_prefill_kernel(AttnPrefillParams p) {
   attn_prefill_op<kBlock>(p, 0, attn_prefill_items(p.n));
+}
+
+// The balanced form (attn_prefill_split_items(n) workgroups of 256; attn_prefill_balanced(n)).
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) attn_prefill_split_kernel(AttnPrefillSplitParams p) {
+  static_assert(kBlock == 256, "four waves per prefill workgroup");
+  __shared__ prefill_detail::Shared sh;
+  prefill_detail::prefill_items<1, true>(p.a, &p, 0, attn_prefill_split_items(p.a.n), sh);
 }
 
 }  // namespace miso::kernels

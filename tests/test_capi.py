@@ -68,6 +68,17 @@ def test_host_validation_rejects_bad_arguments(lib):
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 8, 3, 10, 8192, N), lib, "KV cache is full")
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 3, 10, 100, N), lib, "qg_stride")
     rejected(lib.miso_attn_prefill(P, P, P, P, P, 0, 3, 10, 8194, N), lib, "multiple of 4")
+    W = 1 << 20
+    rejected(lib.miso_attn_prefill_ws(P, P, P, P, P, 0, 0, 10, 8192, P, W, N), lib,
+             "n must be >= 1")
+    rejected(lib.miso_attn_prefill_ws(P, P, P, P, P, 8, 3, 10, 8192, P, W, N), lib,
+             "KV cache is full")
+    rejected(lib.miso_attn_prefill_ws(P, P, P, P, P, 0, 3, 10, 8192, N, W, N), lib, "workspace")
+    rejected(lib.miso_attn_prefill_ws(P, P, P, P, P, 0, 3, 10, 8192, P + 4, W, N), lib,
+             "workspace")
+    need = lib.miso_attn_prefill_workspace_bytes(2000)
+    rejected(lib.miso_attn_prefill_ws(P, P, P, P, P, 0, 2000, 2000, 8192, P, need - 1, N), lib,
+             "smaller than")
     rejected(lib.miso_attn_prep(P, P, P, P, P, P, P, P, P, 10, 10, 1e-6, N), lib, "full")
     rejected(lib.miso_attn_prep_batch(P, P, P, P, P, P, P, P, P, 8, 10, 1e-6, 3, 9216, N), lib,
              "full")
@@ -205,3 +216,15 @@ def test_ragged_scratch_sizes(lib):
     assert lib.miso_attn_ragged_splits(512) == 1 and lib.miso_attn_ragged_splits(513) == 2
     assert lib.miso_attn_ragged_splits(16384) == 32
     assert lib.miso_attn_ragged_partials(64, 16384) == 64 * 2 * 32 * 8
+
+
+def test_prefill_workspace_bytes(lib):
+    """The balanced prefill's workspace (n <= 2048): a fixed 1 KiB of pair counters, then (m, l)
+    and O of both parts of each pair; nothing for the launches that take the plain layout."""
+    for n in (0, 2049, 3000, 4095, 4096, 1 << 20):
+        assert lib.miso_attn_prefill_workspace_bytes(n) == 0
+    for n in (1, 16, 17, 32, 33, 1000, 2047, 2048):
+        pairs = 2 * (((n + 15) // 16) // 2)
+        assert lib.miso_attn_prefill_workspace_bytes(n) == 1024 + pairs * 2 * 128 * 258 * 4
+    assert max(lib.miso_attn_prefill_workspace_bytes(n) for n in range(1, 4200, 7)) == \
+        lib.miso_attn_prefill_workspace_bytes(2048)

@@ -6,6 +6,9 @@ blocks, a 32-key sub-chunk crossing, a non-empty prefix) with q = 2 N(0,1), then
 configs C3 (2048 tokens, empty cache; every row) and C4 (8192 tokens after an 8192-token prefix;
 a deterministic row sample covering first/last tiles and diagonal tiles), plus two size-free
 properties: chunked prefill equals one-shot prefill, and prefill row t equals decode at pos0+t+1.
+The balanced form (miso_attn_prefill_ws: heavy token blocks split between two workgroups, the
+parts merged through a workspace) is checked the same way, on shapes with and without split
+blocks, plus run-to-run bit equality and reuse of one workspace across sizes.
 Gate: |got - ref| <= 2e-3 + 1e-2 |ref| for every element (f32 output).
 """
 from __future__ import annotations
@@ -20,8 +23,9 @@ pytestmark = pytest.mark.gpu
 H, D = 16, 256
 
 
-def run_prefill(attn, torch, p, pos0=None, n=None, t_from=0):
-    """Prefill tokens [t_from, t_from + n) of the case (positions pos0 + t)."""
+def run_prefill(attn, torch, p, pos0=None, n=None, t_from=0, scratch=None):
+    """Prefill tokens [t_from, t_from + n) of the case (positions pos0 + t); with `scratch`, the
+    balanced form."""
     pos0 = p["pos0"] if pos0 is None else pos0
     n = p["n"] if n is None else n
     S = p["qg_stride"]
@@ -29,16 +33,16 @@ def run_prefill(attn, torch, p, pos0=None, n=None, t_from=0):
     qg = to_dev(torch, p["qg"][t_from * S:(t_from + n) * S])
     k, v = to_dev(torch, p["k"]), to_dev(torch, p["v"])
     core = torch.full((n * H * D,), -1.0, device="cuda")
-    attn.attn_prefill(q, qg, k, v, core, pos0, n, p["max_ctx"], S)
+    attn.attn_prefill(q, qg, k, v, core, pos0, n, p["max_ctx"], S, scratch=scratch)
     torch.cuda.synchronize()
     return to_host(core).reshape(n, H, D)
 
 
 def check(O, attn, torch, pos0, n, q_scale=2.0, seed=None, rows=None, name="prefill",
-          max_ctx=None):
+          max_ctx=None, scratch=None):
     p = O.prefill_inputs(1000 + 17 * pos0 + n if seed is None else seed, pos0, n,
                          max_ctx if max_ctx else pos0 + n + 5, q_scale=q_scale)
-    got = run_prefill(attn, torch, p)
+    got = run_prefill(attn, torch, p, scratch=scratch)
     rows = np.arange(n) if rows is None else np.asarray(rows)
     ref = O.prefill_f64(p["q"], p["qg"], p["qg_stride"], p["k"], p["v"], pos0, p["max_ctx"], rows)
     st = O.compare(got[rows], ref)
@@ -129,3 +133,63 @@ def test_reference_prefill_kernel_agrees_with_oracle(O, attn, torch_mod, ref_ker
                             np.arange(n))
         rel = np.sqrt(((got - ref) ** 2).sum(axis=2) / (ref ** 2).sum(axis=2)).max()
         assert rel <= 1e-5, rel
+
+
+@pytest.fixture(scope="module")
+def prefill_scratch(attn, torch_mod):
+    return attn.PrefillScratch()
+
+
+def balanced_rows(pos0, n):
+    """Every row up to 1200 tokens; else the first and last rows of every 64th block, the last
+    128 rows (the heaviest blocks, split) and a seeded sample."""
+    if n <= 1200:
+        return None
+    rng = np.random.default_rng(n + pos0)
+    rows = [b * 16 + r for b in range(0, (n + 15) // 16, 64) for r in (0, 15)]
+    rows += list(range(max(0, n - 128), n)) + rng.choice(n, 64, replace=False).tolist()
+    return np.unique(np.array([r for r in rows if r < n]))
+
+
+@pytest.mark.parametrize("pos0,n", [(0, 1), (0, 16), (0, 17), (0, 48), (0, 129), (0, 300),
+                                    (7, 999), (100, 1500), (3000, 600), (1, 2047),
+                                    (0, 2049), (500, 4000)])
+def test_prefill_balanced_matches_oracle(O, attn, torch_mod, prefill_scratch, pos0, n):
+    check(O, attn, torch_mod, pos0, n, rows=balanced_rows(pos0, n), name="balanced",
+          scratch=prefill_scratch)
+
+
+def test_prefill_balanced_c3_all_rows(O, attn, torch_mod, prefill_scratch):
+    """C3 through the balanced form: 2048 tokens, empty cache, every row."""
+    check(O, attn, torch_mod, 0, 2048, q_scale=1.0, seed=2048, max_ctx=2048, name="C3 balanced",
+          scratch=prefill_scratch)
+
+
+def test_prefill_balanced_repeatable(O, attn, torch_mod, prefill_scratch):
+    """Bit-equal across calls (the merge does not depend on which part arrives second), one
+    workspace across sizes, and within the gate of the one-block-per-workgroup form."""
+    torch = torch_mod
+    p = O.prefill_inputs(777, 0, 2048, 2048, q_scale=1.0)
+    first = run_prefill(attn, torch, p, scratch=prefill_scratch)
+    small = O.prefill_inputs(778, 40, 333, 400, q_scale=2.0)
+    a = run_prefill(attn, torch, small, scratch=prefill_scratch)
+    for _ in range(3):
+        again = run_prefill(attn, torch, p, scratch=prefill_scratch)
+        assert np.array_equal(again, first)
+    assert np.array_equal(run_prefill(attn, torch, small, scratch=prefill_scratch), a)
+    plain = run_prefill(attn, torch, p)
+    st = O.compare(first, plain.astype(np.float64))
+    report("balanced vs plain C3 inputs", st)
+    assert st["ok"], st
+    assert not np.array_equal(first, plain)  # the split blocks did merge two parts
+
+
+@pytest.mark.parametrize("n", [2049, 4096])
+def test_prefill_balanced_wide_is_plain(O, attn, torch_mod, prefill_scratch, n):
+    """Past 2048 tokens the balanced entry runs the one-block-per-workgroup layout (one and two
+    row blocks per wave), bit-equal to miso_attn_prefill."""
+    torch = torch_mod
+    p = O.prefill_inputs(n, 0, n, n, q_scale=1.0)
+    assert attn.prefill_workspace_bytes(n) == 0
+    assert np.array_equal(run_prefill(attn, torch, p, scratch=prefill_scratch),
+                          run_prefill(attn, torch, p))
