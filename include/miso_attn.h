@@ -332,7 +332,10 @@ typedef struct miso_attn_layer {
 } miso_attn_layer;
 
 /* Device floats of the decode / prefill workspaces (the engine's AttentionScratch and
- * AttentionPrefillScratch, src/engine/attention.hpp:44-69), for chunks of up to max_tok tokens. */
+ * AttentionPrefillScratch, src/engine/attention.hpp:44-69), for chunks of up to max_tok tokens.
+ * The prefill workspace ends with the balanced prefill's workspace (miso_attn_prefill_ws), which
+ * chunks of up to 2048 tokens use: zero-fill it once when it is allocated (every call leaves its
+ * pair counters zero). */
 uint64_t miso_attn_layer_decode_ws(void);
 uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok);
 

@@ -536,7 +536,8 @@ class LayerWorkspace:
         self.max_tok = max_tok
         self.decode = torch.empty(int(lib.miso_attn_layer_decode_ws()), dtype=torch.float32,
                                   device=device)
-        self.prefill = torch.empty(max(1, int(lib.miso_attn_layer_prefill_ws(max_tok))),
+        # zero-filled once: the balanced prefill's pair counters sit at its end
+        self.prefill = torch.zeros(max(1, int(lib.miso_attn_layer_prefill_ws(max_tok))),
                                    dtype=torch.float32, device=device)
 
 

@@ -70,7 +70,11 @@ AttentionCache::AttentionCache(unsigned n)
 AttentionScratch::AttentionScratch() : ws(L::decode_workspace_floats()) {}
 
 AttentionPrefillScratch::AttentionPrefillScratch(unsigned n)
-    : max_tok(n), ws(L::prefill_workspace_floats(n)) {}
+    : max_tok(n), ws(L::prefill_workspace_floats(n)) {
+  // The balanced prefill's pair counters at the workspace's end start at zero (every chunk
+  // leaves them so).
+  MISO_HIP_CHECK(hipMemset(ws.data(), 0, ws.size() * sizeof(float)));
+}
 
 void attention_decode(const AttentionLayer& w, AttentionCache& cache, AttentionScratch& sc,
                       const RopeConfig& rope, float* h, const float* delta, float* y, float eps,

@@ -141,3 +141,33 @@ def test_layer_rejections(attn, torch_mod, layer_case):
         attn.layer_prefill(layer, big_kc, torch.zeros_like(big_kc), 64, 0, 17,
                            torch.zeros(17 * 2048, device="cuda"), None,
                            torch.zeros(17 * 2048, device="cuda"), EPS, ws)
+
+
+def test_layer_prefill_balanced_chunk(O, attn, torch_mod, layer_case):
+    """One 512-token chunk on an empty cache: the layer's prefill takes the balanced form with
+    split token blocks (chunks of up to 2048 tokens), against the layer oracle."""
+    torch = torch_mod
+    layer, deq, norms = layer_case
+    n = ctx = 512
+    rng = np.random.default_rng(512)
+    h0 = rng.standard_normal((n, 2048)).astype(np.float32)
+    delta = (0.5 * rng.standard_normal((n, 2048))).astype(np.float32)
+    h, d = to_dev(torch, h0.reshape(-1)), to_dev(torch, delta.reshape(-1))
+    y = torch.full((n * 2048,), -1234.5, dtype=torch.float32, device="cuda")
+    kc = torch.zeros(2 * ctx * 256, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    ws = attn.LayerWorkspace(max_tok=n)
+    attn.layer_prefill(layer, kc, vc, ctx, 0, n, h, d, y, EPS, ws)
+    first = to_host(y).copy()
+    h2 = to_dev(torch, h0.reshape(-1))  # the same chunk again over the same workspace
+    attn.layer_prefill(layer, kc, vc, ctx, 0, n, h2, d, y, EPS, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(y), first), "repeat over one workspace"
+    _, ref_y, _, _ = O.layer_f64(h0, delta, deq["q"], deq["k"], deq["v"], deq["o"],
+                                 norms["attn_norm"], norms["q_norm"], norms["k_norm"],
+                                 norms["inv_freq"], 0, ctx, EPS)
+    got = first.reshape(n, 2048).astype(np.float64)
+    err = np.sqrt(((got - ref_y) ** 2).sum(axis=1) / (ref_y ** 2).sum(axis=1))
+    print(f"[layer] 512-token balanced chunk: max rel-L2 {err.max():.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err.max() <= 5e-3, int(err.argmax())
