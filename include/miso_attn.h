@@ -148,14 +148,15 @@ int miso_attn_prefill(const float* q, const float* qg, const uint16_t* k_cache,
  * 16-token block, kernels/attention_prefill.hpp:42-161, so under the causal mask the last block
  * sets the time). Same arguments, contract and output as miso_attn_prefill (within the prefill
  * tolerance, not bitwise: the heavy blocks' keys are summed in two parts; bit-equal from call to
- * call). For n <= 2048 token block B-1-j of the n / 16 blocks is paired with block j and the
- * pair's tiles are shared by two workgroups (at most 256, one per CU); the two parts of a split
- * block meet in `workspace`: miso_attn_prefill_workspace_bytes(n) bytes of device memory,
- * 16-byte aligned, zero-filled once before its first use (every call leaves it reusable; one
- * workspace of miso_attn_prefill_workspace_bytes(2048) bytes serves every n). Calls that overlap
- * on one workspace race. For larger n it runs miso_attn_prefill and the workspace is not used
+ * call). For n <= 2048 (16-token blocks) and for 3841 <= n <= 4096 (32-token blocks) token
+ * block B-1-j of the B blocks is paired with block j and the pair's tiles are shared by two
+ * workgroups (at most 256, one per CU); the two parts of a split block meet in `workspace`:
+ * miso_attn_prefill_workspace_bytes(n) bytes of device memory, 16-byte aligned, zero-filled once
+ * before its first use (every call leaves it reusable; one workspace of
+ * miso_attn_prefill_workspace_bytes(4096) bytes serves every n). Calls that overlap on one
+ * workspace race. For other n it runs miso_attn_prefill and the workspace is not used
  * (miso_attn_prefill_workspace_bytes returns 0). Rejects what miso_attn_prefill rejects and, for
- * n <= 2048, a NULL or misaligned workspace or one smaller than required. */
+ * the balanced sizes, a NULL or misaligned workspace or one smaller than required. */
 uint64_t miso_attn_prefill_workspace_bytes(uint32_t n);
 int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cache,
                          const uint16_t* v_cache, float* core, uint32_t pos0, uint32_t n,
@@ -334,7 +335,7 @@ typedef struct miso_attn_layer {
 /* Device floats of the decode / prefill workspaces (the engine's AttentionScratch and
  * AttentionPrefillScratch, src/engine/attention.hpp:44-69), for chunks of up to max_tok tokens.
  * The prefill workspace ends with the balanced prefill's workspace (miso_attn_prefill_ws), which
- * chunks of up to 2048 tokens use: zero-fill it once when it is allocated (every call leaves its
+ * chunks of up to 4096 tokens use: zero-fill it once when it is allocated (every call leaves its
  * pair counters zero). */
 uint64_t miso_attn_layer_decode_ws(void);
 uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok);

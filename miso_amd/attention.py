@@ -179,10 +179,12 @@ def prefill_workspace_bytes(n: int) -> int:
 
 class PrefillScratch:
     """Workspace of the balanced prefill (miso_attn_prefill_ws) for launches of up to max_n
-    tokens (the form covers n <= 2048), zero-filled once; every call leaves it reusable."""
+    tokens (the form covers n <= 2048 and 3841 <= n <= 4096), zero-filled once; every call leaves
+    it reusable."""
 
-    def __init__(self, max_n: int = 2048, device="cuda"):
-        nbytes = prefill_workspace_bytes(min(max_n, 2048))
+    def __init__(self, max_n: int = 4096, device="cuda"):
+        nbytes = max(prefill_workspace_bytes(min(max_n, 2048)),
+                     prefill_workspace_bytes(min(max_n, 4096)))
         self.buf = torch.zeros(max((nbytes + 3) // 4, 4), dtype=torch.int32, device=device)
         self.nbytes = self.buf.numel() * 4
 

@@ -347,7 +347,8 @@ int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cach
     return fail(fn, "workspace smaller than miso_attn_prefill_workspace_bytes(n)");
   char* const ws = static_cast<char*>(workspace);
   float* const part_ml = reinterpret_cast<float*>(ws + k::kAttnSplitCounterBytes);
-  float* const part_o = part_ml + std::size_t{k::attn_prefill_split_pairs(n)} * 2 * 128 * 2;
+  float* const part_o = part_ml + std::size_t{k::attn_prefill_split_pairs(n)} * 2 *
+                                       k::attn_prefill_split_rows(n) * 2;
   const k::AttnPrefillSplitParams p{a, part_o, part_ml, reinterpret_cast<unsigned*>(ws)};
   k::attn_prefill_split_kernel<256><<<k::attn_prefill_split_items(n), 256, 0,
                                       as_stream(stream)>>>(p);

@@ -260,7 +260,7 @@ inline DecodeWorkspace decode_workspace(float* ws) {
 }
 
 // The prefill workspace ends with the balanced prefill's workspace for chunks of up to
-// min(max_tok, 2048) tokens (attention_prefill.hpp): its pair counters must be zero before the
+// min(max_tok, 4096) tokens (attention_prefill.hpp): its pair counters must be zero before the
 // first chunk, so the whole prefill workspace is zero-filled once when it is allocated (every
 // chunk leaves the counters zero).
 struct PrefillWorkspace {
@@ -270,11 +270,11 @@ struct PrefillWorkspace {
   float* core;   // [max_tok][16][256]
   float* xs;     // [max_tok][4096 / 32] GEMM input sums
   _Float16* xh;  // [max_tok][4096] GEMM input values
-  char* balance;  // attn_prefill_split_workspace_bytes(min(max_tok, 2048)) bytes
+  char* balance;  // attn_prefill_split_workspace_bytes(min(max_tok, 4096)) bytes
 };
 
 inline constexpr std::size_t prefill_balance_floats(unsigned max_tok) {
-  return (attn_prefill_split_workspace_bytes(max_tok < 2048 ? max_tok : 2048) + 15) / 16 * 4;
+  return (attn_prefill_split_workspace_bytes(max_tok < 4096 ? max_tok : 4096) + 15) / 16 * 4;
 }
 
 inline constexpr std::size_t prefill_workspace_floats(unsigned max_tok) {
@@ -333,7 +333,7 @@ inline const char* decode_step(const Weights& w, attn::half_t* k_cache, attn::ha
 
 // n consecutive tokens at pos0 ([n][2048] h / delta / y): the prefill GEMMs, batched prep and
 // causal flash attention over the cache up to each token (the balanced form for chunks of up to
-// 2048 tokens).
+// 4096 tokens).
 inline const char* prefill_step(const Weights& w, attn::half_t* k_cache, attn::half_t* v_cache,
                                 unsigned pos0, unsigned n, unsigned max_ctx, float* h,
                                 const float* delta, float* y, float eps,
@@ -360,10 +360,12 @@ inline const char* prefill_step(const Weights& w, attn::half_t* k_cache, attn::h
                                  kProj};
   attn_prep_batch_kernel<256><<<n * 18, 256, 0, stream>>>(prep);
   const AttnPrefillParams ap{ws.q, ws.proj, k_cache, v_cache, ws.core, pos0, n, max_ctx, kProj};
-  if (attn_prefill_balanced(n)) {  // n <= 2048 <= its workspace's size (n <= max_tok)
+  if (attn_prefill_balanced(n)) {  // n <= 4096 and n <= max_tok: within its workspace
     float* const part_ml = reinterpret_cast<float*>(ws.balance + kAttnSplitCounterBytes);
-    const AttnPrefillSplitParams sp{ap, part_ml + std::size_t{attn_prefill_split_pairs(n)} * 512,
-                                    part_ml, reinterpret_cast<unsigned*>(ws.balance)};
+    const std::size_t ml_floats =
+        std::size_t{attn_prefill_split_pairs(n)} * 2 * attn_prefill_split_rows(n) * 2;
+    const AttnPrefillSplitParams sp{ap, part_ml + ml_floats, part_ml,
+                                    reinterpret_cast<unsigned*>(ws.balance)};
     attn_prefill_split_kernel<256><<<attn_prefill_split_items(n), 256, 0, stream>>>(sp);
   } else {
     attn_prefill_kernel<256><<<attn_prefill_items(n), 256, 0, stream>>>(ap);

@@ -85,27 +85,29 @@ __host__ __device__ inline unsigned attn_prefill_items(unsigned n) {
 // ------------------------------------------------------------------------------------------------
 // Balanced causal prefill (no reference counterpart; the reference launches one workgroup per
 // token block). Under a causal mask block b of a launch sees ~b tiles of keys, so with one
-// workgroup per block the last block sets the time at about twice the mean. For launches of one
-// row block per wave (n < kAttnWideMin) the balanced form pairs block B-1-j with block j (their
-// tile counts sum to a near constant) and gives the pair two workgroups: A takes the heavy
-// block's first S = ceil(pair tiles / 2) tiles, B its remaining tiles and then the light block.
+// workgroup per block the last block sets the time at about twice the mean. For launches of up
+// to 4096 tokens the balanced form pairs block B-1-j with block j (their tile counts sum to a
+// near constant) and gives the pair two workgroups: A takes the heavy block's first
+// S = ceil(pair tiles / 2) tiles, B the heavy block's remaining tiles and then the light block.
 // Both parts of a split block write their partial (m, l, O) to a workspace; whichever finishes
 // second (an agent-scope counter per pair) merges the other's partial into its own and stores
-// the output. Pairs whose heavy block would save fewer than kAttnSplitMinTiles tiles run
-// unsplit (A: the heavy block, B: the light one). The pairing pays while its grid fits the chip
-// at one workgroup per CU (attn_prefill_balanced: n <= 2048 on the 256 CUs of an MI355X);
-// beyond that the one-block layout's extra rounds already even out the load (measured: 3072
-// tokens after a 1024-token prefix, 175 us one-block against 202 us paired).
+// the output.
+// Pairs whose heavy block would save fewer than kAttnSplitMinTiles tiles run unsplit (A: the
+// heavy block, B: the light one). The pairing pays while its grid fits the chip at one
+// workgroup per CU (256 on an MI355X): one row block per wave (16-token blocks) up to 2048
+// tokens, two (32-token blocks) from 3841 to 4096 (attn_prefill_balanced). Otherwise the
+// one-workgroup-per-block layout's extra rounds already even out the load (measured: 3072 tokens
+// after a 1024-token prefix in 16-token pairs, 384 workgroups, 202 us against 175 us).
 // ------------------------------------------------------------------------------------------------
 
 constexpr unsigned kAttnSplitMinTiles = 4;
 constexpr unsigned kAttnBalancedMaxItems = 256;  // CUs of an MI355X
 
-// Workspace of the balanced form, for launches of n < kAttnWideMin: one counter per pair (a
-// fixed region of kAttnSplitMaxPairs, so one workspace serves every n), then (m, l) (f32
-// [slot][128 rows][2]) and O (f32 [slot][128][256]) of the two parts (slots 2 pair, 2 pair + 1)
-// of each pair. The counters must be zero before the first launch over a workspace; every launch
-// leaves them zero. Launches that overlap on one workspace race.
+// Workspace of the balanced form: one counter per pair (a fixed region of kAttnSplitMaxPairs, so
+// one workspace serves every n), then (m, l) (f32 [slot][rows][2]) and O (f32 [slot][rows][256])
+// of the two parts (slots 2 pair, 2 pair + 1) of each pair, rows = 128 per row block per wave.
+// The counters must be zero before the first launch over a workspace; every launch leaves them
+// zero. Launches that overlap on one workspace race.
 struct AttnPrefillSplitParams {
   AttnPrefillParams a;
   float* part_o;
@@ -113,8 +115,20 @@ struct AttnPrefillSplitParams {
   unsigned* counters;
 };
 
+// Row blocks per wave of the balanced form: one up to 2048 tokens, two up to 4096.
+__host__ __device__ constexpr unsigned attn_prefill_balanced_blocks(unsigned n) {
+  return n > 2048 ? 2 : 1;
+}
+__host__ __device__ constexpr unsigned attn_prefill_split_block_count(unsigned n) {
+  const unsigned tokens = kAttnQBlock * attn_prefill_balanced_blocks(n);
+  return (n + tokens - 1) / tokens;
+}
 __host__ __device__ constexpr unsigned attn_prefill_split_pairs(unsigned n) {
-  return attn::kKvHeads * (((n + kAttnQBlock - 1) / kAttnQBlock) / 2);
+  return attn::kKvHeads * (attn_prefill_split_block_count(n) / 2);
+}
+// Rows of one part's partial: 128 query rows per row block.
+__host__ __device__ constexpr unsigned attn_prefill_split_rows(unsigned n) {
+  return 128 * attn_prefill_balanced_blocks(n);
 }
 constexpr unsigned kAttnSplitMaxPairs = attn::kKvHeads * (kAttnWideMin / kAttnQBlock / 2);
 constexpr std::size_t kAttnSplitCounterBytes = kAttnSplitMaxPairs * sizeof(unsigned);
@@ -123,19 +137,23 @@ constexpr std::size_t kAttnSplitCounterBytes = kAttnSplitMaxPairs * sizeof(unsig
 // groups of 4 slots per XCD pair round (XCD = item % 8 as in attn_prefill_items), the two
 // workgroups of a slot in consecutive rounds on the same XCD.
 __host__ __device__ constexpr unsigned attn_prefill_split_items(unsigned n) {
-  const unsigned blocks = (n + kAttnQBlock - 1) / kAttnQBlock;
+  const unsigned blocks = attn_prefill_split_block_count(n);
   const unsigned slots = blocks / 2 + blocks % 2;
   return 16 * ((slots + 3) / 4);
 }
 
-// Whether a launch of n tokens takes the balanced form.
+// Whether a launch of n tokens takes the balanced form: n <= 2048 (16-token blocks) or, with
+// 32-token blocks, when the grid fills the chip (3841 <= n <= 4096); between the two the
+// one-block-per-workgroup layout over two rounds is faster (3072 tokens on an empty cache:
+// 121.6 us against 151.9 us for 192 paired workgroups).
 __host__ __device__ constexpr bool attn_prefill_balanced(unsigned n) {
-  return n > 0 && n < kAttnWideMin && attn_prefill_split_items(n) <= kAttnBalancedMaxItems;
+  return n > 0 && n <= kAttnWideMin && attn_prefill_split_items(n) <= kAttnBalancedMaxItems &&
+         (n <= 2048 || attn_prefill_split_items(n) == kAttnBalancedMaxItems);
 }
 
 __host__ __device__ constexpr std::size_t attn_prefill_split_workspace_bytes(unsigned n) {
-  return kAttnSplitCounterBytes +
-         std::size_t{attn_prefill_split_pairs(n)} * 2 * 128 * (attn::kDim + 2) * sizeof(float);
+  return kAttnSplitCounterBytes + std::size_t{attn_prefill_split_pairs(n)} * 2 *
+                                      attn_prefill_split_rows(n) * (attn::kDim + 2) * sizeof(float);
 }
 
 namespace prefill_detail {
@@ -918,31 +936,35 @@ __device__ __attribute__((always_inline)) inline void prefill_items(
       // back every dirty line of the L2 (the other workgroups' output included), which stalls
       // the XCD for microseconds.
       bool store = true, merge = false;
-      float f_a = 0.0f, f_b = 0.0f;
+      float f_a[kBlocks] = {}, f_b[kBlocks] = {};  // this lane's row (column col)
       bool own_a = true;
-      unsigned oth_off = 0;  // byte offset of the other part's rows (this wave's first)
+      const float* oth = nullptr;  // the other part's rows of this wave (this lane's 16 bytes)
       constexpr int kSc1 = 16;  // cache-policy operand of the buffer builtins: sc1
       const auto part_rsrc = [&](float* base, unsigned floats) __attribute__((always_inline)) {
         return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(4 * floats),
                                                  0x00020000);
       };
-      const unsigned slots = 2 * attn_prefill_split_pairs(p.n);
+      // A part's rows: slot * kPartRows + 32 kBlocks wave + 32 c + r (block c, row r).
+      constexpr unsigned kPartRows = 128 * kBlocks;
+      const unsigned part_rows = 2 * attn_prefill_split_pairs(p.n) * kPartRows;
       if constexpr (kSplit) {
-        static_assert(kBlocks == 1, "the balanced form runs one row block per wave");
         if (jb.part) {
-          const auto o_rsrc = part_rsrc(sp->part_o, slots * 128 * kDim);
-          const auto ml_rsrc = part_rsrc(sp->part_ml, slots * 128 * 2);
-          const unsigned row0 = jb.slot * 128 + 32 * wave;
-          stage_o(0, 1.0f);
-          if (hi == 0)
-            __builtin_amdgcn_raw_buffer_store_b64(
-                __builtin_bit_cast(cdna4::u32x2_t, float2{rw.m[0], l_row[0]}), ml_rsrc,
-                (row0 + col) * 8, 0, kSc1);
+          const auto o_rsrc = part_rsrc(sp->part_o, part_rows * kDim);
+          const auto ml_rsrc = part_rsrc(sp->part_ml, part_rows * 2);
+          const unsigned row0 = jb.slot * kPartRows + 32 * kBlocks * wave;
 #pragma unroll
-          for (int r = 0; r < 32; ++r)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(cdna4::u32x4_t, staged_row(r)), o_rsrc,
-                (row0 + r) * 1024 + 16 * lane, 0, kSc1);
+          for (int c = 0; c < kBlocks; ++c) {
+            stage_o(c, 1.0f);
+            if (hi == 0)
+              __builtin_amdgcn_raw_buffer_store_b64(
+                  __builtin_bit_cast(cdna4::u32x2_t, float2{rw.m[c], l_row[c]}), ml_rsrc,
+                  (row0 + 32 * c + col) * 8, 0, kSc1);
+#pragma unroll
+            for (int r = 0; r < 32; ++r)
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(cdna4::u32x4_t, staged_row(r)), o_rsrc,
+                  (row0 + 32 * c + r) * 1024 + 16 * lane, 0, kSc1);
+          }
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           __syncthreads();
           const unsigned flag = lds0 + 4 * 32 * kStageRow;  // past every wave's staging
@@ -955,73 +977,80 @@ __device__ __attribute__((always_inline)) inline void prefill_items(
           if (store) {  // uniform: the other part's partial is complete
             if (t == 0)  // every launch leaves the counters zero
               __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned orow0 = (jb.slot ^ 1u) * 128 + 32 * wave;
-            const float2 oml = __builtin_bit_cast(
-                float2, __builtin_amdgcn_raw_buffer_load_b64(ml_rsrc, (orow0 + col) * 8, 0, kSc1));
+            const unsigned orow0 = (jb.slot ^ 1u) * kPartRows + 32 * kBlocks * wave;
             own_a = (jb.slot & 1u) == 0;
-            const float m_a = own_a ? rw.m[0] : oml.x, m_b = own_a ? oml.x : rw.m[0];
-            const float l_a = own_a ? l_row[0] : oml.y, l_b = own_a ? oml.y : l_row[0];
-            const float m_max = fmaxf(m_a, m_b);
-            const float e_a = __builtin_amdgcn_exp2f(m_a - m_max);
-            const float e_b = __builtin_amdgcn_exp2f(m_b - m_max);
-            const float inv_l = __builtin_amdgcn_rcpf(l_a * e_a + l_b * e_b);
-            f_a = e_a * inv_l;
-            f_b = e_b * inv_l;
+#pragma unroll
+            for (int c = 0; c < kBlocks; ++c) {
+              const float2 oml = __builtin_bit_cast(
+                  float2, __builtin_amdgcn_raw_buffer_load_b64(ml_rsrc, (orow0 + 32 * c + col) * 8,
+                                                               0, kSc1));
+              const float m_a = own_a ? rw.m[c] : oml.x, m_b = own_a ? oml.x : rw.m[c];
+              const float l_a = own_a ? l_row[c] : oml.y, l_b = own_a ? oml.y : l_row[c];
+              const float m_max = fmaxf(m_a, m_b);
+              const float e_a = __builtin_amdgcn_exp2f(m_a - m_max);
+              const float e_b = __builtin_amdgcn_exp2f(m_b - m_max);
+              const float inv_l = __builtin_amdgcn_rcpf(l_a * e_a + l_b * e_b);
+              f_a[c] = e_a * inv_l;
+              f_b[c] = e_b * inv_l;
+            }
             merge = true;
-            oth_off = orow0 * 1024 + 16 * lane;
+            oth = sp->part_o + std::size_t{orow0} * kDim + 4 * lane;
           }
         }
       }
       if (store) {
 #pragma unroll
         for (int c = 0; c < kBlocks; ++c) {
-          if (!merge)  // a merging part's raw O is still staged from its partial
+          if (!merge) {
             stage_o(c, __builtin_amdgcn_rcpf(l_row[c]));
+          } else if constexpr (kSplit) {
+            // The other part's rows of the block straight into the staging (one agent-coherent
+            // LDS-DMA load per row), then each lane combines its own accumulators with them in
+            // place: O_A f_A + O_B f_B for its row.
+#pragma unroll
+            for (int r = 0; r < 32; ++r)
+              __builtin_amdgcn_global_load_lds(
+                  oth + (32 * c + r) * kDim,
+                  reinterpret_cast<__attribute__((address_space(3))) void*>(stage + kStageRow * r),
+                  16, 0, kSc1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+#pragma unroll
+              for (int r4 = 0; r4 < 4; ++r4) {
+                auto* at = reinterpret_cast<__attribute__((address_space(3))) cdna4::float4_t*>(
+                    stage + kStageRow * col + 16 * (8 * b + 2 * r4 + hi));
+                const cdna4::float4_t w = *at;
+                const cdna4::float4_t v = {oacc[c][b][4 * r4 + 0], oacc[c][b][4 * r4 + 1],
+                                           oacc[c][b][4 * r4 + 2], oacc[c][b][4 * r4 + 3]};
+                const cdna4::float4_t oa = own_a ? v : w, ob = own_a ? w : v;
+                *at = cdna4::float4_t{__builtin_fmaf(ob[0], f_b[c], oa[0] * f_a[c]),
+                                      __builtin_fmaf(ob[1], f_b[c], oa[1] * f_a[c]),
+                                      __builtin_fmaf(ob[2], f_b[c], oa[2] * f_a[c]),
+                                      __builtin_fmaf(ob[3], f_b[c], oa[3] * f_a[c])};
+              }
+          }
           // Rows 8 j + h of the block: token tw + 4 c + j, head kvh * 8 + h; tokens >= n are not
           // stored (their gate loads read token n - 1).
           const unsigned tok0 = tw + 4 * c;
           const float* gate = p.qg + std::size_t{kvh} * kGroup * 2 * kDim + kDim + 4 * lane;
           float* out = p.core + std::size_t{kvh} * kGroup * kDim + 4 * lane;
-          // Rows in flight: all 32 of the block with one block of O in the AGPRs; with two, or
-          // with the other part's rows to add, 16 at a time (the loads of the second half then
-          // wait behind the stores of the first).
-          constexpr int kGateRows = kBlocks == 1 && !kSplit ? 32 : 16;
+          // Gate rows in flight: all 32 of the block with one block of O in the AGPRs; with two,
+          // 16 at a time (the loads of the second half then wait behind the stores of the first).
+          constexpr int kGateRows = kBlocks == 1 ? 32 : 16;
 #pragma unroll
           for (int r0 = 0; r0 < 32; r0 += kGateRows) {
-            float4 gv[kGateRows], ov[kSplit ? kGateRows : 1];
+            float4 gv[kGateRows];
 #pragma unroll
             for (int r = r0; r < r0 + kGateRows; ++r) {
               const unsigned tk = min(tok0 + r / 8, p.n - 1);
               gv[r - r0] = *reinterpret_cast<const float4*>(gate + std::size_t{tk} * p.qg_stride +
                                                             (r % 8) * 2 * kDim);
             }
-            if constexpr (kSplit)
-              if (merge) {
-                const auto o_rsrc = part_rsrc(sp->part_o, slots * 128 * kDim);
-#pragma unroll
-                for (int r = r0; r < r0 + kGateRows; ++r)
-                  ov[r - r0] = __builtin_bit_cast(
-                      float4, __builtin_amdgcn_raw_buffer_load_b128(o_rsrc, oth_off + r * 1024,
-                                                                    0, kSc1));
-              }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = r0; r < r0 + kGateRows; ++r) {
-              cdna4::float4_t v = staged_row(r);
-              if constexpr (kSplit)
-                if (merge) {  // row r's factors from lane r (column r)
-                  const float fa = __builtin_bit_cast(
-                      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f_a), r));
-                  const float fb = __builtin_bit_cast(
-                      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f_b), r));
-                  const cdna4::float4_t w = {ov[r - r0].x, ov[r - r0].y, ov[r - r0].z,
-                                             ov[r - r0].w};
-                  const cdna4::float4_t oa = own_a ? v : w, ob = own_a ? w : v;
-                  v = cdna4::float4_t{__builtin_fmaf(ob[0], fb, oa[0] * fa),
-                                      __builtin_fmaf(ob[1], fb, oa[1] * fa),
-                                      __builtin_fmaf(ob[2], fb, oa[2] * fa),
-                                      __builtin_fmaf(ob[3], fb, oa[3] * fa)};
-                }
+              const cdna4::float4_t v = staged_row(r);
               const float4 g = gv[r - r0];
               float4 o;
               o.x = v[0] * __builtin_amdgcn_rcpf(1.0f + __expf(-g.x));
@@ -1063,7 +1092,11 @@ template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_prefill_split_kernel(AttnPrefillSplitParams p) {
   static_assert(kBlock == 256, "four waves per prefill workgroup");
   __shared__ prefill_detail::Shared sh;
-  prefill_detail::prefill_items<1, true>(p.a, &p, 0, attn_prefill_split_items(p.a.n), sh);
+  const unsigned items = attn_prefill_split_items(p.a.n);
+  if (attn_prefill_balanced_blocks(p.a.n) == 2)  // uniform: the block size follows n
+    prefill_detail::prefill_items<2, true>(p.a, &p, 0, items, sh);
+  else
+    prefill_detail::prefill_items<1, true>(p.a, &p, 0, items, sh);
 }
 
 }  // namespace miso::kernels

@@ -219,12 +219,16 @@ def test_ragged_scratch_sizes(lib):
 
 
 def test_prefill_workspace_bytes(lib):
-    """The balanced prefill's workspace (n <= 2048): a fixed 1 KiB of pair counters, then (m, l)
-    and O of both parts of each pair; nothing for the launches that take the plain layout."""
-    for n in (0, 2049, 3000, 4095, 4096, 1 << 20):
+    """The balanced prefill's workspace (n <= 2048, 3841 <= n <= 4096): a fixed 1 KiB of pair
+    counters, then (m, l) and O of both parts of each pair (128 rows per part with 16-token
+    blocks up to 2048 tokens, 256 with 32-token blocks above); nothing for the launches that take
+    the plain layout."""
+    for n in (0, 2049, 3000, 3840, 4097, 8192, 1 << 20):
         assert lib.miso_attn_prefill_workspace_bytes(n) == 0
-    for n in (1, 16, 17, 32, 33, 1000, 2047, 2048):
-        pairs = 2 * (((n + 15) // 16) // 2)
-        assert lib.miso_attn_prefill_workspace_bytes(n) == 1024 + pairs * 2 * 128 * 258 * 4
+    for n in (1, 16, 17, 32, 33, 1000, 2047, 2048, 3841, 4000, 4095, 4096):
+        tokens = 16 if n <= 2048 else 32
+        pairs = 2 * (((n + tokens - 1) // tokens) // 2)
+        rows = 8 * tokens
+        assert lib.miso_attn_prefill_workspace_bytes(n) == 1024 + pairs * 2 * rows * 258 * 4
     assert max(lib.miso_attn_prefill_workspace_bytes(n) for n in range(1, 4200, 7)) == \
-        lib.miso_attn_prefill_workspace_bytes(2048)
+        lib.miso_attn_prefill_workspace_bytes(4096)

@@ -7,8 +7,10 @@ configs C3 (2048 tokens, empty cache; every row) and C4 (8192 tokens after an 81
 a deterministic row sample covering first/last tiles and diagonal tiles), plus two size-free
 properties: chunked prefill equals one-shot prefill, and prefill row t equals decode at pos0+t+1.
 The balanced form (miso_attn_prefill_ws: heavy token blocks split between two workgroups, the
-parts merged through a workspace) is checked the same way, on shapes with and without split
-blocks, plus run-to-run bit equality and reuse of one workspace across sizes.
+parts merged through a workspace; 16-token blocks up to 2048 tokens, 32-token blocks from 3841
+to 4096)
+is checked the same way, on shapes with and without split blocks, plus run-to-run bit equality
+and reuse of one workspace across sizes.
 Gate: |got - ref| <= 2e-3 + 1e-2 |ref| for every element (f32 output).
 """
 from __future__ import annotations
@@ -152,8 +154,8 @@ def balanced_rows(pos0, n):
 
 
 @pytest.mark.parametrize("pos0,n", [(0, 1), (0, 16), (0, 17), (0, 48), (0, 129), (0, 300),
-                                    (7, 999), (100, 1500), (3000, 600), (1, 2047),
-                                    (0, 2049), (500, 4000)])
+                                    (7, 999), (100, 1500), (3000, 600), (1, 2047), (0, 2049),
+                                    (0, 3841), (500, 4000), (0, 4096), (4096, 4096)])
 def test_prefill_balanced_matches_oracle(O, attn, torch_mod, prefill_scratch, pos0, n):
     check(O, attn, torch_mod, pos0, n, rows=balanced_rows(pos0, n), name="balanced",
           scratch=prefill_scratch)
@@ -184,10 +186,10 @@ def test_prefill_balanced_repeatable(O, attn, torch_mod, prefill_scratch):
     assert not np.array_equal(first, plain)  # the split blocks did merge two parts
 
 
-@pytest.mark.parametrize("n", [2049, 4096])
+@pytest.mark.parametrize("n", [2049, 3840, 4097])
 def test_prefill_balanced_wide_is_plain(O, attn, torch_mod, prefill_scratch, n):
-    """Past 2048 tokens the balanced entry runs the one-block-per-workgroup layout (one and two
-    row blocks per wave), bit-equal to miso_attn_prefill."""
+    """Outside the balanced form's sizes the balanced entry runs the one-workgroup-per-block
+    layout, bit-equal to miso_attn_prefill."""
     torch = torch_mod
     p = O.prefill_inputs(n, 0, n, n, q_scale=1.0)
     assert attn.prefill_workspace_bytes(n) == 0
