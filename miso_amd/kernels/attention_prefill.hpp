@@ -924,7 +924,7 @@ __device__ __attribute__((always_inline)) inline void prefill_items(
         l_row[c] = cdna4::sum_xor32(rw.l[c]);
       // A part of a split block: its partial to the workspace (rows of O relative to 2^m, and
       // (m, l) per row), then the agent-scope counter of the pair; the part that arrives second
-      // merges. Merged rows: O = O_A f_A + O_B f_B, f_X = 2^(m_X - M) / (l_A 2^(m_A - M) +
+      // merges (one that finds the counter already set merges without writing its own). Merged rows: O = O_A f_A + O_B f_B, f_X = 2^(m_X - M) / (l_A 2^(m_A - M) +
       // l_B 2^(m_B - M)), M the larger m, evaluated in this order whichever part merges (the
       // output does not depend on which part arrives second).
       //
@@ -952,28 +952,36 @@ __device__ __attribute__((always_inline)) inline void prefill_items(
           const auto o_rsrc = part_rsrc(sp->part_o, part_rows * kDim);
           const auto ml_rsrc = part_rsrc(sp->part_ml, part_rows * 2);
           const unsigned row0 = jb.slot * kPartRows + 32 * kBlocks * wave;
-#pragma unroll
-          for (int c = 0; c < kBlocks; ++c) {
-            stage_o(c, 1.0f);
-            if (hi == 0)
-              __builtin_amdgcn_raw_buffer_store_b64(
-                  __builtin_bit_cast(cdna4::u32x2_t, float2{rw.m[c], l_row[c]}), ml_rsrc,
-                  (row0 + 32 * c + col) * 8, 0, kSc1);
-#pragma unroll
-            for (int r = 0; r < 32; ++r)
-              __builtin_amdgcn_raw_buffer_store_b128(
-                  __builtin_bit_cast(cdna4::u32x4_t, staged_row(r)), o_rsrc,
-                  (row0 + 32 * c + r) * 1024 + 16 * lane, 0, kSc1);
-          }
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          __syncthreads();
-          const unsigned flag = lds0 + 4 * 32 * kStageRow;  // past every wave's staging
+          auto* flag = reinterpret_cast<__attribute__((address_space(3))) unsigned*>(
+              lds0 + 4 * 32 * kStageRow);  // past every wave's staging
           unsigned* counter = sp->counters + jb.slot / 2;
+          // If the other part has published already, merge without publishing this one.
           if (t == 0)
-            *reinterpret_cast<__attribute__((address_space(3))) unsigned*>(flag) =
-                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __syncthreads();
-          store = *reinterpret_cast<const __attribute__((address_space(3))) unsigned*>(flag) != 0;
+          store = *flag != 0;
+          if (!store) {  // uniform
+#pragma unroll
+            for (int c = 0; c < kBlocks; ++c) {
+              stage_o(c, 1.0f);
+              if (hi == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    __builtin_bit_cast(cdna4::u32x2_t, float2{rw.m[c], l_row[c]}), ml_rsrc,
+                    (row0 + 32 * c + col) * 8, 0, kSc1);
+#pragma unroll
+              for (int r = 0; r < 32; ++r)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(cdna4::u32x4_t, staged_row(r)), o_rsrc,
+                    (row0 + 32 * c + r) * 1024 + 16 * lane, 0, kSc1);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // every wave's partial complete, and the flag read
+            if (t == 0)
+              *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            store = *flag != 0;
+          }
           if (store) {  // uniform: the other part's partial is complete
             if (t == 0)  // every launch leaves the counters zero
               __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
