@@ -169,15 +169,19 @@ def test_prefill_balanced_c3_all_rows(O, attn, torch_mod, prefill_scratch):
 
 def test_prefill_balanced_repeatable(O, attn, torch_mod, prefill_scratch):
     """Bit-equal across calls (the merge does not depend on which part arrives second), one
-    workspace across sizes, and within the gate of the one-block-per-workgroup form."""
+    workspace across sizes and across the 16- and 32-token block layouts (whose partial regions
+    differ), and within the gate of the one-block-per-workgroup form."""
     torch = torch_mod
     p = O.prefill_inputs(777, 0, 2048, 2048, q_scale=1.0)
     first = run_prefill(attn, torch, p, scratch=prefill_scratch)
     small = O.prefill_inputs(778, 40, 333, 400, q_scale=2.0)
     a = run_prefill(attn, torch, small, scratch=prefill_scratch)
+    wide = O.prefill_inputs(779, 0, 4096, 4096, q_scale=1.0)
+    w = run_prefill(attn, torch, wide, scratch=prefill_scratch)
     for _ in range(3):
         again = run_prefill(attn, torch, p, scratch=prefill_scratch)
         assert np.array_equal(again, first)
+        assert np.array_equal(run_prefill(attn, torch, wide, scratch=prefill_scratch), w)
     assert np.array_equal(run_prefill(attn, torch, small, scratch=prefill_scratch), a)
     plain = run_prefill(attn, torch, p)
     st = O.compare(first, plain.astype(np.float64))
