@@ -101,6 +101,10 @@ __host__ __device__ inline unsigned attn_prefill_items(unsigned n) {
 // ------------------------------------------------------------------------------------------------
 
 constexpr unsigned kAttnSplitMinTiles = 4;
+// Tiles moved from B's share of a split pair to A's, for 16- and 32-token blocks (B pays a second
+// query prologue and the light block's output; measured best: none with 16-token blocks, ~1%
+// for 4 with 32-token blocks).
+constexpr unsigned kAttnSplitBias = 0, kAttnSplitBias2 = 4;
 constexpr unsigned kAttnBalancedMaxItems = 256;  // CUs of an MI355X
 
 // Workspace of the balanced form: one counter per pair (a fixed region of kAttnSplitMaxPairs, so
@@ -639,7 +643,8 @@ __device__ __attribute__((always_inline)) inline unsigned item_jobs(const AttnPr
     }
     const unsigned hb = blocks - 1 - pair, lb = pair;
     const unsigned th = block_tiles<kTokens>(p, hb), tl = block_tiles<kTokens>(p, lb);
-    const unsigned cut = (th + tl + 1) / 2;
+    const unsigned bias = kTokens == kAttnQBlock ? kAttnSplitBias : kAttnSplitBias2;
+    const unsigned cut = (th + tl + 1) / 2 + bias;
     // Tiles every row of the heavy block sees in full: the split point stays among them.
     const unsigned full = (p.pos0 + hb * kTokens + 1) / kKeys;
     if (cut + kAttnSplitMinTiles > th || cut > full) {
@@ -924,7 +929,8 @@ __device__ __attribute__((always_inline)) inline void prefill_items(
         l_row[c] = cdna4::sum_xor32(rw.l[c]);
       // A part of a split block: its partial to the workspace (rows of O relative to 2^m, and
       // (m, l) per row), then the agent-scope counter of the pair; the part that arrives second
-      // merges (one that finds the counter already set merges without writing its own). Merged rows: O = O_A f_A + O_B f_B, f_X = 2^(m_X - M) / (l_A 2^(m_A - M) +
+      // merges (one that finds the counter already set merges without writing its own).
+      // Merged rows: O = O_A f_A + O_B f_B, f_X = 2^(m_X - M) / (l_A 2^(m_A - M) +
       // l_B 2^(m_B - M)), M the larger m, evaluated in this order whichever part merges (the
       // output does not depend on which part arrives second).
       //
