@@ -630,9 +630,12 @@ int miso_attn_gemm(const uint8_t* w, int format, const uint16_t* xh, const float
     return fail("miso_attn_gemm", "ldy must be >= n_rows");
   const k::QGemmParams p{w, reinterpret_cast<const _Float16*>(xh), xs, y, k, n_rows, n_tok, ldy};
   const unsigned grid = k::qgemm_tiles(n_rows, n_tok);
-  if (format == 0)
-    k::qgemm_kernel<k::QFormat::Q4K><<<grid, 256, 0, as_stream(stream)>>>(p);
-  else if (format == 1)
+  if (format == 0) {
+    if (const unsigned big = k::qgemm_big_tiles(n_rows, n_tok))
+      k::qgemm_q4k_big_kernel<><<<big, 256, 0, as_stream(stream)>>>(p);
+    else
+      k::qgemm_kernel<k::QFormat::Q4K><<<grid, 256, 0, as_stream(stream)>>>(p);
+  } else if (format == 1)
     k::qgemm_kernel<k::QFormat::Q6K><<<grid, 256, 0, as_stream(stream)>>>(p);
   else
     return fail("miso_attn_gemm", "format must be 0 (Q4_K) or 1 (Q6_K)");

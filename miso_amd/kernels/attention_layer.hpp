@@ -217,9 +217,12 @@ inline const char* gemm(const Matrix& w, const _Float16* xh, const float* xs, un
     return "GEMM k must be a multiple of 256";
   const QGemmParams p{w.data, xh, xs, y, w.k, w.n, n_tok, ldy};
   const unsigned grid = qgemm_tiles(w.n, n_tok);
-  if (w.format == Format::Q4K)
-    qgemm_kernel<QFormat::Q4K><<<grid, 256, 0, stream>>>(p);
-  else if (w.format == Format::Q6K)
+  if (w.format == Format::Q4K) {
+    if (const unsigned big = qgemm_big_tiles(w.n, n_tok))
+      qgemm_q4k_big_kernel<><<<big, 256, 0, stream>>>(p);
+    else
+      qgemm_kernel<QFormat::Q4K><<<grid, 256, 0, stream>>>(p);
+  } else if (w.format == Format::Q6K)
     qgemm_kernel<QFormat::Q6K><<<grid, 256, 0, stream>>>(p);
   else
     return "weight format must be Q4_K (0) or Q6_K (1)";

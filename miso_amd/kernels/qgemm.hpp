@@ -16,8 +16,8 @@
 // GEMM: a workgroup computes a 64-token x 64-row tile with v_mfma_f32_32x32x16_f16, each of its 4
 // waves a 32 x 32 quarter (the lane's accumulator column is one weight row, so per-row scales are
 // per-lane scalars). K advances in stages of 128. Per stage every thread fetches (two stages
-// ahead, into registers) 64 bytes of the x tile and one 16-byte run of one row's quantized weights, and
-// expands the weights into LDS as exact f16 integers:
+// ahead, into registers) 64 bytes of the x tile and one 16-byte run of one row's quantized
+// weights, and expands the weights into LDS as exact f16 integers:
 //   Q4_K: q sc (<= 945) per weight through the 1024-exponent convert and one fused v_pk_fma_f16;
 //         a block's partial C (16 MFMAs over its 256 k) is scaled by the row's d, and the block's
 //         dmin m term is one more MFMA: A = the tokens' 8 sub-block sums of the block, each split
@@ -29,6 +29,11 @@
 // Workgroups are mapped to tiles in groups of 8 token tiles swept across the row tiles, each XCD
 // a contiguous part of that order, so an XCD's activations and weights are read from the memory
 // side about once and reused through its L2.
+//
+// Q4_K products with at least 256 tiles of 128 x 128 can run qgemm_q4k_big_kernel instead (no
+// reference counterpart; qgemm_big_tiles gives its grid, 0 where it does not pay): each wave a
+// 64 x 64 quarter, so an LDS operand read feeds two MFMAs, with the dequantizing store of the
+// next stage in the same step as the MFMAs; results bit-identical to qgemm_kernel's.
 
 #include <hip/hip_runtime.h>
 
@@ -212,12 +217,13 @@ __device__ __attribute__((always_inline)) inline half2_t split(float v) {
 
 // Writes a fetched stage into the stage-parity buffers (and, for Q4_K, its block's min-term
 // operands and scales into the block-parity ones; both stages of a block write the same values,
-// which are read only after the block's second barrier).
-template <QFormat F>
-__device__ inline void store(const Fetch<F>& f, Lds& sm, unsigned s, unsigned t, bool tok_ok,
-                             bool row_ok) {
+// which are read only after the block's second barrier). The thread's token and row go to tile
+// row off + t / 4.
+template <QFormat F, class L = Lds>
+__device__ inline void store(const Fetch<F>& f, L& sm, unsigned s, unsigned t, bool tok_ok,
+                             bool row_ok, unsigned off = 0) {
   using q4k_gemv_detail::spread_bytes;
-  const unsigned tok = t >> 2, q = t & 3u, buf = s & 1u;
+  const unsigned tok = off + (t >> 2), q = t & 3u, buf = s & 1u;
   const u32x4 zero{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -308,13 +314,14 @@ __device__ __attribute__((always_inline)) inline unsigned xcd_tile(unsigned b, u
 // once per group, where a row tile swept across all token tiles would re-read the whole activation
 // matrix from the memory side for every row tile.
 constexpr unsigned kGroupTok = 8;
+template <unsigned kGroup = kGroupTok>
 __device__ __attribute__((always_inline)) inline void grouped_tile(unsigned t, unsigned n_ttiles,
                                                                   unsigned n_rtiles,
                                                                   unsigned& ttile,
                                                                   unsigned& rtile) {
-  const unsigned per_group = kGroupTok * n_rtiles;
-  const unsigned first_tok = t / per_group * kGroupTok, in = t % per_group;
-  const unsigned width = n_ttiles - first_tok < kGroupTok ? n_ttiles - first_tok : kGroupTok;
+  const unsigned per_group = kGroup * n_rtiles;
+  const unsigned first_tok = t / per_group * kGroup, in = t % per_group;
+  const unsigned width = n_ttiles - first_tok < kGroup ? n_ttiles - first_tok : kGroup;
   ttile = first_tok + in % width;
   rtile = in / width;
 }
@@ -391,22 +398,146 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const QGemmParam
   }
 }
 
-}  // namespace qgemm_detail
+// ---- Q4_K in 128 x 128 tiles (no reference counterpart) ----
+// A workgroup computes 128 tokens x 128 rows, each wave a 64 x 64 quarter (2 x 2 MFMA blocks),
+// so every operand read from LDS feeds two MFMAs instead of one. A stage's tiles are the 64 x 64
+// fetch and store above done twice, at tile rows 0 and 64, and the store of stage s + 1 runs in
+// the same step as the MFMAs of stage s, into the other buffer. Per output element the
+// arithmetic is gemm_tile's in the same order, so both tile shapes give bit-identical results.
+// The LDS (148 KiB) allows one workgroup per CU, against two for the 64 x 64 tiles, so these
+// tiles pay only when they alone fill the chip (qgemm_big_tiles).
+constexpr unsigned kBig = 128, kBigGroupTok = 4;
 
-// Output tiles [first, first + count) of 64 tokens x 64 rows, in grouped_tile's order.
+struct alignas(16) LdsBig {
+  _Float16 x[2][kBig * kBK];
+  _Float16 w[2][kBig * kBK];
+  _Float16 xm[2][kBig][16];
+  _Float16 wm[2][kBig][16];
+  float dd[2][kBig][4];
+};
+
+__device__ __attribute__((always_inline)) inline void gemm_tile_big(const QGemmParams& p,
+                                                                    LdsBig& sm, unsigned m0,
+                                                                    unsigned n0) {
+  constexpr QFormat F = QFormat::Q4K;
+  const unsigned t = threadIdx.x, lane = t % 64, wave = t / 64;
+  const unsigned wt = wave >> 1, wr = wave & 1u, kq = lane / 32;
+  unsigned ar[2], br[2];  // the lane's token rows and weight rows in the tile, per MFMA block
+#pragma unroll
+  for (unsigned i = 0; i < 2; ++i) {
+    ar[i] = 64 * wt + 32 * i + lane % 32;
+    br[i] = 64 * wr + 32 * i + lane % 32;
+  }
+  const unsigned n_stages = p.k / kBK;
+  bool tok_ok[2], row_ok[2];
+#pragma unroll
+  for (unsigned h = 0; h < 2; ++h) {
+    tok_ok[h] = m0 + 64 * h + t / 4 < p.n_tok;
+    row_ok[h] = n0 + 64 * h + t / 4 < p.n_rows;
+  }
+  auto fetch2 = [&](Fetch<F> (&f)[2], unsigned s) __attribute__((always_inline)) {
+    f[0] = fetch<F>(p, n0, m0, s, t);
+    f[1] = fetch<F>(p, n0 + 64, m0 + 64, s, t);
+  };
+  auto store2 = [&](const Fetch<F> (&f)[2], unsigned s) __attribute__((always_inline)) {
+    store<F, LdsBig>(f[0], sm, s, t, tok_ok[0], row_ok[0], 0);
+    store<F, LdsBig>(f[1], sm, s, t, tok_ok[1], row_ok[1], 64);
+  };
+  float16_t acc[2][2], c[2][2];
+#pragma unroll
+  for (unsigned i = 0; i < 2; ++i)
+#pragma unroll
+    for (unsigned j = 0; j < 2; ++j)
+      acc[i][j] = c[i][j] = float16_t{};
+  // Two register sets, even and odd stages, each requested two stages before its store.
+  Fetch<F> fa[2], fb[2];
+  fetch2(fa, 0);
+  asm volatile("" : : : "memory");  // stage 0's loads are issued before stage 1's
+  fetch2(fb, 1);
+  store2(fa, 0);
+  fetch2(fa, 2);
+  auto step = [&](Fetch<F> (&fn)[2], unsigned s) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage s complete in its buffer, and every wave done with the other one (stage s - 1).
+    __syncthreads();
+    if (s + 1 < n_stages) {  // uniform
+      store2(fn, s + 1);
+      fetch2(fn, s + 3);  // past the last stage: re-reads it, never stored
+    }
+    const unsigned buf = s & 1u;
+#pragma unroll
+    for (unsigned kk = 0; kk < kBK / 16; ++kk) {
+      half8_t a[2], b[2];
+#pragma unroll
+      for (unsigned i = 0; i < 2; ++i) {
+        a[i] = *reinterpret_cast<const half8_t*>(sm.x[buf] + chunk_at(ar[i], 2 * kk + kq));
+        b[i] = *reinterpret_cast<const half8_t*>(sm.w[buf] + chunk_at(br[i], 2 * kk + kq));
+      }
+#pragma unroll
+      for (unsigned i = 0; i < 2; ++i)
+#pragma unroll
+        for (unsigned j = 0; j < 2; ++j)
+          c[i][j] = mfma(a[i], b[j], c[i][j]);
+    }
+    if (s % 2 == 1) {  // the block's last stage: its dmin m term, then its d scale
+      const unsigned bb = (s / 2) & 1u;
+#pragma unroll
+      for (unsigned j = 0; j < 2; ++j) {
+        const half8_t bm = *reinterpret_cast<const half8_t*>(&sm.wm[bb][br[j]][8 * kq]);
+        const float d = sm.dd[bb][br[j]][0], dmin = sm.dd[bb][br[j]][1];
+#pragma unroll
+        for (unsigned i = 0; i < 2; ++i) {
+          const half8_t am = *reinterpret_cast<const half8_t*>(&sm.xm[bb][ar[i]][8 * kq]);
+          const float16_t mins = mfma(am, bm, float16_t{});
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            acc[i][j][r] = __builtin_fmaf(d, c[i][j][r], acc[i][j][r]);
+            acc[i][j][r] = __builtin_fmaf(-dmin, mins[r], acc[i][j][r]);
+          }
+          c[i][j] = float16_t{};
+        }
+      }
+    }
+  };
+  for (unsigned s = 0; s < n_stages; s += 2) {  // n_stages is even (k % 256 == 0)
+    step(fb, s);
+    step(fa, s + 1);
+  }
+  // Lane (row br[j], half kq) holds tokens 8 (r / 4) + 4 kq + r % 4 of token block i.
+#pragma unroll
+  for (unsigned j = 0; j < 2; ++j) {
+    const unsigned n = n0 + br[j];
+#pragma unroll
+    for (unsigned i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const unsigned tok = m0 + 64 * wt + 32 * i + 8 * (r / 4) + 4 * kq + r % 4;
+        if (tok < p.n_tok && n < p.n_rows)
+          p.y[std::size_t{tok} * p.ldy + n] = acc[i][j][r];
+      }
+  }
+}
+
+// The 64 x 64 tiles [first, first + count), in grouped_tile's order.
 template <QFormat F>
-__device__ void qgemm_op(const QGemmParams& p, unsigned first, unsigned count) {
-  using namespace qgemm_detail;
-  __shared__ Lds sm;
+__device__ inline void gemm_small(const QGemmParams& p, unsigned first, unsigned count, Lds& sm) {
   const unsigned n_ttiles = (p.n_tok + kBM - 1) / kBM, n_rtiles = (p.n_rows + kBN - 1) / kBN;
   for (unsigned i = blockIdx.x; i < count; i += gridDim.x) {
     const unsigned tile = first + (gridDim.x == count ? xcd_tile(i, count) : i);
     unsigned ttile, rtile;
     grouped_tile(tile, n_ttiles, n_rtiles, ttile, rtile);
-    const unsigned m0 = ttile * kBM, n0 = rtile * kBN;
-    gemm_tile<F, 0>(p, sm, m0, n0);
+    gemm_tile<F, 0>(p, sm, ttile * kBM, rtile * kBN);
     __syncthreads();  // the next tile's first stores reuse buffer 0
   }
+}
+
+}  // namespace qgemm_detail
+
+// Output tiles [first, first + count) of 64 tokens x 64 rows, in grouped_tile's order.
+template <QFormat F>
+__device__ void qgemm_op(const QGemmParams& p, unsigned first, unsigned count) {
+  __shared__ qgemm_detail::Lds sm;
+  qgemm_detail::gemm_small<F>(p, first, count, sm);
 }
 
 __host__ __device__ inline unsigned qgemm_tiles(unsigned n_rows, unsigned n_tok) {
@@ -417,6 +548,34 @@ __host__ __device__ inline unsigned qgemm_tiles(unsigned n_rows, unsigned n_tok)
 template <QFormat F>
 __global__ void __launch_bounds__(qgemm_detail::kThreads) qgemm_kernel(QGemmParams p) {
   qgemm_op<F>(p, 0, qgemm_tiles(p.n_rows, p.n_tok));
+}
+
+// Workgroups for a Q4_K product in 128 x 128 tiles, or 0 where 64 x 64 tiles are faster (at most
+// 64 tokens, or fewer 128 x 128 tiles than the 256 CUs: the 64 x 64 kernel then runs two
+// workgroups per CU). No reference counterpart: callers that know it launch
+// qgemm_q4k_big_kernel on this many workgroups of 256 threads, else qgemm_kernel<Q4K>.
+__host__ __device__ inline unsigned qgemm_big_tiles(unsigned n_rows, unsigned n_tok) {
+  using namespace qgemm_detail;
+  const unsigned tiles = (n_rows + kBig - 1) / kBig * ((n_tok + kBig - 1) / kBig);
+  return n_tok > kBM && tiles >= 256 ? tiles : 0;
+}
+
+// The whole Q4_K product in 128 x 128 tiles (grid-stride over qgemm_big_tiles' tile count, in
+// grouped_tile's order with groups of 4 token tiles). A template, so several translation units
+// may include this header.
+template <int = 0>
+__global__ void __launch_bounds__(qgemm_detail::kThreads) qgemm_q4k_big_kernel(QGemmParams p) {
+  using namespace qgemm_detail;
+  __shared__ LdsBig sm;
+  const unsigned n_ttiles = (p.n_tok + kBig - 1) / kBig, n_rtiles = (p.n_rows + kBig - 1) / kBig;
+  const unsigned count = n_ttiles * n_rtiles;
+  for (unsigned i = blockIdx.x; i < count; i += gridDim.x) {
+    const unsigned tile = gridDim.x == count ? xcd_tile(i, count) : i;
+    unsigned ttile, rtile;
+    grouped_tile<kBigGroupTok>(tile, n_ttiles, n_rtiles, ttile, rtile);
+    gemm_tile_big(p, sm, ttile * kBig, rtile * kBig);
+    __syncthreads();  // the next tile's first stores reuse buffer 0
+  }
 }
 
 }  // namespace miso::kernels

@@ -11,7 +11,8 @@ Cases: the reference's fixture tensors (Q4_K K = 8192 N = 2, Q6_K K = 4096 N = 4
 tests/test_qgemm.hip:199-208), the attention's projections on random blocks (attn_q 2048 -> 8192,
 attn_k 2048 -> 512, attn_output 4096 -> 2048, attn_v Q6_K 2048 -> 512) with token counts that
 leave partial tiles, one token, a row stride ldy > n_rows with canaries past each row, and the
-Python layer's reference error messages.
+Python layer's reference error messages. Q4_K's 128-token tiles equal its 64 x 64 tiles bit for
+bit.
 """
 from __future__ import annotations
 
@@ -100,7 +101,8 @@ def test_reference_fixtures(O, attn, torch_mod):
 
 
 @pytest.mark.parametrize("k,n,n_tok", [(2048, 8192, 130), (2048, 512, 70), (4096, 2048, 200),
-                                       (2048, 1001, 129), (4096, 37, 1), (8192, 100, 65)])
+                                       (2048, 1001, 129), (4096, 37, 1), (8192, 100, 65),
+                                       (2048, 2048, 2048)])
 def test_q4k_shapes(O, attn, torch_mod, k, n, n_tok):
     rng = np.random.default_rng(k + 7 * n + n_tok)
     check(O, attn, torch_mod, "q4_k", random_blocks(rng, n, k), n, k, xs_normal(rng, n_tok, k),
@@ -112,6 +114,36 @@ def test_q6k_shapes(O, attn, torch_mod, k, n, n_tok):
     rng = np.random.default_rng(3 * k + n + n_tok)
     check(O, attn, torch_mod, "q6_k", random_q6k_blocks(rng, n, k), n, k, xs_normal(rng, n_tok, k),
           "random")
+
+
+@pytest.mark.parametrize("k,n,n_tok", [(2048, 8192, 600), (2048, 2000, 2100)])
+def test_q4k_token_tiles_bit_identical(O, attn, torch_mod, k, n, n_tok):
+    """Q4_K runs 128 x 128 tiles (qgemm_q4k_big_kernel) when they give every CU one, as in both
+    cases here (the last token tile partial in both, the last row tile in the second); at most
+    64 tokens always run 64 x 64 tiles (qgemm_kernel). Each output element is the same arithmetic
+    in the same order either way, so the product equals, bit for bit, the same product computed
+    64 tokens at a time."""
+    torch = torch_mod
+    rng = np.random.default_rng(k + n + n_tok)
+    r1 = to_dev(torch, O.q4k_repack_r1(random_blocks(rng, n, k)))
+    x = xs_normal(rng, n_tok, k)
+    ldy = n + 3
+
+    def product(xc):
+        inp = attn.GemmInput(xc.shape[0], k)
+        attn.gemm_input(to_dev(torch, xc.reshape(-1)), k, xc.shape[0], inp)
+        y = torch.full((xc.shape[0] * ldy,), CANARY, dtype=torch.float32, device="cuda")
+        attn.gemm(r1, "q4_k", n, k, inp, y, ldy)
+        torch.cuda.synchronize()
+        return to_host(y).reshape(xc.shape[0], ldy)
+
+    whole = product(x)
+    parts = np.concatenate([product(x[t:t + 64]) for t in range(0, n_tok, 64)])
+    print(f"[qgemm tiles] N={n} K={k} tokens={n_tok}: "
+          f"{int((whole != parts).sum())} elements differ", flush=True)
+    assert (whole[:, n:] == CANARY).all(), "write past n_rows"
+    assert np.isfinite(whole[:, :n]).all()
+    assert np.array_equal(whole, parts)
 
 
 def test_full_row_stride_and_tile_edges(O, attn, torch_mod):
