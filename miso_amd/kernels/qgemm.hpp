@@ -460,10 +460,10 @@ __device__ __attribute__((always_inline)) inline void gemm_tile_big(const QGemmP
     __builtin_amdgcn_sched_barrier(0);
     // Stage s complete in its buffer, and every wave done with the other one (stage s - 1).
     __syncthreads();
-    if (s + 1 < n_stages) {  // uniform
-      store2(fn, s + 1);
-      fetch2(fn, s + 3);  // past the last stage: re-reads it, never stored
-    }
+    // Also at the last stage (a re-read of it into the buffer and block parity nothing reads
+    // again), so that the store shares one scheduling region with the MFMAs.
+    store2(fn, s + 1);
+    fetch2(fn, s + 3);  // past the last stage: re-reads it
     const unsigned buf = s & 1u;
 #pragma unroll
     for (unsigned kk = 0; kk < kBK / 16; ++kk) {
