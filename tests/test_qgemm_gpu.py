@@ -116,13 +116,13 @@ def test_q6k_shapes(O, attn, torch_mod, k, n, n_tok):
           "random")
 
 
-@pytest.mark.parametrize("k,n,n_tok", [(2048, 8192, 600), (2048, 2000, 2100)])
+@pytest.mark.parametrize("k,n,n_tok", [(2048, 8192, 600), (2048, 2000, 2100), (4096, 2048, 2048)])
 def test_q4k_token_tiles_bit_identical(O, attn, torch_mod, k, n, n_tok):
-    """Q4_K runs 128 x 128 tiles (qgemm_q4k_big_kernel) when they give every CU one, as in both
-    cases here (the last token tile partial in both, the last row tile in the second); at most
-    64 tokens always run 64 x 64 tiles (qgemm_kernel). Each output element is the same arithmetic
-    in the same order either way, so the product equals, bit for bit, the same product computed
-    64 tokens at a time."""
+    """Q4_K runs 128 x 128 tiles (qgemm_q4k_big_kernel) when they give every CU one, as in every
+    case here (the last token tile partial in the first two, the last row tile in the second; the
+    third is attn_output's shape, k = 4096); at most 64 tokens always run 64 x 64 tiles
+    (qgemm_kernel). Each output element is the same arithmetic in the same order either way, so
+    the product equals, bit for bit, the same product computed 64 tokens at a time."""
     torch = torch_mod
     rng = np.random.default_rng(k + n + n_tok)
     r1 = to_dev(torch, O.q4k_repack_r1(random_blocks(rng, n, k)))
