@@ -74,6 +74,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-other", action="store_true", help="skip the C1 / C3 / C5 lines")
+    ap.add_argument("--split-valu", action="store_true",
+                    help="with --no-other: still time the VALU form of the C2 split (for "
+                         "counter runs of both split forms)")
     ap.add_argument("--no-device", action="store_true",
                     help="skip the rocm-smi / amd-smi readings (implied under a profiler)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -196,7 +199,38 @@ def eager_loop():
     lib.miso_bench_decode.restype = ctypes.c_double
     lib.miso_bench_decode.argtypes = [i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i32,
                                       vp, vp, vp, vp, u32, u32, u32, i32, i32, vp]
+    lib.miso_bench_layer_decode.restype = ctypes.c_double
+    lib.miso_bench_layer_decode.argtypes = [vp, vp, vp, u32, u32, vp, vp, ctypes.c_float, vp, i32,
+                                            vp]
     return lib
+
+
+def bench_combine_curve(torch, A, lib, inputs):
+    """The combine alone against the split count, as the reference's bench/attention/
+    bench_combine.hip:15-67 measures it: partials m ~ 10 U(-1, 1), l ~ 1 + 16 |U(-1, 1)|,
+    o ~ U(-1, 1), gate ~ U(-1, 1) (own generator), 300 untimed then 2000 timed back-to-back
+    launches between two events, median of 3 runs; us per launch."""
+    q, qg, caches = inputs
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(71)
+    cap = 129
+    u = lambda n: torch.rand(n, generator=gen, device="cuda") * 2 - 1
+    m = u(2 * cap * 8) * 10
+    l_ = 1 + u(2 * cap * 8).abs() * 16
+    o = u(2 * cap * 8 * 256)
+    g = u(16 * 512)
+    core = torch.empty(H * D, device="cuda")
+    sc = type("Partials", (), {"part_m": m, "part_l": l_, "part_o": o})()
+    curve = {}
+    for ns in (1, 16, 22, 57, 60, 65, 128, 129):
+        runs = sorted(eager_decode(torch, lib, 2, q, g, caches[:1], core, sc, 0, ns, 300, 2000)
+                      for _ in range(3))
+        curve[str(ns)] = round(runs[1] * 1e3, 3)
+    log(f"combine alone (us per launch by split count): {curve}")
+    return {"workload": "attn_combine_kernel<64,true,4><<<64,64>>> alone over random partials, "
+                        "by split count (the reference's bench/attention/bench_combine.hip "
+                        "method: 300 warm + 2000 timed launches, median of 3 runs)",
+            "us_by_splits": curve}
 
 
 def eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits, warmup, iters):
@@ -263,21 +297,29 @@ def bench_decode(torch, A, args, inputs, max_splits, f16_query=False, label="C2"
     timing = "graph"
     t_step, t_split, t_comb = g_step_t, g_split_t, g_comb_t
     lib = eager_loop()
+    windows = None
     if lib is not None:
         timing = "eager"
-        ev = lambda mode: eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits,
-                                       args.warmup, steps)
-        t_step = ev(3 if f16_query else 0)
-        t_comb = ev(2)
-        t_split = ev(1) if not f16_query else t_step - t_comb
-        log(f"decode {label} (eager): step {t_step * 1e3:.2f} us, split {t_split * 1e3:.2f} us, "
-            f"combine {t_comb * 1e3:.2f} us")
+        windows = {}
+
+        def ev(mode, name):
+            # the median of three eager windows of `steps` calls each
+            w = [eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits, args.warmup,
+                              steps) for _ in range(3)]
+            windows[name] = [round(x * 1e3, 3) for x in w]
+            return sorted(w)[1]
+
+        t_step = ev(3 if f16_query else 0, "step")
+        t_comb = ev(2, "combine")
+        t_split = ev(1, "split") if not f16_query else t_step - t_comb
+        log(f"decode {label} (eager, median of 3 windows): step {t_step * 1e3:.2f} us "
+            f"{windows['step']}, split {t_split * 1e3:.2f} us, combine {t_comb * 1e3:.2f} us")
     step(0)
     torch.cuda.synchronize()
     return {
         "steps": steps, "t_step_ms": t_step, "t_split_ms": t_split, "t_comb_ms": t_comb,
         "graph_ms": {"step": g_step_t, "split": g_split_t, "combine": g_comb_t},
-        "timing": timing,
+        "timing": timing, "windows_us": windows,
         "kv_bytes": kv_bytes, "n_splits": n_splits, "L": L, "core0": core.cpu().numpy(),
     }
 
@@ -289,6 +331,7 @@ def decode_line(dec, workload):
             "combine_us": round(dec["t_comb_ms"] * 1e3, 3), "n_splits": dec["n_splits"],
             "timing": dec["timing"],
             "graph_us_per_step": round(dec["graph_ms"]["step"] * 1e3, 3),
+            "eager_windows_us": dec["windows_us"],
             "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
@@ -318,10 +361,12 @@ def bench_prefill(torch, A, args):
     log(f"prefill C4: {t:.3f} ms, {tflops:.1f} TFLOP/s")
     host = None
     if not args.no_cpu:
+        torch.cuda.synchronize()
         host = {
             "q": q.cpu().numpy(), "qg": qg.cpu().numpy(),
             "k": k.view(torch.int16).cpu().numpy().view("uint16"),
             "v": v.view(torch.int16).cpu().numpy().view("uint16"),
+            "core": core.cpu().numpy().reshape(n, H, D),  # the last timed call's output
         }
     return {"t_ms": t, "flop": flop, "tflops": tflops, "pos0": pos0, "n": n,
             "max_ctx": max_ctx, "host": host}
@@ -607,11 +652,41 @@ def bench_other(torch, A, args):
                                                   lws), 1)
     time_replays(torch, g, 1)
     tp = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / 3
+    curve = None
+    lib = eager_loop()
+    if lib is not None:
+        # The reference's layer decode curve (bench/attention/bench_attention.hip:15-33): 64
+        # eager decode steps between two events at each context, the cache growing by one row
+        # per step, in a cache of 32768 + 256 rows; the median of 3 windows.
+        import ctypes
+        mc = 32768 + 256
+        ck = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
+        cv = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
+        h1 = torch.full((2048,), 0.1, device="cuda")
+        curve = {}
+        for ctx in (16, 1024, 4096, 16384, 32768):
+            w = []
+            for _ in range(3):
+                torch.cuda.synchronize()
+                r = lib.miso_bench_layer_decode(
+                    ctypes.addressof(layer.c), ck.data_ptr(), cv.data_ptr(), ctx, mc,
+                    h1.data_ptr(), y.data_ptr(), 1e-6, lws.decode.data_ptr(), 64,
+                    torch.cuda.current_stream().cuda_stream)
+                if r < 0:
+                    raise RuntimeError(f"layer decode timing loop failed ({r})")
+                w.append(r)
+            curve[str(ctx)] = round(sorted(w)[1] * 1e3, 2)
+        del ck, cv
+        log(f"layer decode curve (us per token, eager): {curve}")
     out["F3_layer"] = {"workload": "one attention layer step through the engine wiring "
                                    "(miso_attn_layer_decode / _prefill): residual + RMSNorm, "
                                    "q/k/v projections, prep, attention, output projection; "
                                    "synthetic Q4_K / Q6_K weights of the engine's shapes",
                        "decode_ctx": Ld, "decode_us_per_step": round(tl * 1e3, 2),
+                       "decode_curve_us_per_token": curve,
+                       "decode_curve_method": "the reference's bench/attention/"
+                                              "bench_attention.hip: 64 eager steps per context "
+                                              "between two events, cache growing; median of 3",
                        "prefill_tokens": ntk, "prefill_pos0": p0,
                        "prefill_ms_per_chunk": round(tp, 3)}
     del layer, lws, lk, lv, hp, yp
@@ -710,26 +785,38 @@ def torch_mod():
 
 def cpu_prefill_baseline(pre):
     """FP64 oracle on a deterministic sample of C4 query rows (16 heads each), 16 threads:
-    batches of 64 rows spread over the 8192 tokens until about 10 s of CPU work."""
+    batches of 64 rows spread over the 8192 tokens until about 10 s of CPU work. Every oracle row
+    is also the check of the bench's own timed C4 output: the sampled rows must match it within
+    the north star's tolerance, or the bench fails (exit 3)."""
     import numpy as np
     from oracle import oracle as O
     h = pre["host"]
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     order = np.arange(pre["n"], dtype=np.uint32)
     order = order[np.argsort((order * 2654435761) % pre["n"], kind="stable")]  # spread, fixed
-    done, flop, t0 = 0, 0.0, time.perf_counter()
+    done, flop, t0, el = 0, 0.0, time.perf_counter(), 0.0
+    worst = {"max_abs": 0.0, "max_rel": 0.0, "rel_l2_head": 0.0, "n_bad": 0}
     while done < order.size:
         rows = np.sort(order[done:done + 64])
-        O.prefill_f64(h["q"], h["qg"], H * 2 * D, h["k"], h["v"], pre["pos0"], pre["max_ctx"],
-                      rows, threads=threads)
+        t1 = time.perf_counter()
+        ref = O.prefill_f64(h["q"], h["qg"], H * 2 * D, h["k"], h["v"], pre["pos0"],
+                            pre["max_ctx"], rows, threads=threads)
+        el += time.perf_counter() - t1
+        st = O.compare(h["core"][rows], ref)
+        for key in worst:
+            worst[key] = max(worst[key], st[key])
+        if not st["ok"]:
+            print(f"bench.py: the timed C4 prefill output disagrees with the FP64 oracle on rows "
+                  f"{rows[:4]}...: {st}", file=sys.stderr, flush=True)
+            sys.exit(3)
         flop += float(sum(4.0 * H * D * (pre["pos0"] + int(t) + 1) for t in rows))
         done += rows.size
         if time.perf_counter() - t0 >= 10.0:
             break
-    el = time.perf_counter() - t0
     return {"value": flop / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"C4 prefill: {done} query rows x 16 heads of the FP64 oracle (spread over "
-                      f"the 8192 tokens), {el:.1f} s on {threads} threads"}
+                      f"the 8192 tokens), {el:.1f} s on {threads} threads",
+            "gpu_output_check": {"rows": done, "ok": True, **worst}}
 
 
 def main():
@@ -753,6 +840,13 @@ def main():
     inputs = decode_caches(torch, args)
     dec = bench_decode(torch, A, args, inputs, args.max_splits)
     other = {}
+    if args.no_other and args.split_valu and eager_loop() is not None:
+        q, qg, caches = inputs
+        sc = A.DecodeScratch(args.max_splits)
+        core = torch.empty(H * D, device="cuda")
+        t_valu = eager_decode(torch, eager_loop(), 4, q, qg, caches, core, sc, args.ctx,
+                              dec["n_splits"], args.warmup, dec["steps"])
+        log(f"decode C2 split on VALU (eager): {t_valu * 1e3:.2f} us")
     if not args.no_other:
         d16 = bench_decode(torch, A, args, inputs, args.max_splits, f16_query=True,
                            label="C2 f16 query")
@@ -774,6 +868,7 @@ def main():
                 "split_us": round(t_valu * 1e3, 3),
                 "mfma_split_us": round(dec["t_split_ms"] * 1e3, 3),
                 "gbs": round(dec["kv_bytes"] / (t_valu * 1e-3) / 1e9, 1)}
+            other["C2_combine_by_splits"] = bench_combine_curve(torch, A, lib, inputs)
         d60 = bench_decode(torch, A, args, inputs, 60, label="C2 engine cap 60")
         other["C2_engine_cap60"] = decode_line(
             d60, "C2 at the engine's shipped partial capacity kMaxSplits = 60 "
@@ -809,9 +904,11 @@ def main():
             "ctx": dec["L"], "n_splits": dec["n_splits"], "kv_buffers_rotated": args.buffers,
             "step": "split kernel + combine kernel (one decode call)",
             "timing": dec["timing"] + (" (native loop of eager C ABI calls between two HIP "
-                                       "events, as bench/attention/bench_attention.hip)"
+                                       "events, as bench/attention/bench_attention.hip; the "
+                                       "median of 3 windows)"
                                        if dec["timing"] == "eager" else " (HIP graph replays)"),
             "graph_us_per_step": round(dec["graph_ms"]["step"] * 1e3, 3),
+            "eager_windows_us": dec["windows_us"],
             "arithmetic": "the reference's precision (kernels/attention_decode.hpp:150-221): f32 "
                           "query and softmax numerators, each carried as an exact f16 (hi, lo) "
                           "pair into v_mfma_f32_16x16x32_f16 against the f16 KV cache, f32 "

@@ -340,6 +340,13 @@ typedef struct miso_attn_layer {
 uint64_t miso_attn_layer_decode_ws(void);
 uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok);
 
+/* Where each step leaves the attention output before the output projection, as a float offset
+ * into its workspace: the engine's AttentionScratch::core (16 heads x 256 floats, the last decode
+ * step's) and AttentionPrefillScratch::core ([n][16][256], the last prefill chunk's), which its
+ * callers read (tests/test_attention.hip:68,104). */
+uint64_t miso_attn_layer_decode_core(void);
+uint64_t miso_attn_layer_prefill_core(uint32_t max_tok);
+
 /* The token at position len: h += delta (delta may be NULL), y = o(Attention(RMSNorm(h))), K/V
  * appended at len. Replaces attention_decode() (src/engine/attention.hip:76-114): RMSNorm, the
  * q / k / v projections in one launch (Q4_K q and k, Q6_K v; other mixes one GEMV each), prep,

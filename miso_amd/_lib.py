@@ -55,6 +55,8 @@ SIGNATURES = {
     "miso_attn_gemm": (c_int, [P, c_int, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_layer_decode_ws": (c_uint64, []),
     "miso_attn_layer_prefill_ws": (c_uint64, [c_uint32]),
+    "miso_attn_layer_decode_core": (c_uint64, []),
+    "miso_attn_layer_prefill_core": (c_uint64, [c_uint32]),
     "miso_attn_layer_decode": (c_int, [P, P, P, c_uint32, c_uint32, P, P, P, c_float, P, P]),
     "miso_attn_layer_prefill": (c_int, [P, P, P, c_uint32, c_uint32, c_uint32, P, P, P, c_float,
                                         P, c_uint32, P]),

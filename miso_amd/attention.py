@@ -541,6 +541,12 @@ class LayerWorkspace:
         # zero-filled once: the balanced prefill's pair counters sit at its end
         self.prefill = torch.zeros(max(1, int(lib.miso_attn_layer_prefill_ws(max_tok))),
                                    dtype=torch.float32, device=device)
+        # the attention output before the output projection (the engine's scratch.core /
+        # ps.core): the last decode step's [16 * 256], the last prefill chunk's [n][16 * 256]
+        at = int(lib.miso_attn_layer_decode_core())
+        self.decode_core = self.decode[at:at + 4096]
+        at = int(lib.miso_attn_layer_prefill_core(max_tok))
+        self.prefill_core = self.prefill[at:at + max_tok * 4096].view(max_tok, 4096)
 
 
 def _layer_cache(k_cache, v_cache, max_ctx: int):

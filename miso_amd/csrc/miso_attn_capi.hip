@@ -648,6 +648,12 @@ uint64_t miso_attn_layer_prefill_ws(uint32_t max_tok) {
   return k::layer::prefill_workspace_floats(max_tok);
 }
 
+uint64_t miso_attn_layer_decode_core(void) { return k::layer::decode_core_offset(); }
+
+uint64_t miso_attn_layer_prefill_core(uint32_t max_tok) {
+  return k::layer::prefill_core_offset(max_tok);
+}
+
 }  // extern "C"
 
 namespace {

@@ -81,4 +81,34 @@ double miso_bench_decode(int mode, const float* q, const float* qg, const uint16
   return static_cast<double>(ms) / iters;
 }
 
+// ms per token of `iters` eager layer decode steps (miso_attn_layer_decode) at positions len0,
+// len0 + 1, ... -- the cache grows by one row per call, as in the reference's layer bench
+// (bench/attention/bench_attention.hip:22-33: 64 attention_decode calls between two events at
+// each context). One untimed step at len0 first (the timed steps then overwrite its row).
+// Returns a negative value if a call or an event fails.
+double miso_bench_layer_decode(const miso_attn_layer* layer, uint16_t* k, uint16_t* v,
+                               uint32_t len0, uint32_t max_ctx, float* h, float* y, float eps,
+                               float* ws, int iters, void* stream) {
+  if (iters < 1 || uint64_t{len0} + static_cast<uint32_t>(iters) > max_ctx)
+    return -1.0;
+  Timer t;
+  if (!t.a)
+    return -2.0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (miso_attn_layer_decode(layer, k, v, len0, max_ctx, h, nullptr, y, eps, ws, stream) != 0)
+    return -3.0;
+  if (hipEventRecord(t.a, s) != hipSuccess)
+    return -2.0;
+  for (int i = 0; i < iters; ++i)
+    if (miso_attn_layer_decode(layer, k, v, len0 + i, max_ctx, h, nullptr, y, eps, ws, stream) !=
+        0)
+      return -3.0;
+  if (hipEventRecord(t.b, s) != hipSuccess || hipEventSynchronize(t.b) != hipSuccess)
+    return -2.0;
+  float ms = 0.0f;
+  if (hipEventElapsedTime(&ms, t.a, t.b) != hipSuccess)
+    return -2.0;
+  return static_cast<double>(ms) / iters;
+}
+
 }  // extern "C"

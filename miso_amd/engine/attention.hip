@@ -67,24 +67,30 @@ RopeConfig RopeConfig::from(const gguf::File& f) {
 AttentionCache::AttentionCache(unsigned n)
     : max_ctx(n), k(std::size_t{2} * n * 256), v(std::size_t{2} * n * 256) {}
 
-AttentionScratch::AttentionScratch() : ws(L::decode_workspace_floats()) {}
-
 AttentionPrefillScratch::AttentionPrefillScratch(unsigned n)
-    : max_tok(n), ws(L::prefill_workspace_floats(n)) {
-  // The balanced prefill's pair counters at the workspace's end start at zero (every chunk
-  // leaves them so).
-  MISO_HIP_CHECK(hipMemset(ws.data(), 0, ws.size() * sizeof(float)));
+    : max_tok(n),
+      in(n, L::kCore),
+      xn(std::size_t{n} * L::kHidden),
+      proj(std::size_t{n} * AttentionScratch::kProj),
+      q(std::size_t{n} * L::kCore),
+      core(std::size_t{n} * L::kCore),
+      balance(L::prefill_balance_floats(n)) {
+  // The balanced prefill's pair counters start at zero (every chunk leaves them so).
+  if (balance.size() != 0)
+    MISO_HIP_CHECK(hipMemset(balance.data(), 0, balance.size() * sizeof(float)));
 }
 
 void attention_decode(const AttentionLayer& w, AttentionCache& cache, AttentionScratch& sc,
                       const RopeConfig& rope, float* h, const float* delta, float* y, float eps,
                       hipStream_t stream) {
   static_assert(AttentionScratch::kMaxSplits == L::kMaxSplits, "one split cap");
+  static_assert(AttentionScratch::kProj == L::kProj, "one projection layout");
   auto* kc = reinterpret_cast<kernels::attn::half_t*>(cache.k.data());
   auto* vc = reinterpret_cast<kernels::attn::half_t*>(cache.v.data());
-  check("attention_decode",
-        L::decode_step(weights(w, rope), kc, vc, cache.len, cache.max_ctx, h, delta, y, eps,
-                       L::decode_workspace(sc.ws.data()), stream));
+  const L::DecodeWorkspace ws{sc.xn.data(),     sc.proj.data(),   sc.q.data(),     sc.core.data(),
+                              sc.part_m.data(), sc.part_l.data(), sc.part_o.data()};
+  check("attention_decode", L::decode_step(weights(w, rope), kc, vc, cache.len, cache.max_ctx, h,
+                                           delta, y, eps, ws, stream));
   ++cache.len;
 }
 
@@ -94,9 +100,14 @@ void attention_prefill(const AttentionLayer& w, AttentionCache& cache, Attention
   (void)sc;  // the prefill wiring has its own workspace
   auto* kc = reinterpret_cast<kernels::attn::half_t*>(cache.k.data());
   auto* vc = reinterpret_cast<kernels::attn::half_t*>(cache.v.data());
-  check("attention_prefill",
-        L::prefill_step(weights(w, rope), kc, vc, cache.len, n, cache.max_ctx, h, delta, y, eps,
-                        L::prefill_workspace(ps.ws.data(), ps.max_tok), ps.max_tok, stream));
+  const L::PrefillWorkspace ws{ps.xn.data(),   ps.proj.data(), ps.q.data(),
+                               ps.core.data(), ps.in.xs.data(), ps.in.xh.data(),
+                               reinterpret_cast<char*>(ps.balance.data())};
+  check("attention_prefill", L::prefill_step(weights(w, rope), kc, vc, cache.len, n,
+                                             cache.max_ctx, h, delta, y, eps, ws, ps.max_tok,
+                                             stream));
+  if (n != 0)  // the last GEMM input prepared: the chunk's core rows
+    ps.in.k = L::kCore, ps.in.n_tok = n;
   cache.len += n;
 }
 

@@ -6,7 +6,7 @@
 // model.hip use: AttentionLayer::load, RopeConfig::from, AttentionCache, AttentionScratch,
 // AttentionPrefillScratch, attention_decode, attention_prefill). Built inside the engine: it
 // includes the engine's weights.hpp / gguf.hpp / hip_util.hpp. The layouts behind the names are
-// this file's own: four separate weight matrices, and workspaces carved by the wiring.
+// this file's own: four separate weight matrices; the scratch members are the engine's.
 //
 // Sizing retuned for one MI355X: AttentionScratch::kMaxSplits = 128 (the engine: 60). The other
 // two constants live in src/engine/model.hpp (kMaxChunk = 4096 and kPrefillMinTokens = 12 on
@@ -46,20 +46,33 @@ struct AttentionCache {
   DeviceBuffer<std::uint16_t> k, v;
 };
 
-// Decode workspace: the normed row, the [q + gate | k | v] projections, q, core and the split
-// partials for up to kMaxSplits splits.
+// Decode workspace. The members are the engine's (callers read them: the layer's output before
+// the output projection is `core`, 16 heads x 256): the normed row, the [q + gate | k | v]
+// projections, the prepared q, core, and the split partials for up to kMaxSplits splits.
 struct AttentionScratch {
   static constexpr unsigned kMaxSplits = 128;
   static constexpr unsigned kProj = 9216;
-  AttentionScratch();
-  DeviceBuffer<float> ws;
+  DeviceBuffer<float> xn{2048}, proj{kProj}, q{4096}, core{4096};
+  DeviceBuffer<float> part_m{2 * kMaxSplits * 8}, part_l{2 * kMaxSplits * 8};
+  DeviceBuffer<float> part_o{2 * kMaxSplits * 8 * 256};
+  float* qg() { return proj.data(); }
+  float* k() { return proj.data() + 8192; }
+  float* v() { return proj.data() + 8704; }
 };
 
-// Prefill workspace for chunks of up to max_tok tokens.
+// Prefill workspace for chunks of up to max_tok tokens, with the engine's members (`core` holds
+// the last chunk's [n][16][256] attention output) plus `balance`: the balanced prefill's
+// partials and pair counters for chunks of up to min(max_tok, 4096) tokens, zero-filled once here
+// (every chunk leaves the counters zero).
 struct AttentionPrefillScratch {
   explicit AttentionPrefillScratch(unsigned max_tok);
   unsigned max_tok;
-  DeviceBuffer<float> ws;
+  GemmInput in;
+  DeviceBuffer<float> xn, proj, q, core;
+  DeviceBuffer<float> balance;
+  float* qg() { return proj.data(); }
+  float* k() { return proj.data() + 8192; }
+  float* v() { return proj.data() + 8704; }
 };
 
 // h += delta (when delta is set), then y = Attention(RMSNorm(h)) for the token at position

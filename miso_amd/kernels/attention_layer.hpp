@@ -249,6 +249,11 @@ inline constexpr std::size_t decode_workspace_floats() {
          std::size_t{2} * kMaxSplits * 8 * 256;
 }
 
+// Float offset of core in a decode workspace (after part_o, xn, proj and q).
+inline constexpr std::size_t decode_core_offset() {
+  return std::size_t{2} * kMaxSplits * 8 * 256 + kHidden + kProj + kCore;
+}
+
 // Carves ws (16-byte aligned, decode_workspace_floats() floats); every piece stays 16-byte aligned.
 inline DecodeWorkspace decode_workspace(float* ws) {
   DecodeWorkspace d;
@@ -256,7 +261,7 @@ inline DecodeWorkspace decode_workspace(float* ws) {
   d.xn = d.part_o + std::size_t{2} * kMaxSplits * 8 * 256;
   d.proj = d.xn + kHidden;
   d.q = d.proj + kProj;
-  d.core = d.q + kCore;
+  d.core = ws + decode_core_offset();
   d.part_m = d.core + kCore;
   d.part_l = d.part_m + 2 * kMaxSplits * 8;
   return d;
@@ -285,12 +290,17 @@ inline constexpr std::size_t prefill_workspace_floats(unsigned max_tok) {
          prefill_balance_floats(max_tok);
 }
 
+// Float offset of core in a prefill workspace (after xn, proj and q).
+inline constexpr std::size_t prefill_core_offset(unsigned max_tok) {
+  return std::size_t{max_tok} * (kHidden + kProj + kCore);
+}
+
 inline PrefillWorkspace prefill_workspace(float* ws, unsigned max_tok) {
   PrefillWorkspace w;
   w.xn = ws;
   w.proj = w.xn + std::size_t{max_tok} * kHidden;
   w.q = w.proj + std::size_t{max_tok} * kProj;
-  w.core = w.q + std::size_t{max_tok} * kCore;
+  w.core = ws + prefill_core_offset(max_tok);
   w.xs = w.core + std::size_t{max_tok} * kCore;
   w.xh = reinterpret_cast<_Float16*>(w.xs + std::size_t{max_tok} * (kCore / 32));
   w.balance = reinterpret_cast<char*>(w.xh + std::size_t{max_tok} * kCore);

@@ -419,7 +419,7 @@ def rmsnorm_f64(h, weight, eps: float) -> np.ndarray:
 
 
 def layer_f64(h, delta, wq, wk, wv, wo, attn_norm, q_norm, k_norm, inv_freq_arr, pos0: int,
-              max_ctx: int, eps: float, k16=None, v16=None):
+              max_ctx: int, eps: float, k16=None, v16=None, with_core: bool = False):
     """One gated attention layer over T consecutive tokens at pos0..pos0 + T - 1 (the engine's
     attention_decode / attention_prefill, src/engine/attention.hip:76-148, token by token):
     h += delta; xn = RMSNorm(h) attn_norm; [q + gate | k | v] = W xn with xn rounded to f16 (the
@@ -427,7 +427,9 @@ def layer_f64(h, delta, wq, wk, wv, wo, attn_norm, q_norm, k_norm, inv_freq_arr,
     kernels/qgemm.hpp qgemm_act); per-head norms, RoPE and the f16 K/V append (prep_f64);
     attention over the cache up to the token (decode_f64); y = W_o core with core rounded to f16.
     w*: dequantized float matrices [rows][k]. k16 / v16: the f16 caches [2][max_ctx][256]
-    (updated; new zero caches when None). Returns (h, y [T][2048] float64, k16, v16)."""
+    (updated; new zero caches when None). Returns (h, y [T][2048] float64, k16, v16), and with
+    with_core also core [T][4096] float64 (the gated attention output before W_o: the engine's
+    scratch.core, src/engine/attention.hpp:48)."""
     h = np.asarray(h, np.float32).reshape(-1, 2048).copy()
     if delta is not None:
         h = (h + np.asarray(delta, np.float32).reshape(-1, 2048)).astype(np.float32)
@@ -449,6 +451,8 @@ def layer_f64(h, delta, wq, wk, wv, wo, attn_norm, q_norm, k_norm, inv_freq_arr,
                              max_ctx).reshape(-1)
     core16 = core.astype(np.float32).astype(np.float16).astype(np.float64)
     y = core16 @ np.asarray(wo, np.float64).T
+    if with_core:
+        return h, y, k16, v16, core
     return h, y, k16, v16
 
 

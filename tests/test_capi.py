@@ -232,3 +232,16 @@ def test_prefill_workspace_bytes(lib):
         assert lib.miso_attn_prefill_workspace_bytes(n) == 1024 + pairs * 2 * rows * 258 * 4
     assert max(lib.miso_attn_prefill_workspace_bytes(n) for n in range(1, 4200, 7)) == \
         lib.miso_attn_prefill_workspace_bytes(4096)
+
+
+def test_layer_core_offsets(lib):
+    """The engine's scratch.core / ps.core inside the layer workspaces: 16-byte aligned, inside
+    the workspace, and not overlapping the balanced prefill's counters at the prefill workspace's
+    end."""
+    dec = lib.miso_attn_layer_decode_core()
+    assert dec % 4 == 0 and dec + 4096 <= lib.miso_attn_layer_decode_ws()
+    for max_tok in (1, 16, 512, 4096, 8192):
+        at = lib.miso_attn_layer_prefill_core(max_tok)
+        balance = lib.miso_attn_prefill_workspace_bytes(min(max_tok, 4096)) // 4
+        assert at % 4 == 0
+        assert at + max_tok * 4096 <= lib.miso_attn_layer_prefill_ws(max_tok) - balance

@@ -1,6 +1,8 @@
 """Drop-in check of the C++ header API (CPU, compile-only): the reference's own callers of the
 attention kernels -- src/engine/attention.hip, tests/test_attn_splitk.hip and
-bench/attention/*.hip -- and of the Q4_K / Q6_K GEMVs and prefill GEMMs -- src/engine/weights.hip,
+bench/attention/*.hip -- of the engine's attention layer through the drop-in
+miso_amd/engine/attention.hpp -- src/engine/model.hip, tests/test_attention.hip (which reads the
+scratch members) and bench/attention/bench_attention.hip -- and of the Q4_K / Q6_K GEMVs and prefill GEMMs -- src/engine/weights.hip,
 tests/test_q4k_gemv.hip, tests/test_q6k_gemv.hip, tests/test_gemv_dispatch.hip,
 tests/test_qgemm.hip -- compile UNCHANGED for gfx950 with this repository's miso_amd/kernels
 ahead of the reference's kernels/ on the include path, and the preprocessor really picks this repository's headers (while the
@@ -69,18 +71,36 @@ def test_reference_caller_compiles_against_our_headers(caller, direct, tmp_path)
         assert any(p.endswith("/" + direct) for p in included)
 
 
-def _hipcc(src, tmp_path, includes):
+def _hipcc(src, tmp_path, includes, defines=()):
     cmd = [HIPCC, "-std=c++20", "-O1", "--offload-arch=gfx950", "-c", str(src),
            "-o", str(tmp_path / "x.o"), "-H",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            *[a for inc in includes for a in ("-I", str(inc))],
-           "-isystem", str(REF / "third_party")]
+           "-isystem", str(REF / "third_party"), *defines]
     return subprocess.run(cmd, capture_output=True, text=True, timeout=600)
 
 
 def test_engine_model_compiles_with_the_attention_drop_in(tmp_path):
     res = _hipcc(REF / "src/engine/model.hip", tmp_path,
                  [ENGINE, ROOT / "miso_amd" / "kernels", REF / "kernels", REF / "src"])
+    assert res.returncode == 0, res.stderr[-4000:]
+    included = [l.lstrip(". ").strip() for l in res.stderr.splitlines() if l.startswith(".")]
+    hits = [p for p in included if p.endswith("engine/attention.hpp")]
+    assert hits and all(Path(p).resolve().as_posix().startswith(str(ENGINE)) for p in hits), hits
+
+
+# The reference's callers of the engine's attention API, which read the scratch members
+# (tests/test_attention.hip:68 `scratch.core`, :104 `ps.core`) and construct the scratch types
+# (bench/attention/bench_attention.hip:17): unchanged, with the drop-in picked over
+# src/engine/attention.hpp.
+ENGINE_CALLERS = ["tests/test_attention.hip", "bench/attention/bench_attention.hip"]
+
+
+@pytest.mark.parametrize("caller", ENGINE_CALLERS)
+def test_engine_callers_compile_with_the_attention_drop_in(caller, tmp_path):
+    res = _hipcc(REF / caller, tmp_path,
+                 [ENGINE, ROOT / "miso_amd" / "kernels", REF / "kernels", REF / "src"],
+                 ['-DMISO_ORNITH_GGUF="/nonexistent.gguf"', '-DMISO_GOLDEN_DIR="/nonexistent"'])
     assert res.returncode == 0, res.stderr[-4000:]
     included = [l.lstrip(". ").strip() for l in res.stderr.splitlines() if l.startswith(".")]
     hits = [p for p in included if p.endswith("engine/attention.hpp")]

@@ -171,3 +171,52 @@ def test_layer_prefill_balanced_chunk(O, attn, torch_mod, layer_case):
     print(f"[layer] 512-token balanced chunk: max rel-L2 {err.max():.2e}", flush=True)
     assert np.isfinite(got).all()
     assert err.max() <= 5e-3, int(err.argmax())
+
+
+def test_layer_core_after_each_call(O, attn, torch_mod, layer_case):
+    """The attention output each step leaves in its workspace (the engine's scratch.core after
+    attention_decode and ps.core after attention_prefill, which tests/test_attention.hip:68,104
+    read) against the layer oracle's core, read after every call: a 13-token prefill, three
+    decode steps, a 20-token ingest in chunks of 16 (ps.core holds the last chunk's 4 rows) and a
+    decode step. Gates: the reference's own 1e-3 relative L2 per token for decode steps
+    (tests/test_attention.hip:71) and 5e-3 for prefill rows (f16 MFMA operands)."""
+    torch = torch_mod
+    layer, deq, norms = layer_case
+    rng = np.random.default_rng(68)
+    total = 13 + 3 + 20 + 1
+    h0 = rng.standard_normal((total, 2048)).astype(np.float32)
+    h = to_dev(torch, h0.reshape(-1))
+    y = torch.zeros(total * 2048, dtype=torch.float32, device="cuda")
+    kc = torch.zeros(2 * MAX_CTX * 256, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    ws = attn.LayerWorkspace(max_tok=16)
+    _, _, _, _, ref_core = O.layer_f64(h0, None, deq["q"], deq["k"], deq["v"], deq["o"],
+                                       norms["attn_norm"], norms["q_norm"], norms["k_norm"],
+                                       norms["inv_freq"], 0, MAX_CTX, EPS, with_core=True)
+
+    def rows(t, a, b):
+        return t[a * 2048:b * 2048]
+
+    def check(got, a, b, gate, what):
+        got = to_host(got).reshape(b - a, 4096).astype(np.float64)
+        ref = ref_core[a:b]
+        err = np.sqrt(((got - ref) ** 2).sum(axis=1) / (ref ** 2).sum(axis=1))
+        print(f"[layer core] {what} tokens {a}..{b - 1}: max rel-L2 {err.max():.2e}", flush=True)
+        assert np.isfinite(got).all() and err.max() <= gate, (what, a + int(err.argmax()))
+
+    attn.layer_prefill(layer, kc, vc, MAX_CTX, 0, 13, rows(h, 0, 13), None, rows(y, 0, 13), EPS,
+                       ws)
+    torch.cuda.synchronize()
+    check(ws.prefill_core[:13], 0, 13, 5e-3, "prefill")
+    for t in range(13, 16):
+        attn.layer_decode(layer, kc, vc, MAX_CTX, t, rows(h, t, t + 1), None, rows(y, t, t + 1),
+                          EPS, ws)
+        torch.cuda.synchronize()
+        check(ws.decode_core, t, t + 1, 1e-3, "decode")
+    attn.layer_ingest(layer, kc, vc, MAX_CTX, 16, 20, rows(h, 16, 36), None, rows(y, 16, 36), EPS,
+                      ws, chunk=16)
+    torch.cuda.synchronize()
+    check(ws.prefill_core[:4], 32, 36, 5e-3, "ingest's last chunk")
+    attn.layer_decode(layer, kc, vc, MAX_CTX, 36, rows(h, 36, 37), None, rows(y, 36, 37), EPS, ws)
+    torch.cuda.synchronize()
+    check(ws.decode_core, 36, 37, 1e-3, "decode")
