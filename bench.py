@@ -198,11 +198,39 @@ def eager_loop():
     vp, u32, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int
     lib.miso_bench_decode.restype = ctypes.c_double
     lib.miso_bench_decode.argtypes = [i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i32,
-                                      vp, vp, vp, vp, u32, u32, u32, i32, i32, vp]
+                                      vp, vp, vp, vp, u32, u32, u32, i32, i32, vp, vp]
     lib.miso_bench_layer_decode.restype = ctypes.c_double
     lib.miso_bench_layer_decode.argtypes = [vp, vp, vp, u32, u32, vp, vp, ctypes.c_float, vp, i32,
                                             vp]
     return lib
+
+
+def bench_fused(torch, A, lib, args, inputs, dec):
+    """The C2 step in one launch (miso_attn_decode_fused: the splits hand their partials to the
+    last arrivals of each KV head through an agent-scope counter, which merge them) against the
+    two-launch step above: eager (median of 3 windows) and as graph replays."""
+    q, qg, caches = inputs
+    L, R, n = args.ctx, args.buffers, dec["n_splits"]
+    sc = A.DecodeScratch(args.max_splits)
+    core = torch.empty(H * D, device="cuda")
+    w = sorted(eager_decode(torch, lib, 5, q, qg, caches, core, sc, L, n, args.warmup,
+                            dec["steps"]) for _ in range(3))
+    g = graph_of(torch, lambda i: A.attn_decode(q, qg, caches[i % R][0], caches[i % R][1], core,
+                                                sc, L, L, n, fused=True), R)
+    time_replays(torch, g, 2)
+    reps = max(1, (args.steps + R - 1) // R)
+    tg = sorted(time_replays(torch, g, reps)[0] for _ in range(3))[1] / (reps * R)
+    log(f"decode C2 single launch: eager {w[1] * 1e3:.2f} us, graph {tg * 1e3:.2f} us "
+        f"(two launches: eager {dec['t_step_ms'] * 1e3:.2f}, graph "
+        f"{dec['graph_ms']['step'] * 1e3:.2f} us)")
+    return {"workload": "C2 step in one launch (miso_attn_decode_fused): partials stored "
+                        "agent-coherently, the last 32 arrivals per KV head merge the 64 "
+                        "(head, 64-dimension) tiles; measured alternative to split + combine",
+            "us_per_step": round(w[1] * 1e3, 3), "eager_windows_us": [round(x * 1e3, 3) for x in w],
+            "graph_us_per_step": round(tg * 1e3, 3),
+            "two_launch_us_per_step": round(dec["t_step_ms"] * 1e3, 3),
+            "two_launch_graph_us_per_step": round(dec["graph_ms"]["step"] * 1e3, 3),
+            "gbs": round(dec["kv_bytes"] / (w[1] * 1e-3) / 1e9, 1)}
 
 
 def bench_combine_curve(torch, A, lib, inputs):
@@ -234,16 +262,19 @@ def bench_combine_curve(torch, A, lib, inputs):
 
 
 def eager_decode(torch, lib, mode, q, qg, caches, core, sc, L, n_splits, warmup, iters):
-    """ms per call of `iters` eager calls (mode: 0 decode, 1 split, 2 combine, 3 decode f16q)."""
+    """ms per call of `iters` eager calls (mode: 0 decode, 1 split, 2 combine, 3 decode f16q,
+    4 split on VALU, 5 single-launch decode)."""
     import ctypes
     R = len(caches)
     ks = (ctypes.c_void_p * R)(*[k.data_ptr() for k, _ in caches])
     vs = (ctypes.c_void_p * R)(*[v.data_ptr() for _, v in caches])
     torch.cuda.synchronize()
+    sync = getattr(sc, "sync", None)
     ms = lib.miso_bench_decode(mode, q.data_ptr(), qg.data_ptr(), ks, vs, R, core.data_ptr(),
                                sc.part_m.data_ptr(), sc.part_l.data_ptr(), sc.part_o.data_ptr(),
                                L, L, n_splits, warmup, iters,
-                               torch.cuda.current_stream().cuda_stream)
+                               torch.cuda.current_stream().cuda_stream,
+                               sync.data_ptr() if sync is not None else None)
     if ms < 0:
         raise RuntimeError(f"eager timing loop failed ({ms})")
     return ms
@@ -869,6 +900,7 @@ def main():
                 "mfma_split_us": round(dec["t_split_ms"] * 1e3, 3),
                 "gbs": round(dec["kv_bytes"] / (t_valu * 1e-3) / 1e9, 1)}
             other["C2_combine_by_splits"] = bench_combine_curve(torch, A, lib, inputs)
+            other["C2_fused"] = bench_fused(torch, A, lib, args, inputs, dec)
         d60 = bench_decode(torch, A, args, inputs, 60, label="C2 engine cap 60")
         other["C2_engine_cap60"] = decode_line(
             d60, "C2 at the engine's shipped partial capacity kMaxSplits = 60 "

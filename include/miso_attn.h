@@ -110,6 +110,21 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
                      float* part_o, uint32_t len, uint32_t max_ctx, uint32_t n_splits,
                      void* stream);
 
+/* The same decode step in ONE launch (attn_decode_fused_kernel, grid (n_splits, 2) x 256): each
+ * split stores its partial agent-coherently and takes a ticket from its KV head's counter; the
+ * last min(n_splits, 32) arrivals merge the head's 32 (head, 64-dimension) tiles in a fixed order
+ * and apply the gate. No reference counterpart (the reference launches split then combine,
+ * src/engine/attention.hip:103-109). sync: 4 uint32 of device memory, zero-filled once before
+ * the first call; every call leaves it zero; calls that overlap on one sync buffer race.
+ * Results are bit-equal from call to call and within the reference's rel-L2 gate (1e-5) of
+ * miso_attn_decode's frozen merge order. On a device with <= 2 min(n_splits, 32) CUs (where
+ * waiting mergers could hold every CU) it runs miso_attn_decode instead. Rejects what
+ * miso_attn_decode rejects, n_splits > 128 and a NULL or misaligned sync. */
+int miso_attn_decode_fused(const float* q, const float* qg, const uint16_t* k_cache,
+                           const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                           float* part_o, uint32_t* sync, uint32_t len, uint32_t max_ctx,
+                           uint32_t n_splits, void* stream);
+
 /* The decode step with an f16 query and f16 softmax numerators (v_dot2_f32_f16, two products
  * per instruction): attn_split_f16q_kernel<256> then the combine of miso_attn_combine. No
  * reference counterpart -- the reference computes in f32 (kernels/attention_decode.hpp:150-221),

@@ -27,6 +27,7 @@ SIGNATURES = {
     "miso_attn_combine_variant": (c_int, [c_int, P, P, P, P, P, c_uint32, c_uint32, c_uint32,
                                           c_uint32, P]),
     "miso_attn_decode": (c_int, [P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
+    "miso_attn_decode_fused": (c_int, [P, P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_decode_f16q": (c_int, [P, P, P, P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_decode_noalloc": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, P]),
     "miso_attn_prefill": (c_int, [P, P, P, P, P, c_uint32, c_uint32, c_uint32, c_uint32, P]),

@@ -147,14 +147,17 @@ class DecodeScratch:
         self.part_m = torch.empty(n, dtype=torch.float32, device=device)
         self.part_l = torch.empty(n, dtype=torch.float32, device=device)
         self.part_o = torch.empty(n * DIM, dtype=torch.float32, device=device)
+        # the single-launch decode's arrival counters (zero; every call leaves them zero)
+        self.sync = torch.zeros(4, dtype=torch.int32, device=device)
 
 
 def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: int,
                 max_ctx: int, n_splits: Optional[int] = None, stream=None,
-                f16_query: bool = False) -> int:
+                f16_query: bool = False, fused: bool = False) -> int:
     """Split + combine for one decode token over keys [0, length), in the reference's f32
     arithmetic (or, with f16_query, the f16-query / f16-numerator variant
-    miso_attn_decode_f16q). Returns n_splits used."""
+    miso_attn_decode_f16q; with fused, both in one launch, miso_attn_decode_fused). Returns
+    n_splits used."""
     if n_splits is None:
         n_splits = attn_n_splits(length, scratch.max_splits)
     if n_splits > scratch.max_splits:
@@ -166,6 +169,14 @@ def attn_decode(q, qg, k_cache, v_cache, core, scratch: DecodeScratch, length: i
     _need(v_cache, "v_cache", _cache_dtype(v_cache), KV_HEADS * max_ctx * DIM)
     _need(core, "core", f32, Q_HEADS * DIM)
     lib = _lib.load()
+    if fused:
+        if f16_query:
+            raise ValueError("the single-launch decode computes in the reference's f32 arithmetic")
+        _lib.check(lib.miso_attn_decode_fused(
+            _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), _ptr(scratch.part_m),
+            _ptr(scratch.part_l), _ptr(scratch.part_o), _ptr(scratch.sync), length, max_ctx,
+            n_splits, _stream(stream)))
+        return n_splits
     fn = lib.miso_attn_decode_f16q if f16_query else lib.miso_attn_decode
     _lib.check(fn(
         _ptr(q), _ptr(qg), _ptr(k_cache), _ptr(v_cache), _ptr(core), _ptr(scratch.part_m),

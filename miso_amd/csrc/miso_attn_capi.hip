@@ -272,6 +272,38 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
   return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
 }
 
+int miso_attn_decode_fused(const float* q, const float* qg, const uint16_t* k_cache,
+                           const uint16_t* v_cache, float* core, float* part_m, float* part_l,
+                           float* part_o, uint32_t* sync, uint32_t len, uint32_t max_ctx,
+                           uint32_t n_splits, void* stream) {
+  constexpr const char* fn = "miso_attn_decode_fused";
+  if (any_bad(q, qg, k_cache, v_cache, core, part_o, sync) || bad_scalars(part_m) ||
+      bad_scalars(part_l))
+    return fail(fn, kBadPtr);
+  if (len == 0)
+    return fail(fn, "len must be >= 1");
+  if (len > max_ctx)
+    return fail(fn, "len exceeds max_ctx");
+  if (n_splits == 0 || n_splits > k::kAttnTargetSplits)
+    return fail(fn, "n_splits must be 1..128");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return fail(fn, "cannot query the device's compute units");
+  // Waiting mergers hold at most 2 min(n_splits, 32) CUs (one workgroup per CU: 136 KiB of LDS);
+  // with no CU left for the splits still to start, run the two-launch path.
+  if (static_cast<uint32_t>(cus) <= 2 * k::attn_fused_mergers(n_splits))
+    return miso_attn_decode(q, qg, k_cache, v_cache, core, part_m, part_l, part_o, len, max_ctx,
+                            n_splits, stream);
+  const k::AttnDecodeFusedParams p{
+      {q, as_half(k_cache), as_half(v_cache), part_m, part_l, part_o, len, max_ctx, n_splits},
+      qg,
+      core,
+      sync};
+  k::attn_decode_fused_kernel<256><<<dim3(n_splits, 2), 256, 0, as_stream(stream)>>>(p);
+  return launched(fn);
+}
+
 int miso_attn_decode_noalloc(const float* q, const float* qg, const uint16_t* k_cache,
                              const uint16_t* v_cache, float* core, uint32_t len, uint32_t max_ctx,
                              uint32_t n_splits, void* stream) {

@@ -34,13 +34,14 @@ extern "C" {
 // ms per call of `iters` calls after `warmup` untimed ones, rotating over n_buf K/V caches
 // (k[i % n_buf], v[i % n_buf]). mode 0: miso_attn_decode (split + combine); 1: miso_attn_split;
 // 2: miso_attn_combine (over the partials already in part_*); 3: miso_attn_decode_f16q;
-// 4: miso_attn_split_valu.
+// 4: miso_attn_split_valu; 5: miso_attn_decode_fused (sync: its counters).
 // Returns a negative value if a call or an event fails.
 double miso_bench_decode(int mode, const float* q, const float* qg, const uint16_t* const* k,
                          const uint16_t* const* v, int n_buf, float* core, float* part_m,
                          float* part_l, float* part_o, uint32_t len, uint32_t max_ctx,
-                         uint32_t n_splits, int warmup, int iters, void* stream) {
-  if (n_buf < 1 || iters < 1 || warmup < 0 || mode < 0 || mode > 4)
+                         uint32_t n_splits, int warmup, int iters, void* stream, uint32_t* sync) {
+  if (n_buf < 1 || iters < 1 || warmup < 0 || mode < 0 || mode > 5 ||
+      (mode == 5 && sync == nullptr))
     return -1.0;
   auto call = [&](int i) {
     const uint16_t* kc = k[i % n_buf];
@@ -56,6 +57,9 @@ double miso_bench_decode(int mode, const float* q, const float* qg, const uint16
       case 4:
         return miso_attn_split_valu(q, kc, vc, part_m, part_l, part_o, len, max_ctx, n_splits,
                                     stream);
+      case 5:
+        return miso_attn_decode_fused(q, qg, kc, vc, core, part_m, part_l, part_o, sync, len,
+                                      max_ctx, n_splits, stream);
       default:
         return miso_attn_decode_f16q(q, qg, kc, vc, core, part_m, part_l, part_o, len, max_ctx,
                                      n_splits, stream);

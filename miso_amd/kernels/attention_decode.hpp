@@ -798,6 +798,7 @@ constexpr unsigned kTileStages = 4;
 constexpr unsigned kTileBytes = kTileKeys * attn::kDim * 2;  // 16 KiB per K or V tile
 constexpr float kLoScale = 2048.0f;                          // 2^11: the lo half of a pair
 constexpr float kLoWeight = 1.0f / 2048.0f;
+constexpr int kSc1 = 16;  // cache-policy operand of the buffer builtins: sc1 (agent-coherent)
 
 // K tiles in the first 64 KiB (so a K operand address plus its stage offset stays under the
 // 16-bit instruction offset), V tiles in the next 64 KiB, then the KV head's 8 query rows.
@@ -1168,10 +1169,14 @@ __device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& 
 // writes m = -inf, l = 0, o = 0). Every vector-memory load of the stream is a direct LDS load
 // with an explicit wait. `more` says whether the workgroup runs another item afterwards (its LDS
 // is then reused).
-template <class Tiles>
+// kCoherent: the partial is stored with agent-coherent accesses (cache policy sc1, what a relaxed
+// agent-scope atomic access compiles to on gfx950), so a workgroup on another XCD can read it
+// after a counter hand-off (attn_decode_fused_kernel); `part_floats` bounds those stores.
+template <class Tiles, bool kCoherent = false>
 __device__ __attribute__((always_inline)) inline void split_partial_tiles(
     const float* __restrict__ q, const Tiles& tl, AttnSpan span, unsigned kvh, float* part_m,
-    float* part_l, float* part_o, std::size_t base, TileShared& sh, bool more) {
+    float* part_l, float* part_o, std::size_t base, TileShared& sh, bool more,
+    unsigned part_floats = 0) {
   using cdna4::half8_t;
   const unsigned t = threadIdx.x, lane = t & 63u, g = lane >> 4, c = lane & 15u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1338,14 +1343,29 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
       o[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
     }
     if (c < 8) {
-      float4* dst = reinterpret_cast<float4*>(part_o + (base * kGroup + h) * attn::kDim +
-                                              64 * wave + 16 * b + 4 * g);
-      *dst = float4{o[0], o[1], o[2], o[3]};
+      const std::size_t at = (base * kGroup + h) * attn::kDim + 64 * wave + 16 * b + 4 * g;
+      if constexpr (kCoherent)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            cdna4::u32x4_t{__builtin_bit_cast(unsigned, o[0]), __builtin_bit_cast(unsigned, o[1]),
+                           __builtin_bit_cast(unsigned, o[2]), __builtin_bit_cast(unsigned, o[3])},
+            __builtin_amdgcn_make_buffer_rsrc(part_o, 0, static_cast<int>(4 * part_floats),
+                                              0x00020000),
+            static_cast<int>(4 * at), 0, kSc1);
+      else
+        *reinterpret_cast<float4*>(part_o + at) = float4{o[0], o[1], o[2], o[3]};
     }
   }
   if (wave == 0 && lane < 8) {
-    part_m[base * kGroup + h] = st.mt * kLn2;  // -inf stays -inf for an empty span
-    part_l[base * kGroup + h] = L;
+    const float m_nat = st.mt * kLn2;  // -inf stays -inf for an empty span
+    if constexpr (kCoherent) {
+      __hip_atomic_store(part_m + base * kGroup + h, m_nat, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(part_l + base * kGroup + h, L, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      part_m[base * kGroup + h] = m_nat;
+      part_l[base * kGroup + h] = L;
+    }
   }
   if (more)
     tile_barrier();  // LDS is reused by the next item
@@ -1601,6 +1621,167 @@ __device__ void attn_combine_op(const AttnCombineParams& p, unsigned first, unsi
 template <int kBlock, bool kPrepared = false, int kPipeline = 1>
 __global__ void __launch_bounds__(kBlock) attn_combine_kernel(AttnCombineParams p) {
   attn_combine_op<kBlock, kPrepared, kPipeline>(p, 0, attn::kQHeads * (attn::kDim / kBlock));
+}
+
+// ------------------------------------------------------------------------------------------------
+// Single-launch decode (no reference counterpart: the reference launches the split and then the
+// combine, src/engine/attention.hip:103-109). Grid (n_splits, 2) x 256, exactly one item per
+// workgroup. Each workgroup computes its split's partial as attn_split_kernel does, stores it
+// agent-coherently, waits for the stores, and takes a ticket from its KV head's arrival counter.
+// The last T = min(n_splits, 32) arrivals of a KV head become its mergers: merger j waits until
+// every split of the head has arrived (only the stragglers remain by then), then merges tiles
+// j, j + T, ... of the head's 32 (head, 64-dimension) tiles and applies the gate. Earlier arrivals
+// exit at once, so at most 2 T workgroups ever wait, and every workgroup still to start finds a
+// free CU as long as the device has more CUs than that (the host checks it). The wait is bounded
+// (kFusedSpinTicks); a merger that gives up writes NaN to its tiles instead of hanging. The last
+// merger to finish resets the head's counters: every launch leaves them zero, and launches that
+// overlap on one `sync` buffer race.
+//
+// Merge order (fixed, so results are bit-equal from call to call): M = max_c m_c; w_c =
+// __expf(m_c - M); wave w of the merger sums w_c o_c over its quarter of the splits in split
+// order; o = ((S_0 + S_1) + S_2) + S_3; L = the wave-reduction of w_c l_c; core = o / L /
+// (1 + __expf(-gate)). Not the frozen order of attn_combine_kernel, and within the reference's
+// rel-L2 gate of it.
+// ------------------------------------------------------------------------------------------------
+
+struct AttnDecodeFusedParams {
+  AttnSplitParams s;
+  const float* qg;  // [16][512]: gate at h * 512 + 256 + d
+  float* core;      // [16][256]
+  unsigned* sync;   // [2 KV heads][2]: arrivals, finished mergers; zero before the first launch
+};
+
+constexpr unsigned kFusedMaxMergers = 32;  // per KV head: one per (head, 64-dimension) tile
+constexpr unsigned long long kFusedSpinTicks = 5000000;  // 50 ms of the 100 MHz s_memrealtime
+
+__host__ __device__ constexpr unsigned attn_fused_mergers(unsigned n_splits) {
+  return n_splits < kFusedMaxMergers ? n_splits : kFusedMaxMergers;
+}
+
+namespace decode_detail {
+
+struct FusedMergeLds {
+  float w[kAttnTargetSplits], l[kAttnTargetSplits];
+  float part[4][cdna4::kLanes];
+  float red[4];
+};
+
+// Tile t of KV head kvh (head 8 kvh + t / 4, dimensions 64 (t % 4) .. + 63) from the n partials.
+__device__ __attribute__((always_inline)) inline void fused_merge_tile(
+    const AttnDecodeFusedParams& p, unsigned kvh, unsigned t, bool ok, FusedMergeLds& lds) {
+  const unsigned n = p.s.n_splits, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+  const unsigned hl = t / 4, d = 64 * (t % 4) + lane;
+  const std::size_t i0 = std::size_t{kvh} * n * kGroup + hl;  // split c's statistics: i0 + 8 c
+  const unsigned part_floats = 2 * n * kGroup * attn::kDim;
+  const auto o_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.s.part_o), 0,
+                                                        static_cast<int>(4 * part_floats),
+                                                        0x00020000);
+  // This wave's splits [c0, c1): all its partial values in flight at once (at most 32).
+  const unsigned per = (n + 3) / 4, c0 = wave * per, c1 = c0 + per < n ? c0 + per : n;
+  float ov[32];
+#pragma unroll
+  for (unsigned i = 0; i < 32; ++i) {
+    const unsigned c = c0 + i;
+    ov[i] = c < c1 ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   o_rsrc,
+                                                   static_cast<int>(4 * ((i0 + std::size_t{c} *
+                                                                                   kGroup) *
+                                                                              attn::kDim + d)),
+                                                   0, kSc1))
+                   : 0.0f;
+  }
+  float mv = -__builtin_inff(), lv = 0.0f;
+  if (tid < n) {
+    mv = __hip_atomic_load(p.s.part_m + i0 + std::size_t{tid} * kGroup, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    lv = __hip_atomic_load(p.s.part_l + i0 + std::size_t{tid} * kGroup, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const float wm = cdna4::wave_allmax(mv);
+  if (lane == 0)
+    lds.red[wave] = wm;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(lds.red[0], lds.red[1]), fmaxf(lds.red[2], lds.red[3]));
+  const float wc = tid < n ? __expf(mv - M) : 0.0f;
+  if (tid < n)
+    lds.w[tid] = wc, lds.l[tid] = lv;
+  __syncthreads();  // every weight published; lds.red is read
+  const float wl = cdna4::wave_allsum(wc * lv);
+  float acc = 0.0f;
+#pragma unroll
+  for (unsigned i = 0; i < 32; ++i)
+    if (c0 + i < c1)
+      acc = __builtin_fmaf(lds.w[c0 + i], ov[i], acc);
+  lds.part[wave][lane] = acc;
+  if (lane == 0)
+    lds.red[wave] = wl;
+  __syncthreads();
+  if (wave == 0) {
+    const float o = ((lds.part[0][lane] + lds.part[1][lane]) + lds.part[2][lane]) +
+                    lds.part[3][lane];
+    const float L = ((lds.red[0] + lds.red[1]) + lds.red[2]) + lds.red[3];
+    const unsigned h = kvh * kGroup + hl;
+    const float gate = p.qg[h * 2 * attn::kDim + attn::kDim + d];
+    p.core[h * attn::kDim + d] = ok ? o / L / (1.0f + __expf(-gate)) : __builtin_nanf("");
+  }
+  __syncthreads();  // the LDS is reused by the next tile
+}
+
+}  // namespace decode_detail
+
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_decode_fused_kernel(AttnDecodeFusedParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  using namespace decode_detail;
+  __shared__ TileShared sh;
+  const unsigned n = p.s.n_splits;
+  const unsigned kvh = blockIdx.y, split = blockIdx.x;  // grid (n_splits, 2)
+  const std::size_t head = std::size_t{kvh} * p.s.max_ctx * attn::kDim;
+  split_partial_tiles<LinearTiles, true>(
+      p.s.q, LinearTiles{p.s.k_cache + head, p.s.v_cache + head},
+      attn_split_span(p.s.len, n, split), kvh, p.s.part_m, p.s.part_l, p.s.part_o,
+      std::size_t{kvh} * n + split, sh, false, 2 * n * kGroup * attn::kDim);
+  // Arrival: this workgroup's partial stores complete (each wave), then one ticket.
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __syncthreads();
+  auto* lds = reinterpret_cast<FusedMergeLds*>(&sh);
+  auto* flag = reinterpret_cast<unsigned*>(&lds->red[0]);
+  unsigned* const arrivals = p.sync + 2 * kvh;
+  unsigned* const finished = arrivals + 1;
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const unsigned ticket = *flag, mergers = attn_fused_mergers(n);
+  if (ticket + mergers < n)  // uniform
+    return;
+  const unsigned j = ticket + mergers - n;
+  __syncthreads();  // the ticket is read before the flag is reused
+  if (threadIdx.x == 0) {  // every split of this KV head has arrived (bounded wait)
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    unsigned ok = 1;
+    while (__hip_atomic_load(arrivals, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kFusedSpinTicks) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    *flag = ok;
+  }
+  __syncthreads();
+  const bool ok = *flag != 0;
+  __syncthreads();
+  for (unsigned t = j; t < kGroup * 4; t += mergers)
+    fused_merge_tile(p, kvh, t, ok, *lds);
+  if (threadIdx.x == 0) {
+    const unsigned done = __hip_atomic_fetch_add(finished, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (done + 1 == mergers) {  // every merger has passed its wait: reset for the next launch
+      __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(finished, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------------

@@ -427,6 +427,13 @@ __device__ __attribute__((always_inline)) inline void drain_pv() {
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+// drain_pv's wait states tied to the score registers: an asm statement without operands orders
+// only memory accesses, so the scheduler could move the softmax's VALU reads of the scores above
+// it. As an in-out operand, every later use of `s` waits for the nops by data dependence.
+__device__ __attribute__((always_inline)) inline void drain_scores(float16_t& s) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(s));
+}
+
 // S^T = K Q^T of one tile for both blocks: 16 k-steps over head_dim, each K operand read once
 // for two MFMAs. kb: the lane's operand address in the tile's slot before the per-step XOR.
 template <int kBlocks>
@@ -448,7 +455,9 @@ __device__ __attribute__((always_inline)) inline void scores2(const Rows2& rw, u
         s_mfma(s[1], ka, q1);
     }
   }
-  drain_pv();  // the scores are read by the softmax next
+  drain_scores(s[0]);  // the scores are read by the softmax next
+  if constexpr (kBlocks == 2)
+    asm volatile("" : "+v"(s[1]));  // the nops above already cover block 1's last MFMA
 }
 
 // One tile ti of a wave, software-pipelined over two groups of MFMAs (scheduling barriers keep

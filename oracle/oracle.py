@@ -518,6 +518,7 @@ def ref_kernels():
             "ref_attn_prefill": (c_int, [V, V, V, V, V, U, U, U, U]),
             "ref_attn_prep": (c_int, [V, V, V, V, V, V, V, V, V, U, U, c_float]),
             "ref_attn_prep_batch": (c_int, [V, V, V, V, V, V, V, V, V, U, U, c_float, U, U]),
+            "ref_qgemm_act": (c_int, [V, V, V, U, U]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

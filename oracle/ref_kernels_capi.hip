@@ -1,11 +1,13 @@
-// Test infrastructure: extern "C" launchers for the REFERENCE's attention kernels, compiled from
-// the reference tree's own headers (include path set by oracle/Makefile, target `ref`). Used only
-// by GPU tests, as a second checker next to the CPU oracle; never linked into the product.
+// Test infrastructure: extern "C" launchers for the REFERENCE's attention kernels and its prefill
+// GEMM activation prep (qgemm_act_kernel), compiled from the reference tree's own headers
+// (include path set by oracle/Makefile, target `ref`). Used only by GPU tests, as a second
+// checker next to the CPU oracle; never linked into the product.
 //
 // Launch shapes are the reference callers': split <<<dim3(n_splits, 2), 256>>>
 // (src/engine/attention.hip:106), combine variants as tests/test_attn_splitk.hip:78-91 and
 // src/engine/attention.hip:109, prefill <<<attn_prefill_items(n), 256>>> (:143-144), prep
-// <<<18, 256>>> (:183), prep_batch <<<n * 18, 256>>> (:223).
+// <<<18, 256>>> (:183), prep_batch <<<n * 18, 256>>> (:223); qgemm_act <<<ceil(groups / 256), 256>>>
+// (src/engine/weights.hip:310-312).
 
 #include <hip/hip_runtime.h>
 
@@ -13,6 +15,7 @@
 
 #include "attention_decode.hpp"
 #include "attention_prefill.hpp"
+#include "qgemm.hpp"
 
 namespace rk = miso::kernels;
 using rk::attn::half_t;
@@ -86,6 +89,15 @@ int ref_attn_prep_batch(const float* qg, const float* k, const float* v, const f
                                   n,
                                   proj_stride};
   rk::attn_prep_batch_kernel<256><<<n * 18, 256>>>(p);
+  return done();
+}
+
+// The reference's GEMM input prep: x [n_tok][k] rounded to f16 (xh, as uint16 bits) and the sums
+// of each 32-group of the rounded values (xs [n_tok][k / 32]).
+int ref_qgemm_act(const float* x, uint16_t* xh, float* xs, uint32_t k, uint32_t n_tok) {
+  const rk::QGemmActParams p{x, reinterpret_cast<_Float16*>(xh), xs, k, n_tok};
+  const unsigned groups = n_tok * (k / 32);
+  rk::qgemm_act_kernel<<<(groups + 255) / 256, 256>>>(p);
   return done();
 }
 

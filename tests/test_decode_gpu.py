@@ -19,22 +19,23 @@ H, KV, D, G = 16, 2, 256, 8
 CANARY = -9123.5
 
 
-def run_decode(attn, torch, d, max_splits, n_splits=None, f16_query=False):
+def run_decode(attn, torch, d, max_splits, n_splits=None, f16_query=False, fused=False,
+               scratch=None):
     q, qg = to_dev(torch, d["q"]), to_dev(torch, d["qg"])
     k, v = to_dev(torch, d["k"]), to_dev(torch, d["v"])
     core = torch.full((H * D,), CANARY, dtype=torch.float32, device="cuda")
-    sc = attn.DecodeScratch(max_splits)
+    sc = attn.DecodeScratch(max_splits) if scratch is None else scratch
     n = attn.attn_decode(q, qg, k, v, core, sc, d["len"], d["max_ctx"], n_splits,
-                         f16_query=f16_query)
+                         f16_query=f16_query, fused=fused)
     torch.cuda.synchronize()
     return to_host(core).reshape(H, D), n
 
 
 def check(O, attn, torch, length, max_splits, q_scale=2.0, seed=None, max_ctx=None,
-          n_splits=None, name="decode", f16_query=False):
+          n_splits=None, name="decode", f16_query=False, fused=False):
     d = O.decode_inputs(length if seed is None else seed, length,
                         max_ctx if max_ctx else length + 7, q_scale=q_scale)
-    got, n = run_decode(attn, torch, d, max_splits, n_splits, f16_query)
+    got, n = run_decode(attn, torch, d, max_splits, n_splits, f16_query, fused)
     assert not (got == CANARY).any(), "unwritten outputs"
     ref = O.decode_f64(d["q"], d["qg"], d["k"], d["v"], length, d["max_ctx"])
     st = O.compare(got, ref)
@@ -94,6 +95,39 @@ def test_decode_f16_query_variant(O, attn, torch_mod, length):
     and a per-head rel-L2 well above the f32 path's (the variant's documented cost)."""
     check(O, attn, torch_mod, length, 128, q_scale=1.0, seed=length, max_ctx=length,
           name="f16q", f16_query=True)
+
+
+# The single-launch decode (miso_attn_decode_fused): the reference's boundary lengths, C1 and C2,
+# split counts from 1 (one merger merging all 32 tiles) through 31 (fewer mergers than tiles)
+# to 128, against the oracle at the same gates as the two-launch path.
+@pytest.mark.parametrize("length,cap", [(1, 128), (31, 60), (32, 60), (33, 60), (257, 60),
+                                        (1000, 60), (4096, 60), (5000, 3), (3872, 60),
+                                        (32767, 128), (32768, 60), (32769, 128)])
+def test_fused_decode_matches_oracle(O, attn, torch_mod, length, cap):
+    check(O, attn, torch_mod, length, cap, name="fused", fused=True)
+
+
+@pytest.mark.parametrize("length", [512, 32768])
+def test_fused_decode_baseline_configs(O, attn, torch_mod, length):
+    check(O, attn, torch_mod, length, 128, q_scale=1.0, seed=length, max_ctx=length,
+          name="fused baseline", fused=True)
+
+
+def test_fused_decode_repeatable_and_leaves_sync_zero(O, attn, torch_mod):
+    """One scratch (and sync buffer) across calls of decreasing and increasing split counts:
+    each result bit-equal to the same call repeated, within the reference's gate of the
+    two-launch path, and the arrival counters back at zero after every call."""
+    torch = torch_mod
+    sc = attn.DecodeScratch(128)
+    for length, n in ((32768, 128), (1000, 31), (5, 1), (32768, 128), (4096, 64)):
+        d = O.decode_inputs(7 * length + n, length, length, q_scale=1.0)
+        a, _ = run_decode(attn, torch, d, 128, n, fused=True, scratch=sc)
+        assert not to_host(sc.sync).any(), (length, n, to_host(sc.sync))
+        b, _ = run_decode(attn, torch, d, 128, n, fused=True, scratch=sc)
+        assert np.array_equal(a, b), (length, n)
+        two, _ = run_decode(attn, torch, d, 128, n)
+        st = O.compare(a, two.astype(np.float64))
+        assert st["ok"] and st["rel_l2_head"] <= REF_REL_L2, (length, n, st)
 
 
 def test_decode_independent_of_split_count(O, attn, torch_mod):

@@ -50,6 +50,38 @@ def test_activation_prep_is_bit_identical_to_reference_rule(O, attn, torch_mod):
         assert np.array_equal(got_s.view(np.uint32), s.view(np.uint32))
 
 
+def test_activation_prep_matches_the_reference_kernel(O, attn, torch_mod, ref_kernels):
+    """Pins qgemm_act_ref and this repository's gemm_input against the reference's own
+    qgemm_act_kernel (kernels/qgemm.hpp:40-60), built from its sources into oracle/_ref and
+    launched with the engine's shape (src/engine/weights.hip:310-312): xh and xs bit for bit, on
+    the same shapes and values as the test above, the group that rounds to -0 included."""
+    if ref_kernels is None:
+        pytest.skip("oracle/_ref not built (needs the reference tree at build time)")
+    torch = torch_mod
+    rng = np.random.default_rng(3)
+    for n_tok, k in ((70, 2048), (5, 4096), (1, 8192)):
+        x = xs_normal(rng, n_tok, k)
+        x[0, :32] = -1e-9  # a group of values that round to -0
+        xd = to_dev(torch, x.reshape(-1))
+        ref_h = torch.empty(n_tok * k, dtype=torch.float16, device="cuda")
+        ref_s = torch.empty(n_tok * k // 32, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        assert ref_kernels.ref_qgemm_act(xd.data_ptr(), ref_h.data_ptr(), ref_s.data_ptr(), k,
+                                         n_tok) == 0
+        inp = attn.GemmInput(n_tok, k)
+        attn.gemm_input(xd, k, n_tok, inp)
+        torch.cuda.synchronize()
+        rh, rs = to_host(ref_h), to_host(ref_s)
+        h, s = O.qgemm_act_ref(x)
+        assert np.array_equal(rh, h.view(np.uint16)), "oracle rule vs the reference kernel (xh)"
+        assert np.array_equal(rs.view(np.uint32), s.view(np.uint32)), "oracle rule (xs)"
+        assert np.array_equal(to_host(inp.xh)[:n_tok * k], rh), "gemm_input vs reference (xh)"
+        assert np.array_equal(to_host(inp.xs)[:n_tok * k // 32].view(np.uint32),
+                              rs.view(np.uint32)), "gemm_input vs reference (xs)"
+        # -0 halves, and a +0 sum: the sum starts at +0 and +0 + -0 = +0
+        assert rh[:32].tolist() == [0x8000] * 32 and rs.view(np.uint32)[0] == 0
+
+
 def run_gemm(O, attn, torch, fmt, blocks, n, k, x, ldy):
     n_tok = x.shape[0]
     inp = attn.GemmInput(n_tok, k)
