@@ -272,6 +272,23 @@ int miso_attn_decode(const float* q, const float* qg, const uint16_t* k_cache,
   return miso_attn_combine(part_m, part_l, part_o, qg, core, n_splits, stream);
 }
 
+// Compute units of the current device (0 if the query fails), cached per device.
+static unsigned device_cus() {
+  static std::mutex mu;
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cache[dev] = cus;
+  }
+  return static_cast<unsigned>(cache[dev]);
+}
+
 int miso_attn_decode_fused(const float* q, const float* qg, const uint16_t* k_cache,
                            const uint16_t* v_cache, float* core, float* part_m, float* part_l,
                            float* part_o, uint32_t* sync, uint32_t len, uint32_t max_ctx,
@@ -286,13 +303,12 @@ int miso_attn_decode_fused(const float* q, const float* qg, const uint16_t* k_ca
     return fail(fn, "len exceeds max_ctx");
   if (n_splits == 0 || n_splits > k::kAttnTargetSplits)
     return fail(fn, "n_splits must be 1..128");
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+  const unsigned cus = device_cus();
+  if (cus == 0)
     return fail(fn, "cannot query the device's compute units");
   // Waiting mergers hold at most 2 min(n_splits, 32) CUs (one workgroup per CU: 136 KiB of LDS);
   // with no CU left for the splits still to start, run the two-launch path.
-  if (static_cast<uint32_t>(cus) <= 2 * k::attn_fused_mergers(n_splits))
+  if (cus <= 2 * k::attn_fused_mergers(n_splits))
     return miso_attn_decode(q, qg, k_cache, v_cache, core, part_m, part_l, part_o, len, max_ctx,
                             n_splits, stream);
   const k::AttnDecodeFusedParams p{
@@ -413,8 +429,15 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
   const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
   if (items > 0x7FFFFFFFull)
     return fail("miso_attn_decode_ragged", "batch x splits too large for one grid");
-  k::attn_ragged_split_kernel<256>
-      <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
+  // One streaming workgroup per CU where the batch fits its item list; else one workgroup per
+  // (sequence, KV head, split) slot. Same partials either way.
+  const unsigned cus = device_cus();
+  const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(cus, items));
+  if (cus > 0 && k::attn_ragged_stream_fits(batch, s_max, grid))
+    k::attn_ragged_stream_kernel<256><<<grid, 256, 0, as_stream(stream)>>>(p);
+  else
+    k::attn_ragged_split_kernel<256>
+        <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
   int rc = launched("miso_attn_decode_ragged(split)");
   if (rc != 0)
     return rc;

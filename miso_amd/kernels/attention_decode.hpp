@@ -1842,6 +1842,330 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
       (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split, sh, false);
 }
 
+// The same splits on one workgroup per CU (no reference counterpart). Each workgroup takes items
+// w, w + G, w + 2 G, ... of the batch's (sequence, KV head, split) list (sequence-major, KV head,
+// then split; each workgroup computes the list's sequence offsets itself), so the workgroups'
+// item counts differ by at most one. The K/V ring runs straight across item boundaries: tile
+// tau + 3 of the workgroup's tile sequence is issued while tile tau is processed, whichever item
+// either belongs to, and each item's query rows are copied into one of three LDS slots right
+// after its first tile. Per item the arithmetic, the partial and its layout are
+// split_partial_tiles' (so the partials equal attn_ragged_split_kernel's bit for bit), and
+// attn_ragged_combine_kernel merges them. Batches of up to kRaggedStreamMaxBatch sequences whose
+// per-workgroup item count fits kRaggedStreamMaxItems (attn_ragged_stream_fits).
+constexpr unsigned kRaggedStreamMaxBatch = 512;
+constexpr unsigned kRaggedStreamMaxItems = 64;
+
+__host__ __device__ constexpr bool attn_ragged_stream_fits(unsigned batch, unsigned s_max,
+                                                         unsigned grid) {
+  return batch <= kRaggedStreamMaxBatch && grid > 0 &&
+         (std::size_t{batch} * attn::kKvHeads * s_max + grid - 1) / grid <= kRaggedStreamMaxItems;
+}
+
+namespace decode_detail {
+
+struct StreamItem {
+  std::size_t kv0;        // element offset of the item's K/V head rows
+  unsigned begin, end;    // its key span
+  unsigned seq, kvh;
+  unsigned part;          // its partial's row group: (seq * 2 + kvh) * s_max + split
+  unsigned tiles;         // its 32-key tiles (0 for an empty span)
+};
+
+struct alignas(1024) StreamShared {
+  unsigned char k[kTileStages][kTileBytes];
+  unsigned char v[kTileStages][kTileBytes];
+  float q[3][kGroup][attn::kDim];
+  unsigned prefix[kRaggedStreamMaxBatch + 1];
+  StreamItem items[kRaggedStreamMaxItems];
+};
+
+}  // namespace decode_detail
+
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_ragged_stream_kernel(AttnRaggedParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  using namespace decode_detail;
+  using cdna4::half8_t;
+  __shared__ StreamShared sh;
+  const unsigned t = threadIdx.x, lane = t & 63u, g = lane >> 4, c = lane & 15u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const unsigned G = gridDim.x, w = blockIdx.x;
+
+  // Sequence offsets of the item list (wave 0: 64 sequences per step, an inclusive scan).
+  if (wave == 0) {
+    unsigned run = 0;
+    if (lane == 0)
+      sh.prefix[0] = 0;
+    for (unsigned base = 0; base < p.batch; base += cdna4::kLanes) {
+      const unsigned s_ = base + lane;
+      unsigned cnt = 0;
+      if (s_ < p.batch) {
+        const unsigned len = p.lens[s_] < p.len_cap ? p.lens[s_] : p.len_cap;
+        cnt = attn::kKvHeads * attn_ragged_seq_splits(len, p.s_max);
+      }
+      unsigned incl = cnt;
+#pragma unroll
+      for (unsigned d = 1; d < cdna4::kLanes; d *= 2) {
+        const unsigned up = __shfl_up(incl, d, cdna4::kLanes);
+        incl += lane >= d ? up : 0u;
+      }
+      if (s_ < p.batch)
+        sh.prefix[s_ + 1] = run + incl;
+      run += __shfl(incl, cdna4::kLanes - 1, cdna4::kLanes);
+    }
+  }
+  __syncthreads();
+  const unsigned total = sh.prefix[p.batch];
+  const unsigned n_items = w < total ? (total - w + G - 1) / G : 0;
+  for (unsigned j = t; j < n_items; j += kBlock) {
+    const unsigned k = w + j * G;
+    unsigned lo = 0, hi = p.batch;  // the sequence s with prefix[s] <= k < prefix[s + 1]
+    while (hi - lo > 1) {
+      const unsigned mid = (lo + hi) / 2;
+      if (sh.prefix[mid] <= k)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const unsigned r = k - sh.prefix[lo], n = (sh.prefix[lo + 1] - sh.prefix[lo]) / 2;
+    const unsigned kvh = r / n, split = r % n;
+    const unsigned len = p.lens[lo] < p.len_cap ? p.lens[lo] : p.len_cap;
+    const AttnSpan span = attn_split_span(len, n, split);
+    sh.items[j] = StreamItem{p.kv_offsets[lo] + std::size_t{kvh} * len * attn::kDim,
+                             span.begin, span.end, lo, kvh,
+                             (lo * attn::kKvHeads + kvh) * p.s_max + split,
+                             (span.end - span.begin + kTileKeys - 1) / kTileKeys};
+  }
+  __syncthreads();
+  // Items with an empty span (capped split counts) have no tiles: their partial is written here,
+  // (-inf, 0, 0) as the split writes it, and both cursors below skip them.
+  for (unsigned j = 0; j < n_items; ++j) {
+    const unsigned part = __builtin_amdgcn_readfirstlane(sh.items[j].part);
+    if (__builtin_amdgcn_readfirstlane(sh.items[j].tiles) != 0)
+      continue;
+    float* po = p.part_o + std::size_t{part} * kGroup * attn::kDim;
+#pragma unroll
+    for (unsigned i = 0; i < kGroup * attn::kDim / kBlock; ++i)
+      po[i * kBlock + t] = 0.0f;
+    if (t < kGroup) {
+      p.part_m[std::size_t{part} * kGroup + t] = -__builtin_inff();
+      p.part_l[std::size_t{part} * kGroup + t] = 0.0f;
+    }
+  }
+
+  // Tile cursor over the workgroup's items: tiles of item j in order, items in order.
+  auto item_tiles = [&](unsigned j) __attribute__((always_inline)) {
+    return __builtin_amdgcn_readfirstlane(sh.items[j].tiles);
+  };
+  auto next_item = [&](unsigned j) __attribute__((always_inline)) {  // first non-empty >= j
+    while (j < n_items && item_tiles(j) == 0)
+      ++j;
+    return j;
+  };
+  unsigned total_tiles = 0;
+  for (unsigned j = 0; j < n_items; ++j)
+    total_tiles += item_tiles(j);
+  if (total_tiles == 0)  // uniform
+    return;
+
+  const unsigned k_lds0 = cdna4::lds_offset(sh.k[0]) + 4096 * wave;
+  const unsigned v_lds0 = cdna4::lds_offset(sh.v[0]) + 4096 * wave;
+  unsigned koff[4], voff[4];
+#pragma unroll
+  for (unsigned i = 0; i < 4; ++i) {
+    const unsigned jj = 2 * i + (lane >> 5), r = 8 * wave + jj, q_ = lane & 31u;
+    koff[i] = jj * 512 + 16 * tile_swz_k(r, q_) - 1024 * i;
+    voff[i] = jj * 512 + 16 * tile_swz_v(r, q_) - 1024 * i;
+  }
+  // The issue cursor: item ji, its tile ti, global tile tau_i.
+  unsigned ji = next_item(0), ti = 0, tau_i = 0;
+  auto issue_next = [&]() __attribute__((always_inline)) {
+    const StreamItem& it = sh.items[ji];
+    const unsigned begin = __builtin_amdgcn_readfirstlane(it.begin);
+    const unsigned end = __builtin_amdgcn_readfirstlane(it.end);
+    const unsigned kv0_lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(it.kv0));
+    const unsigned kv0_hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(it.kv0 >> 32));
+    const std::size_t kv0 = (std::size_t{kv0_hi} << 32) | kv0_lo;
+    const unsigned stage = tau_i % kTileStages;
+    issue_tile(LinearTiles{p.k_cache + kv0, p.v_cache + kv0}, begin + ti * kTileKeys, end - 1,
+               k_lds0 + stage * kTileBytes, v_lds0 + stage * kTileBytes, koff, voff, wave, lane);
+    if (ti == 0) {  // the item's query rows into slot ji % 3, after its first tile
+      const unsigned seq = __builtin_amdgcn_readfirstlane(it.seq);
+      const unsigned kvh = __builtin_amdgcn_readfirstlane(it.kvh);
+      const float* q = p.q + std::size_t{seq} * attn::kQHeads * attn::kDim;
+#pragma unroll
+      for (unsigned i = 0; i < 2; ++i) {
+        const unsigned h = 2 * wave + i;
+        cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
+                          cdna4::lds_offset(sh.q[ji % 3][h]));
+      }
+    }
+    ++tau_i;
+    if (++ti == item_tiles(ji)) {
+      ti = 0;
+      ji = next_item(ji + 1);
+    }
+  };
+
+  const unsigned kl = 512 * c + 16 * (g ^ (c & 3u)) + 64 * (c >> 2);
+  unsigned vl[4];
+  {
+    const unsigned r = (lane >> 2) & 3u, e = lane & 3u, row = 4 * g + r;
+#pragma unroll
+    for (unsigned b = 0; b < 4; ++b)
+      vl[b] = 512 * row + 32 * ((4 * wave + b) ^ (row & 7u)) + 8 * e;
+  }
+  auto kslot = [&](unsigned tau) __attribute__((always_inline)) {
+    return cdna4::lds_offset(sh.k[tau % kTileStages]) + kl;
+  };
+  auto vslot = [&](unsigned tau) __attribute__((always_inline)) {
+    return cdna4::lds_offset(sh.v[tau % kTileStages]);
+  };
+  const TileLane tln = tile_lane(lane);
+  TileState st;
+  f32x4 s_cur[2] = {f32x4{}, f32x4{}};
+
+  // Start item j (its first tile, global tile tau, has landed): state reset, query pairs from its
+  // slot, scores of its first tile.
+  auto start_item = [&](unsigned j, unsigned tau) __attribute__((always_inline)) {
+    st.m = 0.0f;
+    st.mt = -__builtin_inff();
+    st.l = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      st.o[b] = f32x4{};
+    const float* qrow = sh.q[j % 3][c & 7u];
+    constexpr float kScale = kLog2e / 16.0f;
+#pragma unroll
+    for (unsigned s_ = 0; s_ < 8; ++s_) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s_ + g));
+      const float4 x1 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s_ + g) + 4);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      _Float16 hv[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float v = xs[jj] * kScale;
+        hv[jj] = pair_half(static_cast<_Float16>(v), v, tln);
+      }
+      st.q[s_] = half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
+    }
+    half8_t ka[2][8];
+    read_k(ka, kslot(tau));
+#pragma unroll
+    for (unsigned s_ = 0; s_ < 8; ++s_)
+      score_step(s_cur, ka, st.q[s_], s_);
+  };
+  auto softmax_pv = [&](const half8_t (&va)[4], TileSoftmax& sm, bool moved, bool first)
+      __attribute__((always_inline)) {
+    if (moved)
+      tile_rescale(sm, st, first, tln);
+    st.l += sm.lt;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
+  };
+
+  // The first three tiles, then item 0's start.
+  for (unsigned i = 0; i < kTileStages - 1 && tau_i < total_tiles; ++i)
+    issue_next();
+  wait_tiles_after(total_tiles - 1 < 2 ? total_tiles - 1 : 2);
+  tile_barrier();
+  unsigned jc = next_item(0), tc = 0;  // the compute cursor: item jc, its tile tc
+  unsigned jc_tiles = item_tiles(jc);
+  start_item(jc, 0);
+
+  // Partial writes at the end of the previous two iterations (0 or 1 each): their stores count in
+  // vmcnt after tile tau + 1's copy (issued at the top of iteration tau - 2), so the wait for that
+  // tile allows 4 instructions per write -- the 4 16-byte stores every wave issues (lanes 0-7 of
+  // each wave store) -- besides the 8 of a later tile copy. Wave 0's two further stores only make
+  // it wait longer.
+  unsigned wrote1 = 0, wrote2 = 0;
+  for (unsigned tau = 0; tau < total_tiles; ++tau) {
+    const StreamItem& cur = sh.items[jc];
+    const unsigned begin = __builtin_amdgcn_readfirstlane(cur.begin);
+    const unsigned end = __builtin_amdgcn_readfirstlane(cur.end);
+    const unsigned stores = 4 * (wrote1 + wrote2);
+    wrote2 = wrote1;
+    wrote1 = 0;
+    if (tau + 1 < total_tiles) {  // tile tau + 1 lands; every wave is done with tile tau - 1
+      const unsigned ahead = tau_i - (tau + 2);  // copies issued after tile tau + 1's
+      switch ((ahead < 1 ? 8 * ahead : 8) + stores) {
+        case 0: cdna4::wait_vmcnt<0>(); break;
+        case 4: cdna4::wait_vmcnt<4>(); break;
+        case 8: cdna4::wait_vmcnt<8>(); break;
+        case 12: cdna4::wait_vmcnt<12>(); break;
+        default: cdna4::wait_vmcnt<16>(); break;
+      }
+      tile_barrier();
+      if (tau_i < total_tiles)
+        issue_next();  // tile tau + 3, into tile tau - 1's stage
+    }
+    TileSoftmax sm;
+    const unsigned k0 = begin + tc * kTileKeys;
+    if (k0 + kTileKeys > end)  // uniform: only an item's last tile
+      tile_scores_joined<true>(sm, s_cur, st.m, k0, end, lane, tln);
+    else
+      tile_scores_joined<false>(sm, s_cur, st.m, k0, end, lane, tln);
+    half8_t va[4];
+    if (tc + 1 < jc_tiles) {  // scores of the item's next tile under this tile's softmax
+      half8_t ka[2][8];
+      read_k(ka, kslot(tau + 1));
+      read_v(va, vslot(tau), vl);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 s_next[2];
+#pragma unroll
+      for (unsigned s_ = 0; s_ < 8; ++s_)
+        score_step(s_next, ka, st.q[s_], s_);
+      const bool moved = tile_decide(sm, st, tc == 0, tln);
+      asm volatile("" : "+v"(sm.lt), "+v"(sm.pb));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      }
+      softmax_pv(va, sm, moved, tc == 0);
+      s_cur[0] = s_next[0];
+      s_cur[1] = s_next[1];
+      ++tc;
+      continue;
+    }
+    // The item's last tile: its softmax and P V alone, then its partial.
+    read_v(va, vslot(tau), vl);
+    const bool moved = tile_decide(sm, st, tc == 0, tln);
+    softmax_pv(va, sm, moved, tc == 0);
+    {
+      const unsigned part = __builtin_amdgcn_readfirstlane(cur.part);
+      const float f = __builtin_amdgcn_exp2f(st.m - st.mt);
+      const float L = cdna4::sum_xor32(cdna4::sum_xor16(st.l)) * f;
+      const unsigned h = c & 7u;
+#pragma unroll
+      for (unsigned b = 0; b < 4; ++b) {
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = st.o[b][i] * f;
+          o[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
+        }
+        if (c < 8)
+          *reinterpret_cast<float4*>(p.part_o + (std::size_t{part} * kGroup + h) * attn::kDim +
+                                     64 * wave + 16 * b + 4 * g) = float4{o[0], o[1], o[2], o[3]};
+      }
+      if (wave == 0 && lane < 8) {
+        p.part_m[std::size_t{part} * kGroup + h] = st.mt * kLn2;
+        p.part_l[std::size_t{part} * kGroup + h] = L;
+      }
+      wrote1 = 1;
+    }
+    if (tau + 1 < total_tiles) {  // the next item's first tile (tile tau + 1) has landed
+      jc = next_item(jc + 1);
+      tc = 0;
+      jc_tiles = item_tiles(jc);
+      start_item(jc, tau + 1);
+    }
+  }
+}
+
 // One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's. (A
 // template, so every translation unit including this header may instantiate it.)
 template <int = 0>

@@ -57,3 +57,40 @@ def test_ragged_empty_sequence_is_zero(O, attn, torch_mod):
                        np.array([5, 1, 9], np.uint32))
     for s in (0, 2):
         assert O.compare(got[s], ref[s])["ok"]
+
+
+def check_all(O, attn, torch, lens, seed, max_len=None, name="ragged"):
+    r, got = run(O, attn, torch, lens, seed, max_len)
+    ref = O.ragged_f64(r["q"], r["gate"], r["k"], r["v"], r["offsets"], lens)
+    live = np.asarray(lens) > 0
+    st = O.compare(got[live], ref[live])
+    report(f"{name} batch={len(lens)} sum_len={int(np.sum(lens))}", st)
+    assert st["ok"] and st["rel_l2_head"] <= REF_REL_L2, st
+    assert not got[~live].any()
+
+
+def test_ragged_stream_many_short_items(O, attn, torch_mod):
+    """The streaming split (one workgroup per CU, the K/V ring running across items) over many
+    items of one or two 32-key tiles -- query rows cycle through the three LDS slots at every
+    tile -- with empty sequences among them and a few long ones."""
+    rng = np.random.default_rng(300)
+    lens = rng.integers(1, 65, 300).astype(np.uint32)
+    lens[::37] = 0
+    lens[[5, 150, 299]] = (3000, 1025, 513)
+    check_all(O, attn, torch_mod, lens, 300, name="stream short items")
+
+
+def test_ragged_stream_empty_span(O, attn, torch_mod):
+    """A sequence longer than max_len: its split count is capped at max_len's, and with 65537
+    keys in 128 splits of 65 units the last split's span is empty (its partial is written as
+    (-inf, 0, 0) without tiles)."""
+    lens = np.array([65537, 700, 33], np.uint32)
+    check_all(O, attn, torch_mod, lens, 65537, max_len=65536, name="stream empty span")
+
+
+def test_ragged_wide_batch_fallback(O, attn, torch_mod):
+    """A batch above the streaming split's descriptor limit (512 sequences) runs one workgroup
+    per (sequence, KV head, split); same gates."""
+    rng = np.random.default_rng(600)
+    lens = rng.integers(0, 700, 600).astype(np.uint32)
+    check_all(O, attn, torch_mod, lens, 600, name="fallback batch")
