@@ -944,11 +944,13 @@ __device__ __attribute__((always_inline)) inline void issue_tile(
 //   mt: the true max; l: the sum of this lane's numerators (keys 4 g + i and 16 + 4 g + i of
 //   every tile, relative to m).
 //   o[b]: O^T of dimensions 64 w + 16 b + 4 g + i, column c, relative to m.
-struct TileState {
+template <int kBlocks>
+struct TileStateT {
   cdna4::half8_t q[8];
   float m, mt, l;
-  f32x4 o[4];
+  f32x4 o[kBlocks];
 };
+using TileState = TileStateT<4>;
 
 // The K operands of one tile (both 16-key blocks, 8 k-steps): ka[kb][s] at (kaddr + 8192 kb) ^
 // 64 s, kaddr = the tile's K slot + the lane's offset.
@@ -1108,8 +1110,9 @@ __device__ __attribute__((always_inline)) inline void tile_numerators(TileSoftma
 // Head max over the tile (the lane's 8 keys, then the 4 lanes g of its column; every tile has a
 // key in the split, so it is finite), the true max, and the speculative numerators. `first`:
 // the split's first tile (wave-uniform).
-template <bool kV = false>
-__device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& sm, TileState& st,
+template <bool kV = false, int kBlocks = 4>
+__device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& sm,
+                                                                 TileStateT<kBlocks>& st,
                                                                  bool first, const TileLane& tl,
                                                                  const float* vr = nullptr) {
   const float* x = sm.x;
@@ -1131,10 +1134,11 @@ __device__ __attribute__((always_inline)) inline bool tile_decide(TileSoftmax& s
 // taken branch; as C++, the compiler hoists copies of O out of it to every iteration). The
 // leading no-ops let the last P V MFMA's results settle; the trailing ones separate the AGPR
 // writes from the next MFMA reading them.
-__device__ __attribute__((always_inline)) inline void tile_scale_o(f32x4 (&o)[4], float c) {
+template <int kBlocks>
+__device__ __attribute__((always_inline)) inline void tile_scale_o(f32x4 (&o)[kBlocks], float c) {
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float x = o[b][i], tmp;
@@ -1151,8 +1155,9 @@ __device__ __attribute__((always_inline)) inline void tile_scale_o(f32x4 (&o)[4]
 
 // The rare path: move the reference max of each head by d = max(0, tile max) (the tile max on
 // the first tile), rescale l and O, and redo the numerators.
-template <bool kV = false>
-__device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& sm, TileState& st,
+template <bool kV = false, int kBlocks = 4>
+__device__ __attribute__((always_inline)) inline void tile_rescale(TileSoftmax& sm,
+                                                                  TileStateT<kBlocks>& st,
                                                                   bool first, const TileLane& tl,
                                                                   const float* vr = nullptr) {
   const float d = first ? sm.mx : fmaxf(sm.mx, 0.0f);
@@ -1366,6 +1371,414 @@ __device__ __attribute__((always_inline)) inline void split_partial_tiles(
       part_m[base * kGroup + h] = m_nat;
       part_l[base * kGroup + h] = L;
     }
+  }
+  if (more)
+    tile_barrier();  // LDS is reused by the next item
+}
+
+// ------------------------------------------------------------------------------------------------
+// Per-wave tiles. Each wave streams whole 32-key tiles of its own (tiles w, w + 4, ... of an
+// item) through its own K and V slot (sh.k[w], sh.v[w]) and keeps its own softmax state with O
+// over all 256 dimensions (16 blocks), so no score or softmax is computed twice and the tile
+// loop has no workgroup barrier: the next tile's K is issued as soon as this tile's K operands
+// are in registers, its V as soon as this tile's V operands are. The four wave states of an
+// item are merged in LDS at its end (wave_merge_*).
+// ------------------------------------------------------------------------------------------------
+
+// Wait until at most n of this wave's vector-memory instructions are in flight, n rounded down to
+// a multiple of 4 and capped at 60 (waiting for more than needed is only slower).
+__device__ __attribute__((always_inline)) inline void wait_vm_at_most(unsigned n) {
+  switch (n < 60 ? n / 4 : 15) {
+    case 0: cdna4::wait_vmcnt<0>(); break;
+    case 1: cdna4::wait_vmcnt<4>(); break;
+    case 2: cdna4::wait_vmcnt<8>(); break;
+    case 3: cdna4::wait_vmcnt<12>(); break;
+    case 4: cdna4::wait_vmcnt<16>(); break;
+    case 5: cdna4::wait_vmcnt<20>(); break;
+    case 6: cdna4::wait_vmcnt<24>(); break;
+    case 7: cdna4::wait_vmcnt<28>(); break;
+    case 8: cdna4::wait_vmcnt<32>(); break;
+    case 9: cdna4::wait_vmcnt<36>(); break;
+    case 10: cdna4::wait_vmcnt<40>(); break;
+    case 11: cdna4::wait_vmcnt<44>(); break;
+    case 12: cdna4::wait_vmcnt<48>(); break;
+    case 13: cdna4::wait_vmcnt<52>(); break;
+    case 14: cdna4::wait_vmcnt<56>(); break;
+    default: cdna4::wait_vmcnt<60>(); break;
+  }
+}
+
+// Copy of 8 rows of one K or V tile whose rows all exist: instruction i moves rows 2 i + lane / 32
+// of the group at xt, LDS chunk position lane % 32 of those rows at lds (`off`: the lane's byte
+// offset from xt minus 1024 i, since the instruction offset moves the global and the LDS address
+// alike). Non-temporal loads; M0 is saved and restored.
+__device__ __attribute__((always_inline)) inline void issue_rows4(const void* xt,
+                                                                 const unsigned (&off)[4],
+                                                                 unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %6\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %5 nt\n\t"
+      "global_load_lds_dwordx4 %2, %5 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %3, %5 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:3072 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(xt), "s"(lds)
+      : "memory");
+}
+
+// Copy offsets of a wave's whole-tile copies, in the layout of the tile slots (row r at byte
+// 512 r, chunk position p holding chunk tile_swz(r, p)): group g (rows 8 g ..), instruction i,
+// row r = 8 g + 2 i + lane / 32. K's swizzle depends on r % 16 (so on g's parity), V's on r % 8.
+struct WaveCopy {
+  unsigned koff[2][4];
+  unsigned voff[4];
+};
+__device__ __attribute__((always_inline)) inline WaveCopy wave_copy_offsets(unsigned lane) {
+  WaveCopy cp;
+#pragma unroll
+  for (unsigned i = 0; i < 4; ++i) {
+    const unsigned j = 2 * i + (lane >> 5), p = lane & 31u;
+#pragma unroll
+    for (unsigned par = 0; par < 2; ++par)
+      cp.koff[par][i] = j * 512 + 16 * tile_swz_k(8 * par + j, p) - 1024 * i;
+    cp.voff[i] = j * 512 + 16 * tile_swz_v(j, p) - 1024 * i;
+  }
+  return cp;
+}
+
+// This wave's copy of the whole K (kV false) or V (kV true) tile at key k0 into its slot at lds:
+// 4 groups of 8 rows, always 16 vector-memory instructions; rows past last_row read last_row
+// instead (they are masked at use), so no load leaves the item's rows.
+template <bool kV, class Tiles>
+__device__ __attribute__((always_inline)) inline void issue_wave_tile(const Tiles& tl, unsigned k0,
+                                                                     unsigned last_row,
+                                                                     unsigned lds,
+                                                                     const WaveCopy& cp,
+                                                                     unsigned lane) {
+#pragma unroll
+  for (unsigned g = 0; g < 4; ++g) {
+    const unsigned gs = k0 + 8 * g;  // the group's first row (wave-uniform)
+    const unsigned(&off)[4] = kV ? cp.voff : cp.koff[g & 1u];
+    if (gs + 7 <= last_row) {
+      issue_rows4(uniform(kV ? tl.v_at(gs) : tl.k_at(gs)), off, lds + 4096 * g);
+    } else {
+      const unsigned row0 = gs <= last_row ? gs : last_row;
+      const unsigned lim = last_row - row0;  // rows of the group past last_row read row0 + lim
+      const attn::half_t* X = kV ? tl.v_at(row0) : tl.k_at(row0);
+#pragma unroll
+      for (unsigned i = 0; i < 4; ++i) {
+        const unsigned j = 2 * i + (lane >> 5), r = 8 * g + j, p = lane & 31u;
+        const std::size_t at = std::size_t{j < lim ? j : lim} * attn::kDim;
+        cdna4::lds_load16_nt(X + at + 8 * (kV ? tile_swz_v(r, p) : tile_swz_k(r, p)),
+                             lds + 4096 * g + 1024 * i);
+      }
+    }
+  }
+}
+
+// The V^T operands of all 16 dimension blocks of a tile (two transpose reads each: rows 4 g + r
+// and 16 + 4 g + r). vl[j]: the lane's offset for blocks j and j + 8 (+256 bytes).
+__device__ __attribute__((always_inline)) inline void read_v_all(cdna4::half8_t (&va)[16],
+                                                                unsigned vslot,
+                                                                const unsigned (&vl)[8]) {
+#pragma unroll
+  for (unsigned b = 0; b < 16; ++b) {
+    const unsigned a = vslot + vl[b & 7u] + 256u * (b >> 3);
+    const cdna4::half4_t lo = lds_tr_b64(a);
+    const cdna4::half4_t up = lds_tr_b64(a + 8192u);
+    va[b] = cdna4::half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+  }
+}
+
+using WaveTileState = TileStateT<16>;
+
+// Per-lane operand offsets of the wave loops: kl into a K slot (as split_partial_tiles), vl[j]
+// into a V slot for dimension blocks j and j + 8.
+struct WaveOperands {
+  unsigned kl;
+  unsigned vl[8];
+};
+__device__ __attribute__((always_inline)) inline WaveOperands wave_operands(unsigned lane) {
+  WaveOperands op;
+  const unsigned g = lane >> 4, c = lane & 15u;
+  op.kl = 512 * c + 16 * (g ^ (c & 3u)) + 64 * (c >> 2);
+  const unsigned r = (lane >> 2) & 3u, e = lane & 3u, row = 4 * g + r;
+#pragma unroll
+  for (unsigned j = 0; j < 8; ++j)
+    op.vl[j] = 512 * row + 32 * (j ^ (row & 7u)) + 8 * e;
+  return op;
+}
+
+// Fresh state of an item; the query pairs from its f32 rows qrows[8][256] (as split_partial_tiles:
+// head c % 8, dimensions 8 (4 s + g) .. + 7, x log2(e)/16, hi half in columns 0-7, lo in 8-15).
+__device__ __attribute__((always_inline)) inline void wave_start(WaveTileState& st,
+                                                                const float (*qrows)[attn::kDim],
+                                                                unsigned lane,
+                                                                const TileLane& tln) {
+  const unsigned g = lane >> 4, c = lane & 15u;
+  st.m = 0.0f;
+  st.mt = -__builtin_inff();
+  st.l = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    st.o[b] = f32x4{};
+  const float* qrow = qrows[c & 7u];
+  constexpr float kScale = kLog2e / 16.0f;
+#pragma unroll
+  for (unsigned s = 0; s < 8; ++s) {
+    const float4 x0 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s + g));
+    const float4 x1 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s + g) + 4);
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    _Float16 hv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = xs[j] * kScale;
+      hv[j] = pair_half(static_cast<_Float16>(v), v, tln);
+    }
+    st.q[s] = cdna4::half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
+  }
+}
+
+// The scores of one tile (its K operands already read into ka).
+__device__ __attribute__((always_inline)) inline void wave_scores(f32x4 (&s)[2],
+                                                                 const cdna4::half8_t (&ka)[2][8],
+                                                                 const WaveTileState& st) {
+#pragma unroll
+  for (unsigned i = 0; i < 8; ++i)
+    score_step(s, ka, st.q[i], i);
+}
+
+// The softmax of one tile whose scores are s; keys k0 + key >= end are masked (only an item's
+// last tile reaches past it). first: the wave's first tile of the item.
+__device__ __attribute__((always_inline)) inline void wave_softmax(
+    TileSoftmax& sm, WaveTileState& st, const f32x4 (&s)[2], unsigned k0, unsigned end,
+    bool first, unsigned lane, const TileLane& tln) {
+  if (k0 + kTileKeys > end)  // uniform
+    tile_scores_joined<true>(sm, s, st.m, k0, end, lane, tln);
+  else
+    tile_scores_joined<false>(sm, s, st.m, k0, end, lane, tln);
+  const bool moved = tile_decide(sm, st, first, tln);
+  if (moved)
+    tile_rescale(sm, st, first, tln);
+  st.l += sm.lt;
+}
+
+// O += V^T P^T of one tile.
+__device__ __attribute__((always_inline)) inline void wave_pv(WaveTileState& st,
+                                                             const TileSoftmax& sm,
+                                                             const cdna4::half8_t (&va)[16]) {
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
+}
+
+// The wave's state relative to its own true max: joined O (valid in lanes c < 8: head c,
+// dimensions 16 b + 4 g + i), l summed over the column (every lane), mt. A wave without tiles
+// (any = false) gives mt = -inf, l = 0, O = 0.
+struct WaveResult {
+  float mt, l;
+  f32x4 o[16];
+};
+__device__ __attribute__((always_inline)) inline void wave_result(WaveResult& r,
+                                                                 const WaveTileState& st, bool any) {
+  const float f = any ? __builtin_amdgcn_exp2f(st.m - st.mt) : 0.0f;
+  r.mt = st.mt;
+  r.l = cdna4::sum_xor32(cdna4::sum_xor16(st.l)) * f;
+#pragma unroll
+  for (unsigned b = 0; b < 16; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = st.o[b][i] * f;
+      r.o[b][i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
+    }
+}
+
+// The merge of the four wave results of one head: M = the largest true max, e_w = 2^(mt_w - M)
+// (0 for a wave without keys; all e 0 when no wave has any), L = sum e_w l_w and O = sum e_w O_w,
+// summed over w = 0 .. 3 in order.
+struct WaveMergeScale {
+  float e[4];
+  float m, l;
+};
+__device__ __attribute__((always_inline)) inline WaveMergeScale wave_merge_scale(
+    const float (&mt)[4], const float (&l)[4]) {
+  WaveMergeScale ms;
+  const float M = fmaxf(fmaxf(mt[0], mt[1]), fmaxf(mt[2], mt[3]));
+  const bool none = M == -__builtin_inff();
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    ms.e[w] = none ? 0.0f : __builtin_amdgcn_exp2f(mt[w] - M);
+    L = __builtin_fmaf(ms.e[w], l[w], L);
+  }
+  ms.m = M;
+  ms.l = L;
+  return ms;
+}
+__device__ __attribute__((always_inline)) inline float4 wave_merge_o(const WaveMergeScale& ms,
+                                                                    const float4 (&o)[4]) {
+  float4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    acc.x = __builtin_fmaf(ms.e[w], o[w].x, acc.x);
+    acc.y = __builtin_fmaf(ms.e[w], o[w].y, acc.y);
+    acc.z = __builtin_fmaf(ms.e[w], o[w].z, acc.z);
+    acc.w = __builtin_fmaf(ms.e[w], o[w].w, acc.w);
+  }
+  return acc;
+}
+
+// The exchange of wave results in LDS. O: wave w's chunk d (dimensions 4 d .. 4 d + 3, counted
+// from the area's first block) of head h at float 4 (8 d + h) of its area; mt[8] and l[8] in its
+// ml area. Lanes c < 8 store (consecutive heads in consecutive 16 bytes: no bank conflict).
+__device__ __attribute__((always_inline)) inline void wave_merge_store(float* area_w, float* ml_w,
+                                                                      const WaveResult& r,
+                                                                      unsigned lane, unsigned b0,
+                                                                      unsigned nb) {
+  const unsigned g = lane >> 4, c = lane & 15u;
+  if (c < 8) {
+#pragma unroll
+    for (unsigned b = 0; b < 16; ++b)
+      if (b >= b0 && b < b0 + nb)
+        *reinterpret_cast<float4*>(area_w + 4 * (8 * (4 * (b - b0) + g) + c)) =
+            float4{r.o[b][0], r.o[b][1], r.o[b][2], r.o[b][3]};
+    if (ml_w != nullptr && g == 0) {
+      ml_w[c] = r.mt;
+      ml_w[8 + c] = r.l;
+    }
+  }
+}
+
+// Head h's merge scale from the four ml areas (ml + w * ml_stride).
+__device__ __attribute__((always_inline)) inline WaveMergeScale wave_merge_load_scale(
+    const float* ml, unsigned ml_stride, unsigned h) {
+  float mt[4], l[4];
+#pragma unroll
+  for (unsigned w = 0; w < 4; ++w) {
+    mt[w] = ml[w * ml_stride + h];
+    l[w] = ml[w * ml_stride + 8 + h];
+  }
+  return wave_merge_scale(mt, l);
+}
+
+// Merged chunk d of head h (area chunk index d, dimensions 4 dim_chunk ..) written to the partial.
+__device__ __attribute__((always_inline)) inline void wave_merge_out(
+    const float* area, unsigned stride, const WaveMergeScale& ms, unsigned d, unsigned dim_chunk,
+    unsigned h, float* part_o, std::size_t base) {
+  float4 o[4];
+#pragma unroll
+  for (unsigned w = 0; w < 4; ++w)
+    o[w] = *reinterpret_cast<const float4*>(area + w * stride + 4 * (8 * d + h));
+  *reinterpret_cast<float4*>(part_o + (base * kGroup + h) * attn::kDim + 4 * dim_chunk) =
+      wave_merge_o(ms, o);
+}
+
+__device__ __attribute__((always_inline)) inline void wave_merge_ml_out(const WaveMergeScale& ms,
+                                                                       unsigned h, float* part_m,
+                                                                       float* part_l,
+                                                                       std::size_t base) {
+  part_m[base * kGroup + h] = ms.m * kLn2;  // -inf stays -inf for an empty item
+  part_l[base * kGroup + h] = ms.l;
+}
+
+// Partial (m, l, o) of KV head kvh over keys [span.begin, span.end) at `base`, as
+// split_partial_tiles computes it, with per-wave tiles: wave w takes tiles w, w + 4, ... and the
+// four results merge at the end through the K slots (wave w's result in its own slot, which no
+// other wave reads before the merge barrier). `more`: the workgroup runs another item
+// afterwards (its LDS is then reused).
+template <class Tiles>
+__device__ __attribute__((always_inline)) inline void split_partial_waves(
+    const float* __restrict__ q, const Tiles& tl, AttnSpan span, unsigned kvh, float* part_m,
+    float* part_l, float* part_o, std::size_t base, TileShared& sh, bool more) {
+  using cdna4::half8_t;
+  const unsigned t = threadIdx.x, lane = t & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const unsigned n_tiles = (span.end - span.begin + kTileKeys - 1) / kTileKeys;
+  const unsigned last_row = span.end - 1;  // unused when n_tiles == 0
+  const unsigned nw = n_tiles > wave ? (n_tiles - wave + 3) / 4 : 0;  // this wave's tiles
+  const unsigned k_lds = cdna4::lds_offset(sh.k[wave]), v_lds = cdna4::lds_offset(sh.v[wave]);
+  const WaveCopy cp = wave_copy_offsets(lane);
+  auto issue_k = [&](unsigned ti) __attribute__((always_inline)) {
+    issue_wave_tile<false>(tl, span.begin + ti * kTileKeys, last_row, k_lds, cp, lane);
+  };
+  auto issue_v = [&](unsigned ti) __attribute__((always_inline)) {
+    issue_wave_tile<true>(tl, span.begin + ti * kTileKeys, last_row, v_lds, cp, lane);
+  };
+
+  // The KV head's 8 query rows (wave w: rows 2 w, 2 w + 1), then the wave's first tile.
+#pragma unroll
+  for (unsigned i = 0; i < 2; ++i) {
+    const unsigned h = 2 * wave + i;
+    cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
+                      cdna4::lds_offset(sh.q[h]));
+  }
+  if (nw > 0) {
+    issue_k(wave);
+    issue_v(wave);
+    cdna4::wait_vmcnt<16>();  // the queries and K landed; V may be in flight
+  } else {
+    cdna4::wait_vmcnt<0>();
+  }
+  tile_barrier();
+  const TileLane tln = tile_lane(lane);
+  const WaveOperands op = wave_operands(lane);
+  WaveTileState st;
+  wave_start(st, sh.q, lane, tln);
+
+  // Tile j of the wave (tile ti = w + 4 j): its K landed. Once the K operands are in registers the
+  // next tile's K goes into the slot, once the V operands are, its V. In flight after K of tile
+  // ti: V of tile ti; after V of tile ti: K of the next tile.
+  for (unsigned j = 0; j < nw; ++j) {
+    const unsigned ti = wave + 4 * j;
+    const bool next = j + 1 < nw;
+    half8_t ka[2][8];
+    read_k(ka, k_lds + op.kl);
+    __builtin_amdgcn_sched_barrier(0);  // every K read in flight before the MFMAs
+    f32x4 s[2];
+    wave_scores(s, ka, st);
+    if (next) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the K operands are in registers
+      issue_k(ti + 4);
+      cdna4::wait_vmcnt<16>();  // V of tile ti
+    } else {
+      cdna4::wait_vmcnt<0>();
+    }
+    half8_t va[16];
+    read_v_all(va, v_lds, op.vl);
+    __builtin_amdgcn_sched_barrier(0);  // the V reads in flight under the softmax
+    TileSoftmax sm;
+    wave_softmax(sm, st, s, span.begin + ti * kTileKeys, span.end, j == 0, lane, tln);
+    if (next) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the V operands are in registers
+      issue_v(ti + 4);
+    }
+    wave_pv(st, sm, va);
+    if (next)
+      cdna4::wait_vmcnt<16>();  // K of the next tile
+  }
+
+  // The merge through the K slots: wave w's result in its own slot (O in the first 8 KiB, mt and
+  // l after it), which only it has used.
+  {
+    WaveResult r;
+    wave_result(r, st, nw > 0);
+    float* mine = reinterpret_cast<float*>(sh.k[wave]);
+    wave_merge_store(mine, mine + 8 * attn::kDim, r, lane, 0, 16);
+  }
+  tile_barrier();
+  {
+    constexpr unsigned kStride = kTileBytes / 4;  // floats from one K slot to the next
+    const float* area = reinterpret_cast<const float*>(sh.k[0]);
+    const unsigned h = t % 8, d = t / 8;
+    const WaveMergeScale ms = wave_merge_load_scale(area + 8 * attn::kDim, kStride, h);
+    wave_merge_out(area, kStride, ms, d, d, h, part_o, base);
+    wave_merge_out(area, kStride, ms, d + 32, d + 32, h, part_o, base);
+    if (d == 0)
+      wave_merge_ml_out(ms, h, part_m, part_l, base);
   }
   if (more)
     tile_barrier();  // LDS is reused by the next item
@@ -1835,7 +2248,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
   if (split >= n_splits)
     return;
   const std::size_t kv0 = p.kv_offsets[seq] + std::size_t{kvh} * len * attn::kDim;
-  decode_detail::split_partial_tiles(
+  decode_detail::split_partial_waves(
       p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
       decode_detail::LinearTiles{p.k_cache + kv0, p.v_cache + kv0},
       attn_split_span(len, n_splits, split), kvh, p.part_m, p.part_l, p.part_o,
@@ -1845,13 +2258,14 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
 // The same splits on one workgroup per CU (no reference counterpart). Each workgroup takes items
 // w, w + G, w + 2 G, ... of the batch's (sequence, KV head, split) list (sequence-major, KV head,
 // then split; each workgroup computes the list's sequence offsets itself), so the workgroups'
-// item counts differ by at most one. The K/V ring runs straight across item boundaries: tile
-// tau + 3 of the workgroup's tile sequence is issued while tile tau is processed, whichever item
-// either belongs to, and each item's query rows are copied into one of three LDS slots right
-// after its first tile. Per item the arithmetic, the partial and its layout are
-// split_partial_tiles' (so the partials equal attn_ragged_split_kernel's bit for bit), and
-// attn_ragged_combine_kernel merges them. Batches of up to kRaggedStreamMaxBatch sequences whose
-// per-workgroup item count fits kRaggedStreamMaxItems (attn_ragged_stream_fits).
+// item counts differ by at most one. Per item, wave v takes the item's tiles v, v + 4, ... as
+// split_partial_waves does, and each wave's tile stream runs straight across item boundaries:
+// its next tile, whichever item holds it, is issued as soon as the current one's operands are
+// in registers. Each item's query rows go into one of two LDS slots while the previous item is
+// processed. Per item the arithmetic, the partial and its layout are split_partial_waves' (so
+// the partials equal attn_ragged_split_kernel's bit for bit), and attn_ragged_combine_kernel
+// merges them. Batches of up to kRaggedStreamMaxBatch sequences whose per-workgroup item count
+// fits kRaggedStreamMaxItems (attn_ragged_stream_fits): one item per lane of a wave.
 constexpr unsigned kRaggedStreamMaxBatch = 512;
 constexpr unsigned kRaggedStreamMaxItems = 64;
 
@@ -1863,21 +2277,17 @@ __host__ __device__ constexpr bool attn_ragged_stream_fits(unsigned batch, unsig
 
 namespace decode_detail {
 
-struct StreamItem {
-  std::size_t kv0;        // element offset of the item's K/V head rows
-  unsigned begin, end;    // its key span
-  unsigned seq, kvh;
-  unsigned part;          // its partial's row group: (seq * 2 + kvh) * s_max + split
-  unsigned tiles;         // its 32-key tiles (0 for an empty span)
-};
-
+// 160 KiB: the four waves' K and V slots, two query-row slots, and the O exchange of one merge
+// pass (128 dimensions of four wave results), which the set-up's sequence offsets use before.
 struct alignas(1024) StreamShared {
-  unsigned char k[kTileStages][kTileBytes];
-  unsigned char v[kTileStages][kTileBytes];
-  float q[3][kGroup][attn::kDim];
-  unsigned prefix[kRaggedStreamMaxBatch + 1];
-  StreamItem items[kRaggedStreamMaxItems];
+  unsigned char k[4][kTileBytes];
+  unsigned char v[4][kTileBytes];
+  float q[2][kGroup][attn::kDim];
+  float merge[4][32 * kGroup * 4];
 };
+static_assert(sizeof(StreamShared) == 160 * 1024, "the CU's LDS");
+static_assert((kRaggedStreamMaxBatch + 1) * sizeof(unsigned) <= sizeof(StreamShared::merge),
+              "sequence offsets in the merge area");
 
 }  // namespace decode_detail
 
@@ -1888,15 +2298,16 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
   using namespace decode_detail;
   using cdna4::half8_t;
   __shared__ StreamShared sh;
-  const unsigned t = threadIdx.x, lane = t & 63u, g = lane >> 4, c = lane & 15u;
+  const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned G = gridDim.x, w = blockIdx.x;
+  unsigned* prefix = reinterpret_cast<unsigned*>(sh.merge);
 
   // Sequence offsets of the item list (wave 0: 64 sequences per step, an inclusive scan).
   if (wave == 0) {
     unsigned run = 0;
     if (lane == 0)
-      sh.prefix[0] = 0;
+      prefix[0] = 0;
     for (unsigned base = 0; base < p.batch; base += cdna4::kLanes) {
       const unsigned s_ = base + lane;
       unsigned cnt = 0;
@@ -1911,39 +2322,50 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
         incl += lane >= d ? up : 0u;
       }
       if (s_ < p.batch)
-        sh.prefix[s_ + 1] = run + incl;
+        prefix[s_ + 1] = run + incl;
       run += __shfl(incl, cdna4::kLanes - 1, cdna4::kLanes);
     }
   }
   __syncthreads();
-  const unsigned total = sh.prefix[p.batch];
+  // Every wave holds the descriptors of the workgroup's items, item j in lane j: its K/V head
+  // rows' element offset, key span, partial row group and tile count (0 for an empty span).
+  const unsigned total = prefix[p.batch];
   const unsigned n_items = w < total ? (total - w + G - 1) / G : 0;
-  for (unsigned j = t; j < n_items; j += kBlock) {
-    const unsigned k = w + j * G;
+  unsigned it_kv_lo = 0, it_kv_hi = 0, it_begin = 0, it_end = 0, it_part = 0, it_tiles = 0,
+           it_seq = 0, it_kvh = 0;
+  if (lane < n_items) {
+    const unsigned k = w + lane * G;
     unsigned lo = 0, hi = p.batch;  // the sequence s with prefix[s] <= k < prefix[s + 1]
     while (hi - lo > 1) {
       const unsigned mid = (lo + hi) / 2;
-      if (sh.prefix[mid] <= k)
+      if (prefix[mid] <= k)
         lo = mid;
       else
         hi = mid;
     }
-    const unsigned r = k - sh.prefix[lo], n = (sh.prefix[lo + 1] - sh.prefix[lo]) / 2;
+    const unsigned r = k - prefix[lo], n = (prefix[lo + 1] - prefix[lo]) / 2;
     const unsigned kvh = r / n, split = r % n;
     const unsigned len = p.lens[lo] < p.len_cap ? p.lens[lo] : p.len_cap;
     const AttnSpan span = attn_split_span(len, n, split);
-    sh.items[j] = StreamItem{p.kv_offsets[lo] + std::size_t{kvh} * len * attn::kDim,
-                             span.begin, span.end, lo, kvh,
-                             (lo * attn::kKvHeads + kvh) * p.s_max + split,
-                             (span.end - span.begin + kTileKeys - 1) / kTileKeys};
+    const std::size_t kv0 = p.kv_offsets[lo] + std::size_t{kvh} * len * attn::kDim;
+    it_kv_lo = static_cast<unsigned>(kv0);
+    it_kv_hi = static_cast<unsigned>(kv0 >> 32);
+    it_begin = span.begin;
+    it_end = span.end;
+    it_part = (lo * attn::kKvHeads + kvh) * p.s_max + split;
+    it_tiles = (span.end - span.begin + kTileKeys - 1) / kTileKeys;
+    it_seq = lo;
+    it_kvh = kvh;
   }
-  __syncthreads();
+  auto get = [](unsigned v, unsigned j) __attribute__((always_inline)) {
+    return static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(j)));
+  };
   // Items with an empty span (capped split counts) have no tiles: their partial is written here,
-  // (-inf, 0, 0) as the split writes it, and both cursors below skip them.
+  // (-inf, 0, 0) as the split writes it, and the item loop skips them.
   for (unsigned j = 0; j < n_items; ++j) {
-    const unsigned part = __builtin_amdgcn_readfirstlane(sh.items[j].part);
-    if (__builtin_amdgcn_readfirstlane(sh.items[j].tiles) != 0)
+    if (get(it_tiles, j) != 0)
       continue;
+    const unsigned part = get(it_part, j);
     float* po = p.part_o + std::size_t{part} * kGroup * attn::kDim;
 #pragma unroll
     for (unsigned i = 0; i < kGroup * attn::kDim / kBlock; ++i)
@@ -1953,216 +2375,137 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
       p.part_l[std::size_t{part} * kGroup + t] = 0.0f;
     }
   }
-
-  // Tile cursor over the workgroup's items: tiles of item j in order, items in order.
-  auto item_tiles = [&](unsigned j) __attribute__((always_inline)) {
-    return __builtin_amdgcn_readfirstlane(sh.items[j].tiles);
-  };
   auto next_item = [&](unsigned j) __attribute__((always_inline)) {  // first non-empty >= j
-    while (j < n_items && item_tiles(j) == 0)
+    while (j < n_items && get(it_tiles, j) == 0)
       ++j;
     return j;
   };
-  unsigned total_tiles = 0;
-  for (unsigned j = 0; j < n_items; ++j)
-    total_tiles += item_tiles(j);
-  if (total_tiles == 0)  // uniform
+  // This wave's first tile at or after item j: the first item from j on with more than `wave`
+  // tiles (n_items if none).
+  auto wave_item = [&](unsigned j) __attribute__((always_inline)) {
+    while (j < n_items && get(it_tiles, j) <= wave)
+      ++j;
+    return j;
+  };
+
+  // Vector-memory instructions this wave has issued since the set-up, and the counts right after
+  // the copies the waits below are for: each wait allows what was issued after its copy.
+  unsigned issued = 0;
+  const unsigned k_lds = cdna4::lds_offset(sh.k[wave]), v_lds = cdna4::lds_offset(sh.v[wave]);
+  const WaveCopy cp = wave_copy_offsets(lane);
+  auto tiles_of = [&](unsigned j) __attribute__((always_inline)) {
+    const std::size_t kv0 = (std::size_t{get(it_kv_hi, j)} << 32) | get(it_kv_lo, j);
+    return LinearTiles{p.k_cache + kv0, p.v_cache + kv0};
+  };
+  auto issue_k = [&](unsigned j, unsigned ti) __attribute__((always_inline)) {
+    issue_wave_tile<false>(tiles_of(j), get(it_begin, j) + ti * kTileKeys, get(it_end, j) - 1,
+                           k_lds, cp, lane);
+    issued += 16;
+  };
+  auto issue_v = [&](unsigned j, unsigned ti) __attribute__((always_inline)) {
+    issue_wave_tile<true>(tiles_of(j), get(it_begin, j) + ti * kTileKeys, get(it_end, j) - 1,
+                          v_lds, cp, lane);
+    issued += 16;
+  };
+  auto issue_q = [&](unsigned j, unsigned slot) __attribute__((always_inline)) {
+    const float* q = p.q + std::size_t{get(it_seq, j)} * attn::kQHeads * attn::kDim;
+    const unsigned kvh = get(it_kvh, j);
+#pragma unroll
+    for (unsigned i = 0; i < 2; ++i) {
+      const unsigned h = 2 * wave + i;
+      cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
+                        cdna4::lds_offset(sh.q[slot][h]));
+    }
+    issued += 2;
+  };
+
+  unsigned jc = next_item(0);  // the item being computed
+  if (jc >= n_items)           // uniform
     return;
-
-  const unsigned k_lds0 = cdna4::lds_offset(sh.k[0]) + 4096 * wave;
-  const unsigned v_lds0 = cdna4::lds_offset(sh.v[0]) + 4096 * wave;
-  unsigned koff[4], voff[4];
-#pragma unroll
-  for (unsigned i = 0; i < 4; ++i) {
-    const unsigned jj = 2 * i + (lane >> 5), r = 8 * wave + jj, q_ = lane & 31u;
-    koff[i] = jj * 512 + 16 * tile_swz_k(r, q_) - 1024 * i;
-    voff[i] = jj * 512 + 16 * tile_swz_v(r, q_) - 1024 * i;
+  issue_q(jc, 0);
+  unsigned mark_q = issued;
+  // The wave's tile cursor: item pj, tile pt (pj = n_items: none); the counts after its copies.
+  unsigned pj = wave_item(jc), pt = wave, mark_k = 0, mark_v = 0;
+  if (pj < n_items) {
+    issue_k(pj, pt);
+    mark_k = issued;
+    issue_v(pj, pt);
+    mark_v = issued;
   }
-  // The issue cursor: item ji, its tile ti, global tile tau_i.
-  unsigned ji = next_item(0), ti = 0, tau_i = 0;
-  auto issue_next = [&]() __attribute__((always_inline)) {
-    const StreamItem& it = sh.items[ji];
-    const unsigned begin = __builtin_amdgcn_readfirstlane(it.begin);
-    const unsigned end = __builtin_amdgcn_readfirstlane(it.end);
-    const unsigned kv0_lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(it.kv0));
-    const unsigned kv0_hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(it.kv0 >> 32));
-    const std::size_t kv0 = (std::size_t{kv0_hi} << 32) | kv0_lo;
-    const unsigned stage = tau_i % kTileStages;
-    issue_tile(LinearTiles{p.k_cache + kv0, p.v_cache + kv0}, begin + ti * kTileKeys, end - 1,
-               k_lds0 + stage * kTileBytes, v_lds0 + stage * kTileBytes, koff, voff, wave, lane);
-    if (ti == 0) {  // the item's query rows into slot ji % 3, after its first tile
-      const unsigned seq = __builtin_amdgcn_readfirstlane(it.seq);
-      const unsigned kvh = __builtin_amdgcn_readfirstlane(it.kvh);
-      const float* q = p.q + std::size_t{seq} * attn::kQHeads * attn::kDim;
-#pragma unroll
-      for (unsigned i = 0; i < 2; ++i) {
-        const unsigned h = 2 * wave + i;
-        cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
-                          cdna4::lds_offset(sh.q[ji % 3][h]));
-      }
-    }
-    ++tau_i;
-    if (++ti == item_tiles(ji)) {
-      ti = 0;
-      ji = next_item(ji + 1);
-    }
-  };
-
-  const unsigned kl = 512 * c + 16 * (g ^ (c & 3u)) + 64 * (c >> 2);
-  unsigned vl[4];
-  {
-    const unsigned r = (lane >> 2) & 3u, e = lane & 3u, row = 4 * g + r;
-#pragma unroll
-    for (unsigned b = 0; b < 4; ++b)
-      vl[b] = 512 * row + 32 * ((4 * wave + b) ^ (row & 7u)) + 8 * e;
-  }
-  auto kslot = [&](unsigned tau) __attribute__((always_inline)) {
-    return cdna4::lds_offset(sh.k[tau % kTileStages]) + kl;
-  };
-  auto vslot = [&](unsigned tau) __attribute__((always_inline)) {
-    return cdna4::lds_offset(sh.v[tau % kTileStages]);
-  };
   const TileLane tln = tile_lane(lane);
-  TileState st;
-  f32x4 s_cur[2] = {f32x4{}, f32x4{}};
-
-  // Start item j (its first tile, global tile tau, has landed): state reset, query pairs from its
-  // slot, scores of its first tile.
-  auto start_item = [&](unsigned j, unsigned tau) __attribute__((always_inline)) {
-    st.m = 0.0f;
-    st.mt = -__builtin_inff();
-    st.l = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      st.o[b] = f32x4{};
-    const float* qrow = sh.q[j % 3][c & 7u];
-    constexpr float kScale = kLog2e / 16.0f;
-#pragma unroll
-    for (unsigned s_ = 0; s_ < 8; ++s_) {
-      const float4 x0 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s_ + g));
-      const float4 x1 = *reinterpret_cast<const float4*>(qrow + 8 * (4 * s_ + g) + 4);
-      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      _Float16 hv[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const float v = xs[jj] * kScale;
-        hv[jj] = pair_half(static_cast<_Float16>(v), v, tln);
-      }
-      st.q[s_] = half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
+  const WaveOperands op = wave_operands(lane);
+  const unsigned h = t % 8, d = t / 8;  // the merge's head and dimension chunk
+  WaveTileState st;
+  for (unsigned ord = 0;; ++ord) {
+    wait_vm_at_most(issued - mark_q);  // this wave's query rows of item jc
+    tile_barrier();                    // every wave's
+    wave_start(st, sh.q[ord & 1u], lane, tln);
+    tile_barrier();  // every wave has read slot ord % 2 (its m, l exchange follows below)
+    const unsigned jn = next_item(jc + 1);
+    if (jn < n_items) {  // the next item's query rows into the other slot
+      issue_q(jn, (ord + 1) & 1u);
+      mark_q = issued;
     }
-    half8_t ka[2][8];
-    read_k(ka, kslot(tau));
-#pragma unroll
-    for (unsigned s_ = 0; s_ < 8; ++s_)
-      score_step(s_cur, ka, st.q[s_], s_);
-  };
-  auto softmax_pv = [&](const half8_t (&va)[4], TileSoftmax& sm, bool moved, bool first)
-      __attribute__((always_inline)) {
-    if (moved)
-      tile_rescale(sm, st, first, tln);
-    st.l += sm.lt;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      st.o[b] = mfma16(va[b], sm.pb, st.o[b]);
-  };
-
-  // The first three tiles, then item 0's start.
-  for (unsigned i = 0; i < kTileStages - 1 && tau_i < total_tiles; ++i)
-    issue_next();
-  wait_tiles_after(total_tiles - 1 < 2 ? total_tiles - 1 : 2);
-  tile_barrier();
-  unsigned jc = next_item(0), tc = 0;  // the compute cursor: item jc, its tile tc
-  unsigned jc_tiles = item_tiles(jc);
-  start_item(jc, 0);
-
-  // Partial writes at the end of the previous two iterations (0 or 1 each): their stores count in
-  // vmcnt after tile tau + 1's copy (issued at the top of iteration tau - 2), so the wait for that
-  // tile allows 4 instructions per write -- the 4 16-byte stores every wave issues (lanes 0-7 of
-  // each wave store) -- besides the 8 of a later tile copy. Wave 0's two further stores only make
-  // it wait longer.
-  unsigned wrote1 = 0, wrote2 = 0;
-  for (unsigned tau = 0; tau < total_tiles; ++tau) {
-    const StreamItem& cur = sh.items[jc];
-    const unsigned begin = __builtin_amdgcn_readfirstlane(cur.begin);
-    const unsigned end = __builtin_amdgcn_readfirstlane(cur.end);
-    const unsigned stores = 4 * (wrote1 + wrote2);
-    wrote2 = wrote1;
-    wrote1 = 0;
-    if (tau + 1 < total_tiles) {  // tile tau + 1 lands; every wave is done with tile tau - 1
-      const unsigned ahead = tau_i - (tau + 2);  // copies issued after tile tau + 1's
-      switch ((ahead < 1 ? 8 * ahead : 8) + stores) {
-        case 0: cdna4::wait_vmcnt<0>(); break;
-        case 4: cdna4::wait_vmcnt<4>(); break;
-        case 8: cdna4::wait_vmcnt<8>(); break;
-        case 12: cdna4::wait_vmcnt<12>(); break;
-        default: cdna4::wait_vmcnt<16>(); break;
+    const unsigned begin = get(it_begin, jc), end = get(it_end, jc);
+    bool any = false;
+    while (pj == jc) {
+      const unsigned ti = pt, mk = mark_k, mv = mark_v;
+      // The next tile of this wave: the item's tile ti + 4, else its first tile in a later item.
+      unsigned nj = jc, nt = ti + 4;
+      if (nt >= get(it_tiles, jc)) {
+        nj = wave_item(jc + 1);
+        nt = wave;
       }
-      tile_barrier();
-      if (tau_i < total_tiles)
-        issue_next();  // tile tau + 3, into tile tau - 1's stage
-    }
-    TileSoftmax sm;
-    const unsigned k0 = begin + tc * kTileKeys;
-    if (k0 + kTileKeys > end)  // uniform: only an item's last tile
-      tile_scores_joined<true>(sm, s_cur, st.m, k0, end, lane, tln);
-    else
-      tile_scores_joined<false>(sm, s_cur, st.m, k0, end, lane, tln);
-    half8_t va[4];
-    if (tc + 1 < jc_tiles) {  // scores of the item's next tile under this tile's softmax
+      const bool next = nj < n_items;
+      wait_vm_at_most(issued - mk);  // K of tile ti
       half8_t ka[2][8];
-      read_k(ka, kslot(tau + 1));
-      read_v(va, vslot(tau), vl);
+      read_k(ka, k_lds + op.kl);
       __builtin_amdgcn_sched_barrier(0);
-      f32x4 s_next[2];
-#pragma unroll
-      for (unsigned s_ = 0; s_ < 8; ++s_)
-        score_step(s_next, ka, st.q[s_], s_);
-      const bool moved = tile_decide(sm, st, tc == 0, tln);
-      asm volatile("" : "+v"(sm.lt), "+v"(sm.pb));
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      f32x4 s[2];
+      wave_scores(s, ka, st);
+      if (next) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the K operands are in registers
+        issue_k(nj, nt);
+        mark_k = issued;
       }
-      softmax_pv(va, sm, moved, tc == 0);
-      s_cur[0] = s_next[0];
-      s_cur[1] = s_next[1];
-      ++tc;
-      continue;
+      wait_vm_at_most(issued - mv);  // V of tile ti
+      half8_t va[16];
+      read_v_all(va, v_lds, op.vl);
+      __builtin_amdgcn_sched_barrier(0);
+      TileSoftmax sm;
+      wave_softmax(sm, st, s, begin + ti * kTileKeys, end, !any, lane, tln);
+      if (next) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the V operands are in registers
+        issue_v(nj, nt);
+        mark_v = issued;
+      }
+      wave_pv(st, sm, va);
+      any = true;
+      pj = nj;
+      pt = nt;
     }
-    // The item's last tile: its softmax and P V alone, then its partial.
-    read_v(va, vslot(tau), vl);
-    const bool moved = tile_decide(sm, st, tc == 0, tln);
-    softmax_pv(va, sm, moved, tc == 0);
+    // The item's partial: the four wave results merged in two passes of 128 dimensions through
+    // sh.merge; mt and l through the query slot this item used (read by every wave above).
     {
-      const unsigned part = __builtin_amdgcn_readfirstlane(cur.part);
-      const float f = __builtin_amdgcn_exp2f(st.m - st.mt);
-      const float L = cdna4::sum_xor32(cdna4::sum_xor16(st.l)) * f;
-      const unsigned h = c & 7u;
-#pragma unroll
-      for (unsigned b = 0; b < 4; ++b) {
-        float o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float x = st.o[b][i] * f;
-          o[i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
-        }
-        if (c < 8)
-          *reinterpret_cast<float4*>(p.part_o + (std::size_t{part} * kGroup + h) * attn::kDim +
-                                     64 * wave + 16 * b + 4 * g) = float4{o[0], o[1], o[2], o[3]};
-      }
-      if (wave == 0 && lane < 8) {
-        p.part_m[std::size_t{part} * kGroup + h] = st.mt * kLn2;
-        p.part_l[std::size_t{part} * kGroup + h] = L;
-      }
-      wrote1 = 1;
+      WaveResult r;
+      wave_result(r, st, any);
+      float* ml = &sh.q[ord & 1u][0][0];
+      const std::size_t part = get(it_part, jc);
+      wave_merge_store(sh.merge[wave], ml + 16 * wave, r, lane, 0, 8);
+      tile_barrier();
+      const WaveMergeScale ms = wave_merge_load_scale(ml, 16, h);
+      wave_merge_out(&sh.merge[0][0], 32 * kGroup * 4, ms, d, d, h, p.part_o, part);
+      if (d == 0)
+        wave_merge_ml_out(ms, h, p.part_m, p.part_l, part);
+      tile_barrier();
+      wave_merge_store(sh.merge[wave], nullptr, r, lane, 8, 8);
+      tile_barrier();
+      wave_merge_out(&sh.merge[0][0], 32 * kGroup * 4, ms, d, d + 32, h, p.part_o, part);
+      issued += 2;  // at least one 16-byte store per pass and wave
     }
-    if (tau + 1 < total_tiles) {  // the next item's first tile (tile tau + 1) has landed
-      jc = next_item(jc + 1);
-      tc = 0;
-      jc_tiles = item_tiles(jc);
-      start_item(jc, tau + 1);
-    }
+    jc = jn;
+    if (jc >= n_items)
+      break;
   }
 }
 
@@ -2239,7 +2582,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
       std::size_t{2} * attn::kDim << p.log2_page,
       std::size_t{kvh} * attn::kDim << p.log2_page};
   const AttnSpan span = attn_split_span(len, n_splits, split);
-  decode_detail::split_partial_tiles(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
+  decode_detail::split_partial_waves(p.q + std::size_t{seq} * attn::kQHeads * attn::kDim,
                                      decode_detail::paged_tiles(rows, span), span, kvh, p.part_m,
                                      p.part_l, p.part_o,
                                      (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
