@@ -472,8 +472,14 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
                              lens,   part_m,           part_l,           part_o,
                              batch,  s_max,            max_pages,
                              static_cast<unsigned>(__builtin_ctz(page_size))};
-  k::attn_paged_split_kernel<256>
-      <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
+  // As the ragged decode: one streaming workgroup per CU where the batch fits its item list.
+  const unsigned cus = device_cus();
+  const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(cus, items));
+  if (cus > 0 && k::attn_ragged_stream_fits(batch, s_max, grid))
+    k::attn_paged_stream_kernel<256><<<grid, 256, 0, as_stream(stream)>>>(p);
+  else
+    k::attn_paged_split_kernel<256>
+        <<<static_cast<unsigned>(items), 256, 0, as_stream(stream)>>>(p);
   int rc = launched("miso_attn_decode_paged(split)");
   if (rc != 0)
     return rc;

@@ -1450,34 +1450,54 @@ __device__ __attribute__((always_inline)) inline WaveCopy wave_copy_offsets(unsi
   return cp;
 }
 
+// Row `row` of group G of a tile (K: kV false, V: kV true), for the wave copies. Sources whose
+// rows need the group (the paged stream's per-tile pages) overload it.
+template <bool kV, unsigned G, class Tiles>
+__device__ __attribute__((always_inline)) inline const attn::half_t* tile_group_row(
+    const Tiles& tl, unsigned row) {
+  return kV ? tl.v_at(row) : tl.k_at(row);
+}
+
+// Group G (rows 8 G .. 8 G + 7) of this wave's copy of a tile at key k0 into its slot at lds: 4
+// vector-memory instructions; rows past last_row read last_row instead (they are masked at use),
+// so no load leaves the item's rows.
+template <bool kV, unsigned G, class Tiles>
+__device__ __attribute__((always_inline)) inline void issue_wave_group(const Tiles& tl,
+                                                                      unsigned k0,
+                                                                      unsigned last_row,
+                                                                      unsigned lds,
+                                                                      const WaveCopy& cp,
+                                                                      unsigned lane) {
+  const unsigned gs = k0 + 8 * G;  // the group's first row (wave-uniform)
+  const unsigned(&off)[4] = kV ? cp.voff : cp.koff[G & 1u];
+  if (gs + 7 <= last_row) {
+    issue_rows4(uniform(tile_group_row<kV, G>(tl, gs)), off, lds + 4096 * G);
+  } else {
+    const unsigned row0 = gs <= last_row ? gs : last_row;
+    const unsigned lim = last_row - row0;  // rows of the group past last_row read row0 + lim
+    const attn::half_t* X = tile_group_row<kV, G>(tl, row0);
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i) {
+      const unsigned j = 2 * i + (lane >> 5), r = 8 * G + j, p = lane & 31u;
+      const std::size_t at = std::size_t{j < lim ? j : lim} * attn::kDim;
+      cdna4::lds_load16_nt(X + at + 8 * (kV ? tile_swz_v(r, p) : tile_swz_k(r, p)),
+                           lds + 4096 * G + 1024 * i);
+    }
+  }
+}
+
 // This wave's copy of the whole K (kV false) or V (kV true) tile at key k0 into its slot at lds:
-// 4 groups of 8 rows, always 16 vector-memory instructions; rows past last_row read last_row
-// instead (they are masked at use), so no load leaves the item's rows.
+// 4 groups of 8 rows, always 16 vector-memory instructions.
 template <bool kV, class Tiles>
 __device__ __attribute__((always_inline)) inline void issue_wave_tile(const Tiles& tl, unsigned k0,
                                                                      unsigned last_row,
                                                                      unsigned lds,
                                                                      const WaveCopy& cp,
                                                                      unsigned lane) {
-#pragma unroll
-  for (unsigned g = 0; g < 4; ++g) {
-    const unsigned gs = k0 + 8 * g;  // the group's first row (wave-uniform)
-    const unsigned(&off)[4] = kV ? cp.voff : cp.koff[g & 1u];
-    if (gs + 7 <= last_row) {
-      issue_rows4(uniform(kV ? tl.v_at(gs) : tl.k_at(gs)), off, lds + 4096 * g);
-    } else {
-      const unsigned row0 = gs <= last_row ? gs : last_row;
-      const unsigned lim = last_row - row0;  // rows of the group past last_row read row0 + lim
-      const attn::half_t* X = kV ? tl.v_at(row0) : tl.k_at(row0);
-#pragma unroll
-      for (unsigned i = 0; i < 4; ++i) {
-        const unsigned j = 2 * i + (lane >> 5), r = 8 * g + j, p = lane & 31u;
-        const std::size_t at = std::size_t{j < lim ? j : lim} * attn::kDim;
-        cdna4::lds_load16_nt(X + at + 8 * (kV ? tile_swz_v(r, p) : tile_swz_k(r, p)),
-                             lds + 4096 * g + 1024 * i);
-      }
-    }
-  }
+  issue_wave_group<kV, 0>(tl, k0, last_row, lds, cp, lane);
+  issue_wave_group<kV, 1>(tl, k0, last_row, lds, cp, lane);
+  issue_wave_group<kV, 2>(tl, k0, last_row, lds, cp, lane);
+  issue_wave_group<kV, 3>(tl, k0, last_row, lds, cp, lane);
 }
 
 // The V^T operands of all 16 dimension blocks of a tile (two transpose reads each: rows 4 g + r
@@ -1827,7 +1847,11 @@ __device__ __attribute__((always_inline)) inline void split_items(const AttnSpli
 
 namespace decode_detail {
 
-// Items [first, first + count) of a split launch on the matrix cores (split_partial_tiles).
+// Splits longer than this many keys (8 tiles, two per wave) run with per-wave tiles.
+constexpr unsigned kSplitWavesMinKeys = 8 * kTileKeys;
+
+// Items [first, first + count) of a split launch on the matrix cores (split_partial_waves, or
+// split_partial_tiles for short splits).
 __device__ __attribute__((always_inline)) inline void split_items_mfma(const AttnSplitParams& p,
                                                                        unsigned first,
                                                                        unsigned count) {
@@ -1836,10 +1860,17 @@ __device__ __attribute__((always_inline)) inline void split_items_mfma(const Att
        item += gridDim.x * gridDim.y) {
     const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
     const std::size_t head = std::size_t{kvh} * p.max_ctx * attn::kDim;
-    split_partial_tiles(p.q, LinearTiles{p.k_cache + head, p.v_cache + head},
-                        attn_split_span(p.len, p.n_splits, split), kvh, p.part_m, p.part_l,
-                        p.part_o, std::size_t{kvh} * p.n_splits + split, sh,
-                        item + gridDim.x * gridDim.y < first + count);
+    const AttnSpan span = attn_split_span(p.len, p.n_splits, split);
+    const LinearTiles tl{p.k_cache + head, p.v_cache + head};
+    const std::size_t base = std::size_t{kvh} * p.n_splits + split;
+    const bool more = item + gridDim.x * gridDim.y < first + count;
+    // Per-wave tiles once every wave has more than two of them; a shorter split keeps the
+    // shared ring, whose first three tiles are in flight together (per-wave tiles would wait
+    // for two load latencies one after the other).
+    if (span.end - span.begin > kSplitWavesMinKeys)
+      split_partial_waves(p.q, tl, span, kvh, p.part_m, p.part_l, p.part_o, base, sh, more);
+    else
+      split_partial_tiles(p.q, tl, span, kvh, p.part_m, p.part_l, p.part_o, base, sh, more);
   }
 }
 
@@ -2289,15 +2320,112 @@ static_assert(sizeof(StreamShared) == 160 * 1024, "the CU's LDS");
 static_assert((kRaggedStreamMaxBatch + 1) * sizeof(unsigned) <= sizeof(StreamShared::merge),
               "sequence offsets in the merge area");
 
-}  // namespace decode_detail
+// The batch of a streaming launch, whatever its layout.
+struct StreamBatch {
+  const float* q;  // [batch][16][256] (unscaled)
+  float* part_m;
+  float* part_l;
+  float* part_o;
+  const uint32_t* lens;
+  unsigned batch, s_max, len_cap;
+};
 
-template <int kBlock>
-__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
-attn_ragged_stream_kernel(AttnRaggedParams p) {
-  static_assert(kBlock == 256, "four waves per split workgroup");
-  using namespace decode_detail;
+__device__ __attribute__((always_inline)) inline unsigned lane_value(unsigned v, unsigned j) {
+  return static_cast<unsigned>(
+      __builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(j)));
+}
+
+// Where an item's tiles lie. describe() runs in lane j for item j (its sequence, KV head and
+// capped length); prepare(j, ...) runs, wave-uniform, for a tile before issue<kV>(j, ...) copies
+// its K and V (the same tile, in that order).
+struct RaggedStreamSource {  // contiguous rows: K [2][len][256] at kv_offsets[s]
+  const attn::half_t* k_cache;
+  const attn::half_t* v_cache;
+  const uint64_t* kv_offsets;
+  unsigned kv_lo = 0, kv_hi = 0;  // lane j: item j's element offset
+  __device__ __attribute__((always_inline)) void describe(unsigned seq, unsigned kvh,
+                                                          unsigned len) {
+    const std::size_t kv0 = kv_offsets[seq] + std::size_t{kvh} * len * attn::kDim;
+    kv_lo = static_cast<unsigned>(kv0);
+    kv_hi = static_cast<unsigned>(kv0 >> 32);
+  }
+  __device__ __attribute__((always_inline)) void prepare(unsigned, unsigned, unsigned, unsigned,
+                                                         unsigned) {}
+  template <bool kV>
+  __device__ __attribute__((always_inline)) void issue(unsigned j, unsigned k0, unsigned last_row,
+                                                       unsigned lds, const WaveCopy& cp,
+                                                       unsigned lane) const {
+    const std::size_t kv0 = (std::size_t{lane_value(kv_hi, j)} << 32) | lane_value(kv_lo, j);
+    issue_wave_tile<kV>(LinearTiles{k_cache + kv0, v_cache + kv0}, k0, last_row, lds, cp, lane);
+  }
+};
+
+// The pages of one tile's four 8-row groups (a group never straddles pages: pages hold a
+// multiple of 8 rows and spans start at multiples of 8; a group past the item's last row reads
+// that row, in the page of the group holding it), read from the page table with scalar loads
+// when the tile is prepared, one tile ahead of its copy.
+struct PagedTileRows {
+  const attn::half_t* k_pages;
+  const attn::half_t* v_pages;
+  std::size_t page_halves, head_off;
+  unsigned log2_page;
+  int page0, page1, page2, page3;  // group g's page (the group is a compile-time index below)
+  template <unsigned G>
+  __device__ __attribute__((always_inline)) std::size_t at(unsigned row) const {
+    const int pg = G == 0 ? page0 : G == 1 ? page1 : G == 2 ? page2 : page3;
+    return std::size_t(static_cast<unsigned>(pg)) * page_halves + head_off +
+           std::size_t{row & ((1u << log2_page) - 1u)} * attn::kDim;
+  }
+};
+template <bool kV, unsigned G>
+__device__ __attribute__((always_inline)) inline const attn::half_t* tile_group_row(
+    const PagedTileRows& tl, unsigned row) {
+  return (kV ? tl.v_pages : tl.k_pages) + tl.template at<G>(row);
+}
+
+struct PagedStreamSource {
+  const attn::half_t* k_pages;
+  const attn::half_t* v_pages;
+  const int32_t* page_table;  // [batch][max_pages]
+  unsigned max_pages, log2_page;
+  PagedTileRows next{};
+  __device__ __attribute__((always_inline)) void describe(unsigned, unsigned, unsigned) {}
+  // Tile at key k0 of item (seq, kvh) whose last row is last_row: the page of each group's first
+  // row (or of last_row for groups past it), read through the constant address space so the
+  // loads are scalar (the table is not written by the launch).
+  __device__ __attribute__((always_inline)) void prepare(unsigned seq, unsigned kvh, unsigned k0,
+                                                         unsigned last_row, unsigned) {
+    typedef const __attribute__((address_space(4))) int32_t ctab;
+    ctab* row = (ctab*)(page_table + std::size_t{seq} * max_pages);  // NOLINT: address space
+    next.k_pages = k_pages;
+    next.v_pages = v_pages;
+    next.log2_page = log2_page;
+    next.page_halves = std::size_t{2} * attn::kDim << log2_page;
+    next.head_off = std::size_t{kvh} * attn::kDim << log2_page;
+    auto page_of = [&](unsigned g) __attribute__((always_inline)) {
+      const unsigned r = k0 + 8 * g < last_row ? k0 + 8 * g : last_row;
+      return row[r >> log2_page];
+    };
+    next.page0 = page_of(0);
+    next.page1 = page_of(1);
+    next.page2 = page_of(2);
+    next.page3 = page_of(3);
+  }
+  template <bool kV>
+  __device__ __attribute__((always_inline)) void issue(unsigned, unsigned k0, unsigned last_row,
+                                                       unsigned lds, const WaveCopy& cp,
+                                                       unsigned lane) const {
+    issue_wave_tile<kV>(next, k0, last_row, lds, cp, lane);
+  }
+};
+
+// The streaming split over the batch's items (attn_ragged_stream_kernel's description), with
+// the tiles where Src says they are.
+template <class Src>
+__device__ __attribute__((always_inline)) inline void stream_items(const StreamBatch& p, Src& src,
+                                                                  StreamShared& sh) {
   using cdna4::half8_t;
-  __shared__ StreamShared sh;
+  constexpr unsigned kBlock = 256;
   const unsigned t = threadIdx.x, lane = t & 63u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const unsigned G = gridDim.x, w = blockIdx.x;
@@ -2327,12 +2455,12 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
     }
   }
   __syncthreads();
-  // Every wave holds the descriptors of the workgroup's items, item j in lane j: its K/V head
-  // rows' element offset, key span, partial row group and tile count (0 for an empty span).
+  // Every wave holds the descriptors of the workgroup's items, item j in lane j: key span,
+  // partial row group, tile count (0 for an empty span), sequence and KV head (and what Src
+  // keeps).
   const unsigned total = prefix[p.batch];
   const unsigned n_items = w < total ? (total - w + G - 1) / G : 0;
-  unsigned it_kv_lo = 0, it_kv_hi = 0, it_begin = 0, it_end = 0, it_part = 0, it_tiles = 0,
-           it_seq = 0, it_kvh = 0;
+  unsigned it_begin = 0, it_end = 0, it_part = 0, it_tiles = 0, it_seq = 0, it_kvh = 0;
   if (lane < n_items) {
     const unsigned k = w + lane * G;
     unsigned lo = 0, hi = p.batch;  // the sequence s with prefix[s] <= k < prefix[s + 1]
@@ -2347,9 +2475,7 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
     const unsigned kvh = r / n, split = r % n;
     const unsigned len = p.lens[lo] < p.len_cap ? p.lens[lo] : p.len_cap;
     const AttnSpan span = attn_split_span(len, n, split);
-    const std::size_t kv0 = p.kv_offsets[lo] + std::size_t{kvh} * len * attn::kDim;
-    it_kv_lo = static_cast<unsigned>(kv0);
-    it_kv_hi = static_cast<unsigned>(kv0 >> 32);
+    src.describe(lo, kvh, len);
     it_begin = span.begin;
     it_end = span.end;
     it_part = (lo * attn::kKvHeads + kvh) * p.s_max + split;
@@ -2357,15 +2483,12 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
     it_seq = lo;
     it_kvh = kvh;
   }
-  auto get = [](unsigned v, unsigned j) __attribute__((always_inline)) {
-    return static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(j)));
-  };
   // Items with an empty span (capped split counts) have no tiles: their partial is written here,
   // (-inf, 0, 0) as the split writes it, and the item loop skips them.
   for (unsigned j = 0; j < n_items; ++j) {
-    if (get(it_tiles, j) != 0)
+    if (lane_value(it_tiles, j) != 0)
       continue;
-    const unsigned part = get(it_part, j);
+    const unsigned part = lane_value(it_part, j);
     float* po = p.part_o + std::size_t{part} * kGroup * attn::kDim;
 #pragma unroll
     for (unsigned i = 0; i < kGroup * attn::kDim / kBlock; ++i)
@@ -2376,14 +2499,14 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
     }
   }
   auto next_item = [&](unsigned j) __attribute__((always_inline)) {  // first non-empty >= j
-    while (j < n_items && get(it_tiles, j) == 0)
+    while (j < n_items && lane_value(it_tiles, j) == 0)
       ++j;
     return j;
   };
-  // This wave's first tile at or after item j: the first item from j on with more than `wave`
-  // tiles (n_items if none).
+  // The first item from j on with more than `wave` tiles (n_items if none): where this wave's
+  // next tile lies when the current item has no more of its tiles.
   auto wave_item = [&](unsigned j) __attribute__((always_inline)) {
-    while (j < n_items && get(it_tiles, j) <= wave)
+    while (j < n_items && lane_value(it_tiles, j) <= wave)
       ++j;
     return j;
   };
@@ -2393,23 +2516,23 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
   unsigned issued = 0;
   const unsigned k_lds = cdna4::lds_offset(sh.k[wave]), v_lds = cdna4::lds_offset(sh.v[wave]);
   const WaveCopy cp = wave_copy_offsets(lane);
-  auto tiles_of = [&](unsigned j) __attribute__((always_inline)) {
-    const std::size_t kv0 = (std::size_t{get(it_kv_hi, j)} << 32) | get(it_kv_lo, j);
-    return LinearTiles{p.k_cache + kv0, p.v_cache + kv0};
+  auto prepare = [&](unsigned j, unsigned ti) __attribute__((always_inline)) {
+    src.prepare(lane_value(it_seq, j), lane_value(it_kvh, j),
+                lane_value(it_begin, j) + ti * kTileKeys, lane_value(it_end, j) - 1, j);
   };
   auto issue_k = [&](unsigned j, unsigned ti) __attribute__((always_inline)) {
-    issue_wave_tile<false>(tiles_of(j), get(it_begin, j) + ti * kTileKeys, get(it_end, j) - 1,
-                           k_lds, cp, lane);
+    src.template issue<false>(j, lane_value(it_begin, j) + ti * kTileKeys,
+                              lane_value(it_end, j) - 1, k_lds, cp, lane);
     issued += 16;
   };
   auto issue_v = [&](unsigned j, unsigned ti) __attribute__((always_inline)) {
-    issue_wave_tile<true>(tiles_of(j), get(it_begin, j) + ti * kTileKeys, get(it_end, j) - 1,
-                          v_lds, cp, lane);
+    src.template issue<true>(j, lane_value(it_begin, j) + ti * kTileKeys,
+                             lane_value(it_end, j) - 1, v_lds, cp, lane);
     issued += 16;
   };
   auto issue_q = [&](unsigned j, unsigned slot) __attribute__((always_inline)) {
-    const float* q = p.q + std::size_t{get(it_seq, j)} * attn::kQHeads * attn::kDim;
-    const unsigned kvh = get(it_kvh, j);
+    const float* q = p.q + std::size_t{lane_value(it_seq, j)} * attn::kQHeads * attn::kDim;
+    const unsigned kvh = lane_value(it_kvh, j);
 #pragma unroll
     for (unsigned i = 0; i < 2; ++i) {
       const unsigned h = 2 * wave + i;
@@ -2427,6 +2550,7 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
   // The wave's tile cursor: item pj, tile pt (pj = n_items: none); the counts after its copies.
   unsigned pj = wave_item(jc), pt = wave, mark_k = 0, mark_v = 0;
   if (pj < n_items) {
+    prepare(pj, pt);
     issue_k(pj, pt);
     mark_k = issued;
     issue_v(pj, pt);
@@ -2446,17 +2570,19 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
       issue_q(jn, (ord + 1) & 1u);
       mark_q = issued;
     }
-    const unsigned begin = get(it_begin, jc), end = get(it_end, jc);
+    const unsigned begin = lane_value(it_begin, jc), end = lane_value(it_end, jc);
     bool any = false;
     while (pj == jc) {
       const unsigned ti = pt, mk = mark_k, mv = mark_v;
       // The next tile of this wave: the item's tile ti + 4, else its first tile in a later item.
       unsigned nj = jc, nt = ti + 4;
-      if (nt >= get(it_tiles, jc)) {
+      if (nt >= lane_value(it_tiles, jc)) {
         nj = wave_item(jc + 1);
         nt = wave;
       }
       const bool next = nj < n_items;
+      if (next)
+        prepare(nj, nt);
       wait_vm_at_most(issued - mk);  // K of tile ti
       half8_t ka[2][8];
       read_k(ka, k_lds + op.kl);
@@ -2490,7 +2616,7 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
       WaveResult r;
       wave_result(r, st, any);
       float* ml = &sh.q[ord & 1u][0][0];
-      const std::size_t part = get(it_part, jc);
+      const std::size_t part = lane_value(it_part, jc);
       wave_merge_store(sh.merge[wave], ml + 16 * wave, r, lane, 0, 8);
       tile_barrier();
       const WaveMergeScale ms = wave_merge_load_scale(ml, 16, h);
@@ -2507,6 +2633,20 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
     if (jc >= n_items)
       break;
   }
+}
+
+}  // namespace decode_detail
+
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_ragged_stream_kernel(AttnRaggedParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  __shared__ decode_detail::StreamShared sh;
+  decode_detail::RaggedStreamSource src{p.k_cache, p.v_cache, p.kv_offsets};
+  decode_detail::stream_items(
+      decode_detail::StreamBatch{p.q, p.part_m, p.part_l, p.part_o, p.lens, p.batch, p.s_max,
+                                 p.len_cap},
+      src, sh);
 }
 
 // One 64-thread workgroup per (sequence, head, 64-dim tile); the merge is combine_wave's. (A
@@ -2587,6 +2727,23 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
                                      p.part_l, p.part_o,
                                      (std::size_t{seq} * attn::kKvHeads + kvh) * p.s_max + split,
                                      sh, false);
+}
+
+// The paged splits on one workgroup per CU (no reference counterpart): attn_ragged_stream_kernel
+// over a paged cache, each tile's pages read from the page table one tile ahead of its copy.
+// The partials equal attn_paged_split_kernel's (and the contiguous ragged ones) bit for bit; the
+// same limits (attn_ragged_stream_fits).
+template <int kBlock>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_paged_stream_kernel(AttnPagedParams p) {
+  static_assert(kBlock == 256, "four waves per split workgroup");
+  __shared__ decode_detail::StreamShared sh;
+  decode_detail::PagedStreamSource src{p.k_pages, p.v_pages, p.page_table, p.max_pages,
+                                       p.log2_page};
+  decode_detail::stream_items(
+      decode_detail::StreamBatch{p.q, p.part_m, p.part_l, p.part_o, p.lens, p.batch, p.s_max,
+                                 attn_paged_len_cap(p.max_pages, p.log2_page)},
+      src, sh);
 }
 
 }  // namespace miso::kernels

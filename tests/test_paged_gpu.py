@@ -87,6 +87,14 @@ def test_paged_c5_shape(O, attn, torch_mod):
     assert np.array_equal(ragged.view(np.uint32), paged.view(np.uint32))
 
 
+def test_paged_wide_batch_fallback(O, attn, torch_mod):
+    """600 sequences, above the streaming kernels' batch limit: both layouts run one workgroup
+    per (sequence, KV head, split) slot, still bit-identical."""
+    lens = np.random.default_rng(601).integers(0, 700, 600).astype(np.uint32)
+    _, ragged, paged = run_both(O, attn, torch_mod, lens, 601, 16)
+    assert np.array_equal(ragged.view(np.uint32), paged.view(np.uint32))
+
+
 def test_paged_empty_sequence_is_zero(O, attn, torch_mod):
     lens = np.array([5, 0, 9], np.uint32)
     _, ragged, paged = run_both(O, attn, torch_mod, lens, 6, 8, max_len=16)

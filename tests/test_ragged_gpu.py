@@ -70,9 +70,10 @@ def check_all(O, attn, torch, lens, seed, max_len=None, name="ragged"):
 
 
 def test_ragged_stream_many_short_items(O, attn, torch_mod):
-    """The streaming split (one workgroup per CU, the K/V ring running across items) over many
-    items of one or two 32-key tiles -- query rows cycle through the three LDS slots at every
-    tile -- with empty sequences among them and a few long ones."""
+    """The streaming split (one workgroup per CU, each wave's tile stream running across items)
+    over many items of one or two 32-key tiles -- most waves have no tile in most items, and the
+    query rows alternate between the two LDS slots at every item -- with empty sequences among
+    them and a few long ones."""
     rng = np.random.default_rng(300)
     lens = rng.integers(1, 65, 300).astype(np.uint32)
     lens[::37] = 0
@@ -94,3 +95,25 @@ def test_ragged_wide_batch_fallback(O, attn, torch_mod):
     rng = np.random.default_rng(600)
     lens = rng.integers(0, 700, 600).astype(np.uint32)
     check_all(O, attn, torch_mod, lens, 600, name="fallback batch")
+
+
+def test_ragged_stream_equals_split_kernel(O, attn, torch_mod):
+    """The streaming kernel and the one-workgroup-per-split kernel compute each item the same
+    way: a 600-sequence batch (above the streaming limit of 512) and its first 100 sequences as
+    a batch of their own (streamed) give bit-identical rows."""
+    torch = torch_mod
+    rng = np.random.default_rng(602)
+    lens = rng.integers(0, 1100, 600).astype(np.uint32)
+    r = O.ragged_inputs(602, lens)
+    q, gate = to_dev(torch, r["q"]), to_dev(torch, r["gate"])
+    k, v = to_dev(torch, r["k"]), to_dev(torch, r["v"])
+    offs, d_lens = to_dev(torch, r["offsets"]), to_dev(torch, r["lens"])
+    out = {}
+    for batch in (600, 100):
+        sc = attn.RaggedScratch(batch, int(lens[:batch].max()))
+        core = torch.full((batch * H * D,), -9123.5, device="cuda")
+        attn.attn_decode_ragged(q[:batch * H * D], gate[:batch * H * D], k, v, offs[:batch],
+                                d_lens[:batch], core, sc)
+        torch.cuda.synchronize()
+        out[batch] = to_host(core).reshape(batch, H, D)
+    assert np.array_equal(out[600][:100].view(np.uint32), out[100].view(np.uint32))
