@@ -74,6 +74,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-other", action="store_true", help="skip the C1 / C3 / C5 lines")
+    ap.add_argument("--other", default=None,
+                    help="comma-separated subset of the other configurations: C2var (the C2 "
+                         "variants: f16 query, VALU split, combine curve, fused, cap 60), C1, "
+                         "C3, C5 (with C5_paged), fp8 (C2_fp8, C4_fp8), gemv, qgemm, layer")
     ap.add_argument("--split-valu", action="store_true",
                     help="with --no-other: still time the VALU form of the C2 split (for "
                          "counter runs of both split forms)")
@@ -425,315 +429,317 @@ def synthetic_q6k(torch, gen, copies, n, k):
 
 
 def bench_other(torch, A, args):
-    """C1, C3 and C5 of the survey's configuration table (synthetic N(0,1) inputs)."""
+    """The other configurations (synthetic N(0,1) inputs): C1, C3, C5 (contiguous and paged),
+    C2 / C4 over an fp8 cache, the projection GEMVs and GEMMs, the layer step. --other picks a
+    subset (for profiler runs)."""
     import numpy as np
     out = {}
-    # C1: decode at ctx 512 (1 MiB of K/V: cache-resident, latency-bound).
-    L = 512
+    pick = None if args.other is None else set(args.other.split(","))
+
+    def want(name):
+        return pick is None or name in pick
+
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(L)
-    q = torch.randn(H * D, generator=gen, device="cuda")
-    qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
-    k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
-    v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
-    sc = A.DecodeScratch(args.max_splits)
-    n1 = A.attn_n_splits(L, args.max_splits)
-    core = torch.empty(H * D, device="cuda")
-    g = graph_of(torch, lambda i: A.attn_decode(q, qg, k, v, core, sc, L, L, n1), 6)
-    time_replays(torch, g, 2)
-    ms = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1]
-    t1 = ms / 120
-    out["C1"] = {"workload": "decode, 1 sequence x 1 token, ctx 512 (warm cache)",
-                 "us_per_call": round(t1 * 1e3, 3), "n_splits": n1,
-                 "gbs": round(2048 * L / (t1 * 1e-3) / 1e9, 1)}
-    # C3: causal prefill, 2048 tokens, empty cache.
-    n3 = 2048
-    gen.manual_seed(n3)
-    q = torch.randn(n3 * H * D, generator=gen, device="cuda")
-    qg = torch.randn(n3 * H * 2 * D, generator=gen, device="cuda")
-    k = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
-    v = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
-    core = torch.empty(n3 * H * D, device="cuda")
-    flop3 = 4.0 * H * D * (n3 * (n3 + 1) // 2)
-    # Ten calls per graph (one call per replay is bound by the replay launch, ~89 us here), the
-    # balanced form (miso_attn_prefill_ws) and the one-workgroup-per-block form side by side.
-    scratch = A.PrefillScratch(n3)
-    t3 = {}
-    for form, sc in (("balanced", scratch), ("one_block", None)):
-        g = graph_of(torch, lambda i: A.attn_prefill(q, qg, k, v, core, 0, n3, n3, scratch=sc), 10)
-        time_replays(torch, g, 1)
-        t3[form] = sorted(time_replays(torch, g, 2)[0] for _ in range(3))[1] / 20
-        del g
-    out["C3"] = {"workload": "causal prefill, 2048 tokens, empty cache (balanced form)",
-                 "ms_per_call": round(t3["balanced"], 4),
-                 "tflops": round(flop3 / (t3["balanced"] * 1e-3) / 1e12, 1),
-                 "frac": round(flop3 / (t3["balanced"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                 "one_block_ms_per_call": round(t3["one_block"], 4),
-                 "one_block_tflops": round(flop3 / (t3["one_block"] * 1e-3) / 1e12, 1)}
-    del q, qg, k, v, core, scratch
-    # C5: ragged decode, 64 sequences, lengths uniform in [1024, 16384] (numpy, seed 64).
-    lens = np.random.default_rng(64).integers(1024, 16385, 64).astype(np.int64)
-    offs = np.zeros(64, dtype=np.int64)
-    offs[1:] = np.cumsum(lens * KV * D)[:-1]
-    total = int((lens * KV * D).sum())
-    gen.manual_seed(64)
-    qb = torch.randn(64 * H * D, generator=gen, device="cuda")
-    gate = torch.randn(64 * H * D, generator=gen, device="cuda")
-    kc = torch.randn(total, generator=gen, device="cuda").half()
-    vc = torch.randn(total, generator=gen, device="cuda").half()
-    d_offs = torch.from_numpy(offs).cuda()
-    d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
-    scr = A.RaggedScratch(64, int(lens.max()))
-    core = torch.empty(64 * H * D, device="cuda")
-    g = graph_of(torch, lambda i: A.attn_decode_ragged(qb, gate, kc, vc, d_offs, d_lens, core,
-                                                       scr), 1)
-    time_replays(torch, g, 2)
-    ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
-    t5 = ms / 10
-    bytes5 = 2048.0 * float(lens.sum())
-    out["C5"] = {"workload": "ragged decode, 64 sequences x 1 token, lengths U[1024,16384] "
-                             "(numpy seed 64), dense sigmoid gate",
-                 "sum_len": int(lens.sum()), "ms_per_call": round(t5, 4),
-                 "gbs": round(bytes5 / (t5 * 1e-3) / 1e9, 1),
-                 "frac": round(bytes5 / (t5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    del kc, vc
-    # C5 over a KV page pool: the same lengths, 16-row pages in a random order.
-    page = 16
-    npg = (lens + page - 1) // page
-    max_pages = int(npg.max())
-    pool = int(npg.sum())
-    perm = np.random.default_rng(65).permutation(pool).astype(np.int32)
-    table = np.zeros((64, max_pages), np.int32)
-    starts = np.concatenate([[0], np.cumsum(npg)[:-1]])
-    for s_, (st, n_) in enumerate(zip(starts, npg)):
-        table[s_, :n_] = perm[st:st + n_]
-    kp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
-    vp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
-    d_table = torch.from_numpy(table).cuda()
-    g = graph_of(torch, lambda i: A.attn_decode_paged(qb, gate, kp, vp, d_table, page, d_lens,
-                                                      core, scr), 1)
-    time_replays(torch, g, 2)
-    ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
-    t5p = ms / 10
-    out["C5_paged"] = {"workload": "C5 with the K/V in a pool of 16-row pages in a random order "
-                                   "(page table per sequence)",
-                       "page_size": page, "pages": pool, "ms_per_call": round(t5p, 4),
-                       "gbs": round(bytes5 / (t5p * 1e-3) / 1e9, 1),
-                       "frac": round(bytes5 / (t5p * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    del kp, vp
-    # C2 over an fp8 (e4m3 rows) cache: the same context and buffer rotation as the C2 line,
-    # each cache encoded on the GPU from an N(0,1) f16 cache.
-    L, R = args.ctx, args.buffers
-    gen.manual_seed(L + 1)
-    q = torch.randn(H * D, generator=gen, device="cuda")
-    qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
-    caches8 = []
-    for _ in range(R):
+    if want("C1"):
+        # C1: decode at ctx 512 (1 MiB of K/V: cache-resident, latency-bound).
+        L = 512
+        gen.manual_seed(L)
+        q = torch.randn(H * D, generator=gen, device="cuda")
+        qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
         k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
         v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
-        c8 = A.Fp8Cache(L)
-        A.attn_kv_encode_fp8(k, v, c8, 0, L)
-        caches8.append(c8)
-    del k, v
-    sc = A.DecodeScratch(args.max_splits)
-    n8 = A.attn_n_splits(L, args.max_splits)
-    core = torch.empty(H * D, device="cuda")
-    g = graph_of(torch, lambda i: A.attn_decode_fp8(q, qg, caches8[i % R], core, sc, L, n8), R)
-    time_replays(torch, g, 2)
-    reps = max(1, (args.steps + R - 1) // R)
-    ms = sorted(time_replays(torch, g, reps)[0] for _ in range(3))[1]
-    t8 = ms / (reps * R)
-    bytes8 = 2.0 * KV * L * (D + 4)  # codes and row scales of K and V
-    out["C2_fp8"] = {"workload": f"C2 (decode, 1 sequence x 1 token, ctx {L}) over an e4m3-row "
-                                 "KV cache (1-byte codes + one f32 scale per row)",
-                     "us_per_step": round(t8 * 1e3, 2), "n_splits": n8,
-                     "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
-                     "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    del caches8
-    # C4 over an e4m3-row cache: the 16384 rows widened to f16 into a workspace each call, then
-    # the f16 prefill (attn_prefill_fp8).
-    if not args.no_prefill:
-        pos0, n = 8192, 8192
-        m4 = pos0 + n
-        gen.manual_seed(m4 + 1)
-        q4 = torch.randn(n * H * D, generator=gen, device="cuda")
-        qg4 = torch.randn(n * H * 2 * D, generator=gen, device="cuda")
-        c8 = A.Fp8Cache(m4)
-        A.attn_kv_encode_fp8(torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
-                             torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
-                             c8, 0, m4)
-        ws4 = A.Fp8PrefillScratch(m4)
-        core4 = torch.empty(n * H * D, device="cuda")
-        g = graph_of(torch, lambda _: A.attn_prefill_fp8(q4, qg4, c8, core4, pos0, n, ws4), 1)
+        sc = A.DecodeScratch(args.max_splits)
+        n1 = A.attn_n_splits(L, args.max_splits)
+        core = torch.empty(H * D, device="cuda")
+        g = graph_of(torch, lambda i: A.attn_decode(q, qg, k, v, core, sc, L, L, n1), 6)
+        time_replays(torch, g, 2)
+        ms = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1]
+        t1 = ms / 120
+        out["C1"] = {"workload": "decode, 1 sequence x 1 token, ctx 512 (warm cache)",
+                     "us_per_call": round(t1 * 1e3, 3), "n_splits": n1,
+                     "gbs": round(2048 * L / (t1 * 1e-3) / 1e9, 1)}
+    if want("C3"):
+        # C3: causal prefill, 2048 tokens, empty cache.
+        n3 = 2048
+        gen.manual_seed(n3)
+        q = torch.randn(n3 * H * D, generator=gen, device="cuda")
+        qg = torch.randn(n3 * H * 2 * D, generator=gen, device="cuda")
+        k = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
+        v = torch.randn(KV * n3 * D, generator=gen, device="cuda").half()
+        core = torch.empty(n3 * H * D, device="cuda")
+        flop3 = 4.0 * H * D * (n3 * (n3 + 1) // 2)
+        # Ten calls per graph (one call per replay is bound by the replay launch, ~89 us here), the
+        # balanced form (miso_attn_prefill_ws) and the one-workgroup-per-block form side by side.
+        scratch = A.PrefillScratch(n3)
+        t3 = {}
+        for form, sc in (("balanced", scratch), ("one_block", None)):
+            g = graph_of(torch, lambda i: A.attn_prefill(q, qg, k, v, core, 0, n3, n3, scratch=sc), 10)
+            time_replays(torch, g, 1)
+            t3[form] = sorted(time_replays(torch, g, 2)[0] for _ in range(3))[1] / 20
+            del g
+        out["C3"] = {"workload": "causal prefill, 2048 tokens, empty cache (balanced form)",
+                     "ms_per_call": round(t3["balanced"], 4),
+                     "tflops": round(flop3 / (t3["balanced"] * 1e-3) / 1e12, 1),
+                     "frac": round(flop3 / (t3["balanced"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "one_block_ms_per_call": round(t3["one_block"], 4),
+                     "one_block_tflops": round(flop3 / (t3["one_block"] * 1e-3) / 1e12, 1)}
+        del q, qg, k, v, core, scratch
+    if want("C5"):
+        # C5: ragged decode, 64 sequences, lengths uniform in [1024, 16384] (numpy, seed 64).
+        lens = np.random.default_rng(64).integers(1024, 16385, 64).astype(np.int64)
+        offs = np.zeros(64, dtype=np.int64)
+        offs[1:] = np.cumsum(lens * KV * D)[:-1]
+        total = int((lens * KV * D).sum())
+        gen.manual_seed(64)
+        qb = torch.randn(64 * H * D, generator=gen, device="cuda")
+        gate = torch.randn(64 * H * D, generator=gen, device="cuda")
+        kc = torch.randn(total, generator=gen, device="cuda").half()
+        vc = torch.randn(total, generator=gen, device="cuda").half()
+        d_offs = torch.from_numpy(offs).cuda()
+        d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
+        scr = A.RaggedScratch(64, int(lens.max()))
+        core = torch.empty(64 * H * D, device="cuda")
+        g = graph_of(torch, lambda i: A.attn_decode_ragged(qb, gate, kc, vc, d_offs, d_lens, core,
+                                                           scr), 1)
+        time_replays(torch, g, 2)
+        ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
+        t5 = ms / 10
+        bytes5 = 2048.0 * float(lens.sum())
+        out["C5"] = {"workload": "ragged decode, 64 sequences x 1 token, lengths U[1024,16384] "
+                                 "(numpy seed 64), dense sigmoid gate",
+                     "sum_len": int(lens.sum()), "ms_per_call": round(t5, 4),
+                     "gbs": round(bytes5 / (t5 * 1e-3) / 1e9, 1),
+                     "frac": round(bytes5 / (t5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del kc, vc
+        # C5 over a KV page pool: the same lengths, 16-row pages in a random order.
+        page = 16
+        npg = (lens + page - 1) // page
+        max_pages = int(npg.max())
+        pool = int(npg.sum())
+        perm = np.random.default_rng(65).permutation(pool).astype(np.int32)
+        table = np.zeros((64, max_pages), np.int32)
+        starts = np.concatenate([[0], np.cumsum(npg)[:-1]])
+        for s_, (st, n_) in enumerate(zip(starts, npg)):
+            table[s_, :n_] = perm[st:st + n_]
+        kp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
+        vp = torch.randn(pool * KV * page * D, generator=gen, device="cuda").half()
+        d_table = torch.from_numpy(table).cuda()
+        g = graph_of(torch, lambda i: A.attn_decode_paged(qb, gate, kp, vp, d_table, page, d_lens,
+                                                          core, scr), 1)
+        time_replays(torch, g, 2)
+        ms = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1]
+        t5p = ms / 10
+        out["C5_paged"] = {"workload": "C5 with the K/V in a pool of 16-row pages in a random order "
+                                       "(page table per sequence)",
+                           "page_size": page, "pages": pool, "ms_per_call": round(t5p, 4),
+                           "gbs": round(bytes5 / (t5p * 1e-3) / 1e9, 1),
+                           "frac": round(bytes5 / (t5p * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del kp, vp
+    if want("fp8"):
+        # C2 over an fp8 (e4m3 rows) cache: the same context and buffer rotation as the C2 line,
+        # each cache encoded on the GPU from an N(0,1) f16 cache.
+        L, R = args.ctx, args.buffers
+        gen.manual_seed(L + 1)
+        q = torch.randn(H * D, generator=gen, device="cuda")
+        qg = torch.randn(H * 2 * D, generator=gen, device="cuda")
+        caches8 = []
+        for _ in range(R):
+            k = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+            v = torch.randn(KV * L * D, generator=gen, device="cuda").half()
+            c8 = A.Fp8Cache(L)
+            A.attn_kv_encode_fp8(k, v, c8, 0, L)
+            caches8.append(c8)
+        del k, v
+        sc = A.DecodeScratch(args.max_splits)
+        n8 = A.attn_n_splits(L, args.max_splits)
+        core = torch.empty(H * D, device="cuda")
+        g = graph_of(torch, lambda i: A.attn_decode_fp8(q, qg, caches8[i % R], core, sc, L, n8), R)
+        time_replays(torch, g, 2)
+        reps = max(1, (args.steps + R - 1) // R)
+        ms = sorted(time_replays(torch, g, reps)[0] for _ in range(3))[1]
+        t8 = ms / (reps * R)
+        bytes8 = 2.0 * KV * L * (D + 4)  # codes and row scales of K and V
+        out["C2_fp8"] = {"workload": f"C2 (decode, 1 sequence x 1 token, ctx {L}) over an e4m3-row "
+                                     "KV cache (1-byte codes + one f32 scale per row)",
+                         "us_per_step": round(t8 * 1e3, 2), "n_splits": n8,
+                         "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
+                         "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del caches8
+        # C4 over an e4m3-row cache: the 16384 rows widened to f16 into a workspace each call, then
+        # the f16 prefill (attn_prefill_fp8).
+        if not args.no_prefill:
+            pos0, n = 8192, 8192
+            m4 = pos0 + n
+            gen.manual_seed(m4 + 1)
+            q4 = torch.randn(n * H * D, generator=gen, device="cuda")
+            qg4 = torch.randn(n * H * 2 * D, generator=gen, device="cuda")
+            c8 = A.Fp8Cache(m4)
+            A.attn_kv_encode_fp8(torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
+                                 torch.randn(KV * m4 * D, generator=gen, device="cuda").half(),
+                                 c8, 0, m4)
+            ws4 = A.Fp8PrefillScratch(m4)
+            core4 = torch.empty(n * H * D, device="cuda")
+            g = graph_of(torch, lambda _: A.attn_prefill_fp8(q4, qg4, c8, core4, pos0, n, ws4), 1)
+            time_replays(torch, g, 1)
+            t4 = sorted(time_replays(torch, g, args.prefill_steps)[0]
+                        for _ in range(3))[1] / args.prefill_steps
+            flop4 = 4.0 * H * D * (n * pos0 + n * (n + 1) // 2)
+            out["C4_fp8"] = {"workload": "C4 (causal prefill, 8192 tokens after an 8192-token prefix) "
+                                         "over an e4m3-row cache: rows widened to f16, then the f16 "
+                                         "prefill",
+                             "ms_per_call": round(t4, 4),
+                             "tflops": round(flop4 / (t4 * 1e-3) / 1e12, 1)}
+            del c8, ws4, q4, qg4, core4
+    if want("gemv"):
+        # The projection GEMVs (row f4), f16 activations as the engine; weights rotated over >= 512 MB
+        # of copies so they stream from HBM as a model's layers do.
+        def rotated(nbytes):
+            return max(2, -(-(512 << 20) // nbytes))
+
+        def timed(fn, copies):
+            g = graph_of(torch, fn, copies)
+            time_replays(torch, g, 1)
+            return sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / (3 * copies)
+
+        def line(wbytes, t, copies, **extra):
+            return {**extra, "weight_bytes": wbytes, "us_per_call": round(t * 1e3, 2),
+                    "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                    "frac": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "weight_copies_rotated": copies}
+
+        x2048 = torch.randn(2048, generator=gen, device="cuda")
+        x4096 = torch.randn(4096, generator=gen, device="cuda")
+        gemv = {}
+        for name, k, n in (("attn_q", 2048, 8192), ("attn_k", 2048, 512), ("attn_output", 4096, 2048)):
+            wbytes = n * k // 256 * 144
+            copies = rotated(wbytes)
+            wq = synthetic_q4k(torch, gen, copies, n, k)
+            yg = torch.empty(n, device="cuda")
+            xg = x2048 if k == 2048 else x4096
+            t = timed(lambda i: A.q4k_gemv(wq[i % copies], xg, yg, n, k), copies)
+            gemv[name] = line(wbytes, t, copies, k=k, n_rows=n)
+            del wq
+        out["F4_q4k_gemv"] = {"workload": "Q4_K r1 GEMV y = W x with f16 activations at the engine's "
+                                          "Q4_K attention projections (synthetic blocks, HBM-resident "
+                                          "weights)", **gemv}
+        # attn_v is Q6_K (2048 -> 512); the engine's gemv_pair runs it with attn_q in one launch.
+        w6b, w4b = 512 * A.q6k_row_bytes(2048), 8192 * 2048 // 256 * 144
+        copies = rotated(w6b)
+        w6 = synthetic_q6k(torch, gen, copies, 512, 2048)
+        y6 = torch.empty(512, device="cuda")
+        t6 = timed(lambda i: A.q6k_gemv(w6[i % copies], x2048, y6, 512, 2048), copies)
+        del w6
+        copies_p = rotated(w4b + w6b)
+        w4 = synthetic_q4k(torch, gen, copies_p, 8192, 2048)
+        w6 = synthetic_q6k(torch, gen, copies_p, 512, 2048)
+        y4 = torch.empty(8192, device="cuda")
+        tp = timed(lambda i: A.q4k_q6k_gemv_pair(w4[i % copies_p], 8192, y4, w6[i % copies_p], 512, y6,
+                                                 x2048), copies_p)
+        wk = synthetic_q4k(torch, gen, copies_p, 512, 2048)
+        yk = torch.empty(512, device="cuda")
+        tq = timed(lambda i: A.qkv_gemv(w4[i % copies_p], 8192, y4, wk[i % copies_p], 512, yk,
+                                        w6[i % copies_p], 512, y6, x2048), copies_p)
+        del w4, w6, wk
+        out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired "
+                                          "with attn_q in one launch (synthetic blocks, HBM-resident "
+                                          "weights)",
+                              "attn_v": line(w6b, t6, copies, k=2048, n_rows=512),
+                              "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p),
+                              "attn_q_k_v_one_launch": line(w4b + w6b + 512 * 2048 // 256 * 144, tq,
+                                                            copies_p)}
+    if want("qgemm"):
+        # Prefill projection GEMMs (row f4, kernels/qgemm.hpp) at a 4096-token chunk (the layer's
+        # retuned prefill chunk): TFLOP/s of 2 n_tok n k over the dequantized product.
+        n_tok = 4096
+        gemm = {}
+        for name, fmt, k, n in (("attn_q", "q4_k", 2048, 8192), ("attn_k", "q4_k", 2048, 512),
+                                ("attn_v", "q6_k", 2048, 512), ("attn_output", "q4_k", 4096, 2048)):
+            xa = torch.randn(n_tok * k, generator=gen, device="cuda")
+            inp = A.GemmInput(n_tok, k)
+            A.gemm_input(xa, k, n_tok, inp)
+            wg = (synthetic_q4k(torch, gen, 1, n, k) if fmt == "q4_k"
+                  else synthetic_q6k(torch, gen, 1, n, k))[0]
+            ya = torch.empty(n_tok * n, device="cuda")
+            tg = timed(lambda i: A.gemm(wg, fmt, n, k, inp, ya, n), 4)
+            ta = timed(lambda i: A.gemm_input(xa, k, n_tok, inp), 4)
+            fl = 2.0 * n_tok * n * k
+            gemm[name] = {"format": fmt, "k": k, "n_rows": n, "us_per_call": round(tg * 1e3, 2),
+                          "tflops": round(fl / (tg * 1e-3) / 1e12, 1),
+                          "frac": round(fl / (tg * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                          "gemm_input_us": round(ta * 1e3, 2)}
+            del xa, inp, wg, ya
+        out["F4_qgemm"] = {"workload": f"prefill projection GEMMs over Q4_K / Q6_K r1 weights, "
+                                       f"{n_tok} tokens, f16 activations (gemm_input) and f16 MFMA "
+                                       f"with f32 accumulation; TFLOP/s of 2 n_tok n k",
+                           "tokens": n_tok, **gemm}
+    if want("layer"):
+        # Row f3: one attention layer step through the engine wiring (miso_attn_layer_*), synthetic
+        # Q4_K (q, k, o) and Q6_K (v) weights of the engine's shapes.
+        gen.manual_seed(33)
+        layer = A.Layer((synthetic_q4k(torch, gen, 1, 8192, 2048)[0], "q4_k"),
+                        (synthetic_q4k(torch, gen, 1, 512, 2048)[0], "q4_k"),
+                        (synthetic_q6k(torch, gen, 1, 512, 2048)[0], "q6_k"),
+                        (synthetic_q4k(torch, gen, 1, 2048, 4096)[0], "q4_k"),
+                        torch.ones(2048, device="cuda"), torch.ones(D, device="cuda"),
+                        torch.ones(D, device="cuda"),
+                        (1e7 ** (-torch.arange(32, device="cuda") / 32.0)).float())
+        lws = A.LayerWorkspace(4096)
+        Ld = 32768
+        lk = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
+        lv = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
+        h = torch.randn(2048, generator=gen, device="cuda")
+        dl = torch.randn(2048, generator=gen, device="cuda") * 0.1
+        y = torch.empty(2048, device="cuda")
+        g = graph_of(torch, lambda _: A.layer_decode(layer, lk, lv, Ld, Ld - 1, h, dl, y, 1e-6, lws),
+                     1)
+        time_replays(torch, g, 2)
+        tl = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1] / 20
+        ntk, p0 = 4096, 8192
+        hp = torch.randn(ntk * 2048, generator=gen, device="cuda")
+        yp = torch.empty(ntk * 2048, device="cuda")
+        g = graph_of(torch, lambda _: A.layer_prefill(layer, lk, lv, Ld, p0, ntk, hp, None, yp, 1e-6,
+                                                      lws), 1)
         time_replays(torch, g, 1)
-        t4 = sorted(time_replays(torch, g, args.prefill_steps)[0]
-                    for _ in range(3))[1] / args.prefill_steps
-        flop4 = 4.0 * H * D * (n * pos0 + n * (n + 1) // 2)
-        out["C4_fp8"] = {"workload": "C4 (causal prefill, 8192 tokens after an 8192-token prefix) "
-                                     "over an e4m3-row cache: rows widened to f16, then the f16 "
-                                     "prefill",
-                         "ms_per_call": round(t4, 4),
-                         "tflops": round(flop4 / (t4 * 1e-3) / 1e12, 1)}
-        del c8, ws4, q4, qg4, core4
-    # The projection GEMVs (row f4), f16 activations as the engine; weights rotated over >= 512 MB
-    # of copies so they stream from HBM as a model's layers do.
-    def rotated(nbytes):
-        return max(2, -(-(512 << 20) // nbytes))
-
-    def timed(fn, copies):
-        g = graph_of(torch, fn, copies)
-        time_replays(torch, g, 1)
-        return sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / (3 * copies)
-
-    def line(wbytes, t, copies, **extra):
-        return {**extra, "weight_bytes": wbytes, "us_per_call": round(t * 1e3, 2),
-                "gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
-                "frac": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                "weight_copies_rotated": copies}
-
-    x2048 = torch.randn(2048, generator=gen, device="cuda")
-    x4096 = torch.randn(4096, generator=gen, device="cuda")
-    gemv = {}
-    for name, k, n in (("attn_q", 2048, 8192), ("attn_k", 2048, 512), ("attn_output", 4096, 2048)):
-        wbytes = n * k // 256 * 144
-        copies = rotated(wbytes)
-        wq = synthetic_q4k(torch, gen, copies, n, k)
-        yg = torch.empty(n, device="cuda")
-        xg = x2048 if k == 2048 else x4096
-        t = timed(lambda i: A.q4k_gemv(wq[i % copies], xg, yg, n, k), copies)
-        gemv[name] = line(wbytes, t, copies, k=k, n_rows=n)
-        del wq
-    out["F4_q4k_gemv"] = {"workload": "Q4_K r1 GEMV y = W x with f16 activations at the engine's "
-                                      "Q4_K attention projections (synthetic blocks, HBM-resident "
-                                      "weights)", **gemv}
-    # attn_v is Q6_K (2048 -> 512); the engine's gemv_pair runs it with attn_q in one launch.
-    w6b, w4b = 512 * A.q6k_row_bytes(2048), 8192 * 2048 // 256 * 144
-    copies = rotated(w6b)
-    w6 = synthetic_q6k(torch, gen, copies, 512, 2048)
-    y6 = torch.empty(512, device="cuda")
-    t6 = timed(lambda i: A.q6k_gemv(w6[i % copies], x2048, y6, 512, 2048), copies)
-    del w6
-    copies_p = rotated(w4b + w6b)
-    w4 = synthetic_q4k(torch, gen, copies_p, 8192, 2048)
-    w6 = synthetic_q6k(torch, gen, copies_p, 512, 2048)
-    y4 = torch.empty(8192, device="cuda")
-    tp = timed(lambda i: A.q4k_q6k_gemv_pair(w4[i % copies_p], 8192, y4, w6[i % copies_p], 512, y6,
-                                             x2048), copies_p)
-    wk = synthetic_q4k(torch, gen, copies_p, 512, 2048)
-    yk = torch.empty(512, device="cuda")
-    tq = timed(lambda i: A.qkv_gemv(w4[i % copies_p], 8192, y4, wk[i % copies_p], 512, yk,
-                                    w6[i % copies_p], 512, y6, x2048), copies_p)
-    del w4, w6, wk
-    out["F4_q6k_gemv"] = {"workload": "Q6_K r1 GEMV, f16 activations, attn_v, alone and paired "
-                                      "with attn_q in one launch (synthetic blocks, HBM-resident "
-                                      "weights)",
-                          "attn_v": line(w6b, t6, copies, k=2048, n_rows=512),
-                          "attn_q_plus_attn_v_pair": line(w4b + w6b, tp, copies_p),
-                          "attn_q_k_v_one_launch": line(w4b + w6b + 512 * 2048 // 256 * 144, tq,
-                                                        copies_p)}
-    # Prefill projection GEMMs (row f4, kernels/qgemm.hpp) at a 4096-token chunk (the layer's
-    # retuned prefill chunk): TFLOP/s of 2 n_tok n k over the dequantized product.
-    n_tok = 4096
-    gemm = {}
-    for name, fmt, k, n in (("attn_q", "q4_k", 2048, 8192), ("attn_k", "q4_k", 2048, 512),
-                            ("attn_v", "q6_k", 2048, 512), ("attn_output", "q4_k", 4096, 2048)):
-        xa = torch.randn(n_tok * k, generator=gen, device="cuda")
-        inp = A.GemmInput(n_tok, k)
-        A.gemm_input(xa, k, n_tok, inp)
-        wg = (synthetic_q4k(torch, gen, 1, n, k) if fmt == "q4_k"
-              else synthetic_q6k(torch, gen, 1, n, k))[0]
-        ya = torch.empty(n_tok * n, device="cuda")
-        tg = timed(lambda i: A.gemm(wg, fmt, n, k, inp, ya, n), 4)
-        ta = timed(lambda i: A.gemm_input(xa, k, n_tok, inp), 4)
-        fl = 2.0 * n_tok * n * k
-        gemm[name] = {"format": fmt, "k": k, "n_rows": n, "us_per_call": round(tg * 1e3, 2),
-                      "tflops": round(fl / (tg * 1e-3) / 1e12, 1),
-                      "frac": round(fl / (tg * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                      "gemm_input_us": round(ta * 1e3, 2)}
-        del xa, inp, wg, ya
-    out["F4_qgemm"] = {"workload": f"prefill projection GEMMs over Q4_K / Q6_K r1 weights, "
-                                   f"{n_tok} tokens, f16 activations (gemm_input) and f16 MFMA "
-                                   f"with f32 accumulation; TFLOP/s of 2 n_tok n k",
-                       "tokens": n_tok, **gemm}
-    # Row f3: one attention layer step through the engine wiring (miso_attn_layer_*), synthetic
-    # Q4_K (q, k, o) and Q6_K (v) weights of the engine's shapes.
-    gen.manual_seed(33)
-    layer = A.Layer((synthetic_q4k(torch, gen, 1, 8192, 2048)[0], "q4_k"),
-                    (synthetic_q4k(torch, gen, 1, 512, 2048)[0], "q4_k"),
-                    (synthetic_q6k(torch, gen, 1, 512, 2048)[0], "q6_k"),
-                    (synthetic_q4k(torch, gen, 1, 2048, 4096)[0], "q4_k"),
-                    torch.ones(2048, device="cuda"), torch.ones(D, device="cuda"),
-                    torch.ones(D, device="cuda"),
-                    (1e7 ** (-torch.arange(32, device="cuda") / 32.0)).float())
-    lws = A.LayerWorkspace(4096)
-    Ld = 32768
-    lk = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
-    lv = torch.randn(KV * Ld * D, generator=gen, device="cuda").half()
-    h = torch.randn(2048, generator=gen, device="cuda")
-    dl = torch.randn(2048, generator=gen, device="cuda") * 0.1
-    y = torch.empty(2048, device="cuda")
-    g = graph_of(torch, lambda _: A.layer_decode(layer, lk, lv, Ld, Ld - 1, h, dl, y, 1e-6, lws),
-                 1)
-    time_replays(torch, g, 2)
-    tl = sorted(time_replays(torch, g, 20)[0] for _ in range(3))[1] / 20
-    ntk, p0 = 4096, 8192
-    hp = torch.randn(ntk * 2048, generator=gen, device="cuda")
-    yp = torch.empty(ntk * 2048, device="cuda")
-    g = graph_of(torch, lambda _: A.layer_prefill(layer, lk, lv, Ld, p0, ntk, hp, None, yp, 1e-6,
-                                                  lws), 1)
-    time_replays(torch, g, 1)
-    tp = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / 3
-    curve = None
-    lib = eager_loop()
-    if lib is not None:
-        # The reference's layer decode curve (bench/attention/bench_attention.hip:15-33): 64
-        # eager decode steps between two events at each context, the cache growing by one row
-        # per step, in a cache of 32768 + 256 rows; the median of 3 windows.
-        import ctypes
-        mc = 32768 + 256
-        ck = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
-        cv = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
-        h1 = torch.full((2048,), 0.1, device="cuda")
-        curve = {}
-        for ctx in (16, 1024, 4096, 16384, 32768):
-            w = []
-            for _ in range(3):
-                torch.cuda.synchronize()
-                r = lib.miso_bench_layer_decode(
-                    ctypes.addressof(layer.c), ck.data_ptr(), cv.data_ptr(), ctx, mc,
-                    h1.data_ptr(), y.data_ptr(), 1e-6, lws.decode.data_ptr(), 64,
-                    torch.cuda.current_stream().cuda_stream)
-                if r < 0:
-                    raise RuntimeError(f"layer decode timing loop failed ({r})")
-                w.append(r)
-            curve[str(ctx)] = round(sorted(w)[1] * 1e3, 2)
-        del ck, cv
-        log(f"layer decode curve (us per token, eager): {curve}")
-    out["F3_layer"] = {"workload": "one attention layer step through the engine wiring "
-                                   "(miso_attn_layer_decode / _prefill): residual + RMSNorm, "
-                                   "q/k/v projections, prep, attention, output projection; "
-                                   "synthetic Q4_K / Q6_K weights of the engine's shapes",
-                       "decode_ctx": Ld, "decode_us_per_step": round(tl * 1e3, 2),
-                       "decode_curve_us_per_token": curve,
-                       "decode_curve_method": "the reference's bench/attention/"
-                                              "bench_attention.hip: 64 eager steps per context "
-                                              "between two events, cache growing; median of 3",
-                       "prefill_tokens": ntk, "prefill_pos0": p0,
-                       "prefill_ms_per_chunk": round(tp, 3)}
-    del layer, lws, lk, lv, hp, yp
-    log(f"C1 {out['C1']['us_per_call']} us, C3 {out['C3']['tflops']} TFLOP/s, "
-        f"C5 {out['C5']['gbs']} GB/s, C5 paged {out['C5_paged']['gbs']} GB/s, "
-        f"C2 fp8 {out['C2_fp8']['us_per_step']} us/step, "
-        f"C4 fp8 {out.get('C4_fp8', {}).get('tflops')} TFLOP/s, layer decode "
-        f"{out['F3_layer']['decode_us_per_step']} us, layer prefill chunk "
-        f"{out['F3_layer']['prefill_ms_per_chunk']} ms, q4k gemv "
-        + ", ".join(f"{k_} {v['us_per_call']} us ({v['gbs']} GB/s)"
-                    for k_, v in out['F4_q4k_gemv'].items() if isinstance(v, dict))
-        + f", q6k attn_v {out['F4_q6k_gemv']['attn_v']['us_per_call']} us, q+v pair "
-        f"{out['F4_q6k_gemv']['attn_q_plus_attn_v_pair']['us_per_call']} us, q+k+v "
-        f"{out['F4_q6k_gemv']['attn_q_k_v_one_launch']['us_per_call']} us, qgemm "
-        + ", ".join(f"{k_} {v['tflops']} TFLOP/s" for k_, v in out['F4_qgemm'].items()
-                    if isinstance(v, dict)))
+        tp = sorted(time_replays(torch, g, 3)[0] for _ in range(3))[1] / 3
+        curve = None
+        lib = eager_loop()
+        if lib is not None:
+            # The reference's layer decode curve (bench/attention/bench_attention.hip:15-33): 64
+            # eager decode steps between two events at each context, the cache growing by one row
+            # per step, in a cache of 32768 + 256 rows; the median of 3 windows.
+            import ctypes
+            mc = 32768 + 256
+            ck = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
+            cv = torch.randn(KV * mc * D, generator=gen, device="cuda").half()
+            h1 = torch.full((2048,), 0.1, device="cuda")
+            curve = {}
+            for ctx in (16, 1024, 4096, 16384, 32768):
+                w = []
+                for _ in range(3):
+                    torch.cuda.synchronize()
+                    r = lib.miso_bench_layer_decode(
+                        ctypes.addressof(layer.c), ck.data_ptr(), cv.data_ptr(), ctx, mc,
+                        h1.data_ptr(), y.data_ptr(), 1e-6, lws.decode.data_ptr(), 64,
+                        torch.cuda.current_stream().cuda_stream)
+                    if r < 0:
+                        raise RuntimeError(f"layer decode timing loop failed ({r})")
+                    w.append(r)
+                curve[str(ctx)] = round(sorted(w)[1] * 1e3, 2)
+            del ck, cv
+            log(f"layer decode curve (us per token, eager): {curve}")
+        out["F3_layer"] = {"workload": "one attention layer step through the engine wiring "
+                                       "(miso_attn_layer_decode / _prefill): residual + RMSNorm, "
+                                       "q/k/v projections, prep, attention, output projection; "
+                                       "synthetic Q4_K / Q6_K weights of the engine's shapes",
+                           "decode_ctx": Ld, "decode_us_per_step": round(tl * 1e3, 2),
+                           "decode_curve_us_per_token": curve,
+                           "decode_curve_method": "the reference's bench/attention/"
+                                                  "bench_attention.hip: 64 eager steps per context "
+                                                  "between two events, cache growing; median of 3",
+                           "prefill_tokens": ntk, "prefill_pos0": p0,
+                           "prefill_ms_per_chunk": round(tp, 3)}
+        del layer, lws, lk, lv, hp, yp
+    log("other configurations: " + ", ".join(sorted(out)))
     return out
 
 
@@ -878,7 +884,7 @@ def main():
         t_valu = eager_decode(torch, eager_loop(), 4, q, qg, caches, core, sc, args.ctx,
                               dec["n_splits"], args.warmup, dec["steps"])
         log(f"decode C2 split on VALU (eager): {t_valu * 1e3:.2f} us")
-    if not args.no_other:
+    if not args.no_other and (args.other is None or "C2var" in args.other.split(",")):
         d16 = bench_decode(torch, A, args, inputs, args.max_splits, f16_query=True,
                            label="C2 f16 query")
         other["C2_f16q"] = decode_line(

@@ -5,8 +5,9 @@
 // kernels, with the engine sizing retuned for one MI355X (256 CUs, 288 GB HBM3E):
 //
 //   constant            reference                              here   why (one MI355X)
-//   max decode splits   60   (src/engine/attention.hpp:46)      128   C2 (32768 keys): 21.9 us vs
-//                                                                     27.4 us per decode call
+//   max decode splits   60   (src/engine/attention.hpp:46)      128   C2 (32768 keys): 18.7 us vs
+//                                                                     19.9 us per decode call on
+//                                                                     one box (256 workgroups)
 //   prefill chunk       512  (src/engine/model.hpp:58)          4096  an 8192-token prompt's
 //                                                                     attention: 0.73 ms vs 2.17
 //                                                                     ms (512 workgroups fill the
