@@ -77,7 +77,8 @@ def parse():
     ap.add_argument("--other", default=None,
                     help="comma-separated subset of the other configurations: C2var (the C2 "
                          "variants: f16 query, VALU split, combine curve, fused, cap 60), C1, "
-                         "C3, C5 (with C5_paged), fp8 (C2_fp8, C4_fp8), gemv, qgemm, layer")
+                         "C3, C5 (with C5_paged), fp8 (C2_fp8, C2_long, C4_fp8), gemv, qgemm, "
+                         "layer")
     ap.add_argument("--split-valu", action="store_true",
                     help="with --no-other: still time the VALU form of the C2 split (for "
                          "counter runs of both split forms)")
@@ -565,6 +566,33 @@ def bench_other(torch, A, args):
                          "kv_bytes": int(bytes8), "gbs": round(bytes8 / (t8 * 1e-3) / 1e9, 1),
                          "frac": round(bytes8 / (t8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del caches8
+        # Decode where the stream is long: 262144 keys (the engine's largest cache), the f16 and
+        # the e4m3-row cache side by side, 128 splits, two rotated caches each.
+        Lg = 262144
+        gen.manual_seed(Lg)
+        lk = [torch.randn(KV * Lg * D, generator=gen, device="cuda").half() for _ in range(4)]
+        long16 = [(lk[0], lk[1]), (lk[2], lk[3])]
+        long8 = []
+        for kk, vv in long16:
+            c8 = A.Fp8Cache(Lg)
+            A.attn_kv_encode_fp8(kk, vv, c8, 0, Lg)
+            long8.append(c8)
+        nl = A.attn_n_splits(Lg, args.max_splits)
+        g = graph_of(torch, lambda i: A.attn_decode(q, qg, long16[i % 2][0], long16[i % 2][1],
+                                                    core, sc, Lg, Lg, nl), 2)
+        time_replays(torch, g, 2)
+        tl16 = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1] / 20
+        del g
+        g = graph_of(torch, lambda i: A.attn_decode_fp8(q, qg, long8[i % 2], core, sc, Lg, nl), 2)
+        time_replays(torch, g, 2)
+        tl8 = sorted(time_replays(torch, g, 10)[0] for _ in range(3))[1] / 20
+        del g, lk, long16, long8
+        out["C2_long"] = {"workload": f"decode, 1 sequence x 1 token, ctx {Lg}, over the f16 and "
+                                      "the e4m3-row cache (graph replays)",
+                          "n_splits": nl, "f16_us_per_step": round(tl16 * 1e3, 2),
+                          "f16_gbs": round(2048.0 * Lg / (tl16 * 1e-3) / 1e9, 1),
+                          "fp8_us_per_step": round(tl8 * 1e3, 2),
+                          "fp8_gbs": round(2.0 * KV * Lg * (D + 4) / (tl8 * 1e-3) / 1e9, 1)}
         # C4 over an e4m3-row cache: the 16384 rows widened to f16 into a workspace each call, then
         # the f16 prefill (attn_prefill_fp8).
         if not args.no_prefill:

@@ -1597,22 +1597,25 @@ __device__ __attribute__((always_inline)) inline void wave_pv(WaveTileState& st,
 }
 
 // The wave's state relative to its own true max: joined O (valid in lanes c < 8: head c,
-// dimensions 16 b + 4 g + i), l summed over the column (every lane), mt. A wave without tiles
-// (any = false) gives mt = -inf, l = 0, O = 0.
+// dimensions 16 b + 4 g + i) times o_scale (a power of two: the scale O is kept relative to, 1
+// over f16 rows), l summed over the column (every lane), mt. A wave without tiles (any = false)
+// gives mt = -inf, l = 0, O = 0.
 struct WaveResult {
   float mt, l;
   f32x4 o[16];
 };
 __device__ __attribute__((always_inline)) inline void wave_result(WaveResult& r,
-                                                                 const WaveTileState& st, bool any) {
+                                                                 const WaveTileState& st, bool any,
+                                                                 float o_scale = 1.0f) {
   const float f = any ? __builtin_amdgcn_exp2f(st.m - st.mt) : 0.0f;
+  const float fo = f * o_scale;
   r.mt = st.mt;
   r.l = cdna4::sum_xor32(cdna4::sum_xor16(st.l)) * f;
 #pragma unroll
   for (unsigned b = 0; b < 16; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = st.o[b][i] * f;
+      const float x = st.o[b][i] * fo;
       r.o[b][i] = __builtin_fmaf(cdna4::dpp_mov<cdna4::kRowRor8>(x), kLoWeight, x);
     }
 }

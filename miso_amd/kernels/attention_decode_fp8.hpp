@@ -17,8 +17,9 @@
 //   attn_prep_fp8_kernel<256>       attn_prep (RMSNorm + RoPE) appending the token as e4m3 rows
 //   attn_prep_batch_fp8_kernel<256> the same for a batch of tokens (attn_prep_batch's layout)
 //   attn_kv_fp8_widen_kernel<256>   e4m3 rows -> f16 rows, for the f16 prefill over an e4m3 cache
-//   attn_split_fp8_kernel<256>      split-K partials over e4m3 rows, in the reference's partial
-//                                   layout; attn_combine_kernel merges them unchanged.
+//   attn_split_fp8_kernel<256>      split-K partials over e4m3 rows on the matrix cores, at the
+//                                   f16 split's precision, in the reference's partial layout;
+//                                   attn_combine_kernel merges them unchanged.
 
 #include "attention_decode.hpp"
 
@@ -272,68 +273,110 @@ struct AttnSplitFp8Params {
 
 namespace decode_detail {
 
-// An e4m3 unit is 16 rows: K rows at slot bytes [0, 4096), V rows at [4096, 8192), row r at
-// 256 r -- the f16 unit's 8 KiB slot -- and 64 scales (K rows 0-15, V rows 0-15, then a copy).
-constexpr unsigned kFp8UnitRows = 16;
+// ------------------------------------------------------------------------------------------------
+// The split over e4m3 rows on the matrix cores, per-wave tiles (split_partial_waves' schedule and
+// arithmetic over widened codes). Wave w takes the span's 32-key tiles w, w + 4, ...; a tile's
+// codes (K and V, 8 KiB each) and row scales move by LDS-DMA into one of the wave's two stages,
+// so the wave's next two tiles are in flight while it computes one. The codes widen to f16 in
+// registers (every e4m3 value is an f16 value): K as the A operands of the score MFMAs against
+// the (hi, lo) query pairs, each score then multiplied by its K row scale in f32; V read
+// transposed (ds_read_b64_tr_b8) as the V^T operands. The numerators carry each row's V scale
+// relative to a reference V scale R, the largest the wave has met in the item: O is kept
+// relative to R (rescaled, exactly, when a tile brings a larger one) and multiplied by it at the
+// end. So the arithmetic is the f16 path's (f32-precision query and numerators, f32 accumulation)
+// on the rows the codes and scales define, and a common power-of-two factor on every V scale
+// scales O exactly.
+// ------------------------------------------------------------------------------------------------
 
-constexpr int kFp8Ring = 2;  // units per wave's LDS ring: kFp8Ring - 1 in flight under one
-
-template <int R>
-struct SplitFp8SharedT {
-  static constexpr int kWaveCount = kWaves, kRingUnits = R;
-  SplitSharedT<kWaves, R> base;
-  float scale[kWaves][R][64];
+// Wave w's stages: K codes at [0, 8192), V codes at [8192, 16384), row r at 256 r with 16-byte
+// chunk c at position c ^ fp8_swz(r); the tile's K then V row scales.
+struct alignas(1024) Fp8WaveShared {
+  unsigned char codes[kWaves][2][16384];
+  float scale[kWaves][2][64];
+  float q[kGroup][attn::kDim];
 };
-using SplitFp8Shared = SplitFp8SharedT<kFp8Ring>;
 
-// Global -> LDS copy of one e4m3 unit: 4 row quads of K and of V (1 KiB each: row u0 + 4 i +
-// lane / 16, bytes 16 (lane % 16)), then one 4-byte load per lane of the scales. `kw` / `vw` are
-// the lane's addresses in quad 0, `sw` its scale address. 9 vector-memory instructions.
-__device__ __attribute__((always_inline)) inline void issue_unit_fp8(const uint8_t* kw,
-                                                                     const uint8_t* vw,
-                                                                     const float* sw,
-                                                                     unsigned slot_lds,
-                                                                     unsigned scale_lds) {
+// Chunk swizzle of tile row r: r % 16, with bit 3 flipped for rows 16-31. The A-operand K reads
+// take one chunk of rows 16 kb + 0..15 (16 positions), the transposed V reads rows 4 g + j and
+// 16 + 4 g + j together (8 positions apart).
+__device__ __attribute__((always_inline)) inline unsigned fp8_swz(unsigned r) {
+  return (r & 15u) ^ ((r >> 4 & 1u) << 3);
+}
+
+// Copy offsets of the two 16-row groups of a tile's codes: instruction i moves rows
+// 16 grp + 4 i + lane / 16, chunk position lane % 16 (the lane's offset from the group's first row
+// minus 1024 i, which the instruction offset adds).
+__device__ __attribute__((always_inline)) inline void fp8_copy_offsets(unsigned (&off)[2][4],
+                                                                      unsigned lane) {
+#pragma unroll
+  for (unsigned grp = 0; grp < 2; ++grp)
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i) {
+      const unsigned r = 16 * grp + 4 * i + (lane >> 4), pos = lane & 15u;
+      off[grp][i] = (lane >> 4) * 256 + 16 * (pos ^ fp8_swz(r));
+    }
+}
+
+// 8 copies of 1 KiB: rows 0-15 of the codes at xt to lds, rows 16-31 from xt + 4096 to lds + 4096.
+// M0 is saved and restored.
+__device__ __attribute__((always_inline)) inline void issue_codes32(const void* xt, const void* xt2,
+                                                                   const unsigned (&off)[2][4],
+                                                                   unsigned lds) {
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %4\n\t"
+      "s_mov_b32 m0, %11\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off nt\n\t"
-      "global_load_lds_dwordx4 %1, off offset:1024 nt\n\t"
-      "global_load_lds_dwordx4 %1, off offset:2048 nt\n\t"
-      "global_load_lds_dwordx4 %1, off offset:3072 nt\n\t"
-      "s_mov_b32 m0, %5\n\t"
+      "global_load_lds_dwordx4 %1, %9 nt\n\t"
+      "global_load_lds_dwordx4 %2, %9 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %3, %9 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %4, %9 offset:3072 nt\n\t"
+      "s_mov_b32 m0, %12\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off nt\n\t"
-      "global_load_lds_dwordx4 %2, off offset:1024 nt\n\t"
-      "global_load_lds_dwordx4 %2, off offset:2048 nt\n\t"
-      "global_load_lds_dwordx4 %2, off offset:3072 nt\n\t"
-      "s_mov_b32 m0, %6\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dword %3, off nt\n\t"
+      "global_load_lds_dwordx4 %5, %10 nt\n\t"
+      "global_load_lds_dwordx4 %6, %10 offset:1024 nt\n\t"
+      "global_load_lds_dwordx4 %7, %10 offset:2048 nt\n\t"
+      "global_load_lds_dwordx4 %8, %10 offset:3072 nt\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(kw), "v"(vw), "v"(sw), "s"(slot_lds), "s"(slot_lds + 4096u), "s"(scale_lds)
+      : "v"(off[0][0]), "v"(off[0][1]), "v"(off[0][2]), "v"(off[0][3]), "v"(off[1][0]),
+        "v"(off[1][1]), "v"(off[1][2]), "v"(off[1][3]), "s"(xt), "s"(xt2), "s"(lds),
+        "s"(lds + 4096u)
       : "memory");
 }
 
-// The same copy for the unit that crosses the end of the cache: rows past last_row are clamped
-// to it (they are masked at use). K8 / V8 / KS / VS are the KV head's bases. Also 9 instructions.
-__device__ __attribute__((always_inline)) inline void issue_unit_fp8_clamped(
-    const uint8_t* K8, const uint8_t* V8, const float* KS, const float* VS, unsigned u0,
-    unsigned last_row, unsigned slot_lds, unsigned scale_lds, unsigned lane) {
+// This wave's copy of the codes of the tile at key k0 (X: the KV head's K or V codes) into lds:
+// 8 vector-memory instructions; rows past last_row read last_row (masked at use).
+__device__ __attribute__((always_inline)) inline void issue_fp8_codes(const uint8_t* X,
+                                                                     unsigned k0,
+                                                                     unsigned last_row,
+                                                                     unsigned lds,
+                                                                     const unsigned (&off)[2][4],
+                                                                     unsigned lane) {
+  if (k0 + 31 <= last_row) {
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(
+        uniform(reinterpret_cast<const attn::half_t*>(X + std::size_t{k0} * attn::kDim)));
+    issue_codes32(base, base + 4096, off, lds);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    unsigned row = u0 + 4 * i + (lane >> 4);
-    row = row < last_row ? row : last_row;
-    const std::size_t at = std::size_t{row} * attn::kDim + (lane & 15u) * 16;
-    cdna4::lds_load16_nt(K8 + at, slot_lds + 1024 * i);
-    cdna4::lds_load16_nt(V8 + at, slot_lds + 4096 + 1024 * i);
+    for (unsigned i = 0; i < 8; ++i) {
+      const unsigned r = 4 * i + (lane >> 4), pos = lane & 15u;
+      const unsigned row = k0 + r <= last_row ? k0 + r : last_row;
+      cdna4::lds_load16_nt(X + std::size_t{row} * attn::kDim + 16 * (pos ^ fp8_swz(r)),
+                           lds + 1024 * i);
+    }
   }
-  unsigned row = u0 + (lane & 15u);
-  row = row < last_row ? row : last_row;
-  const float* sw = ((lane & 16u) ? VS : KS) + row;
+}
+
+// The tile's 32 K then 32 V row scales (rows past last_row read last_row): 1 instruction.
+__device__ __attribute__((always_inline)) inline void issue_fp8_scales(const float* KS,
+                                                                      const float* VS,
+                                                                      unsigned k0,
+                                                                      unsigned last_row,
+                                                                      unsigned lds,
+                                                                      unsigned lane) {
+  const unsigned r = k0 + (lane & 31u);
+  const float* sw = ((lane & 32u) ? VS : KS) + (r <= last_row ? r : last_row);
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -342,242 +385,189 @@ __device__ __attribute__((always_inline)) inline void issue_unit_fp8_clamped(
       "global_load_lds_dword %1, off nt\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(sw), "s"(scale_lds)
+      : "v"(sw), "s"(lds)
       : "memory");
 }
 
-// Wait until the unit whose copy was followed by `after` (< 4) more units' copies has landed.
-__device__ __attribute__((always_inline)) inline void wait_fp8_units_after(unsigned after) {
-  switch (after) {
-    case 0: cdna4::wait_vmcnt<0>(); break;
-    case 1: cdna4::wait_vmcnt<9>(); break;
-    case 2: cdna4::wait_vmcnt<18>(); break;
-    default: cdna4::wait_vmcnt<27>(); break;
-  }
+typedef unsigned fp8_u32x2 __attribute__((ext_vector_type(2)));
+typedef int fp8_i32x2 __attribute__((ext_vector_type(2)));
+
+// Eight codes (bytes 0-7 of w) as an f16 x 8 operand, in byte order.
+__device__ __attribute__((always_inline)) inline cdna4::half8_t widen8(unsigned w0, unsigned w1) {
+  return __builtin_bit_cast(cdna4::half8_t,
+                            cdna4::u32x4_t{fp8kv::pair_lo(w0), fp8kv::pair_hi(w0),
+                                           fp8kv::pair_lo(w1), fp8kv::pair_hi(w1)});
 }
 
-// One 8-row half of an e4m3 unit: the lane layout of process_unit, with the K chunk of a row
-// being dimensions 16 dc .. 16 dc + 15 (16 bytes) and the V chunk dimensions 8 c .. 8 c + 7 of
-// rows 2 i + a (8 bytes). Codes widen to f16 exactly; the row scales enter through
-// unit_numerators: scores x K scale (f32), numerators x the row's V scale relative to the unit's
-// largest (vratio <= 1, so the f16 numerator never exceeds the unscaled one). The half's P V
-// accumulates into the unit's f32 sums t (kFirst: the unit's first half starts them).
-template <bool kFirst>
-__device__ __attribute__((always_inline)) inline void process_half_fp8(
-    WaveState& st, const uint4 (&kr)[4], const uint2 (&vr)[4], float ksc, float vratio,
-    const half2_t (&qh)[4][8], unsigned r0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
-    float (&t)[kGroup][8], unsigned lane) {
-  float part[16];
+// The raw operand codes of one stage. K: lane (g, c), key block kb, k-step s reads the 8 codes of
+// dimensions 8 (4 s + g) .. + 7 of row 16 kb + c (chunk (2 s + g / 2) ^ c ^ 8 kb, half g % 2), at
+// kaddr[kb] ^ 32 s, kaddr[kb] = K base + 4096 kb + 256 c + 32 (c / 2 ^ 4 kb) + 16 ((g / 2 ^ c) %
+// 2) + 8 (g % 2). V^T: ds_read_b64_tr_b8 gives lane 16 G + 8 h + j byte j of the 8 bytes lanes
+// 16 G + 2 k + h (k = 0 .. 7) supply, so lane 16 g + 2 k + h supplies dimensions 16 b + 8 h .. + 7
+// of key 4 g + k (k < 4) or 16 + 4 g + k - 4, and lane (g, c) receives dimension 16 b + c of the
+// keys of its k-slots 8 g .. 8 g + 7, in order: vaddr ^ 16 b, vaddr = V base + 256 key + 8 h + 16
+// fp8_swz(key).
+struct Fp8Raw {
+  fp8_u32x2 k[2][8];
+  fp8_i32x2 v[16];
+};
+__device__ __attribute__((always_inline)) inline void read_fp8_stage(Fp8Raw& raw,
+                                                                    unsigned kaddr0,
+                                                                    unsigned kaddr1,
+                                                                    unsigned vaddr) {
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const unsigned w[4] = {kr[rr].x, kr[rr].y, kr[rr].z, kr[rr].w};
-    unsigned kh[8];
+  for (unsigned s = 0; s < 8; ++s)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kh[2 * i] = fp8kv::pair_lo(w[i]);
-      kh[2 * i + 1] = fp8kv::pair_hi(w[i]);
-    }
+    for (unsigned kb = 0; kb < 2; ++kb)
+      raw.k[kb][s] = *reinterpret_cast<const __attribute__((address_space(3))) fp8_u32x2*>(
+          (kb == 0 ? kaddr0 : kaddr1) ^ (32u * s));
 #pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      float acc = dot2_first(qh[hh][0], kh[0]);
-#pragma unroll
-      for (int j = 1; j < 8; ++j)
-        acc = __builtin_amdgcn_fdot2(qh[hh][j], cdna4::as_half2(kh[j]), acc, false);
-      part[4 * hh + rr] = acc;
-    }
-  }
-  const float m_before = st.m;
-  unit_numerators<true>(st, part, r0, span_end, ksc, vratio, pbuf, lane);
-  if constexpr (!kFirst) {
-    // The first half's sums in t were taken against the previous reference max: when this
-    // half moved it, t takes the same per-head correction as o (unit_softmax_state's).
-    if (__builtin_amdgcn_ballot_w64(st.m != m_before)) {  // wave-uniform branch
-      const float corr = __builtin_amdgcn_exp2f(m_before - st.m);
-#pragma unroll
-      for (int h = 0; h < kGroup; ++h) {
-        const float ch =
-            cdna4::as_float(__builtin_amdgcn_readlane(cdna4::as_uint(corr), head_lane(h)));
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          t[h][e] *= ch;
-      }
-    }
-  }
-  // P V over this lane's rows 2 i + a, dimensions 8 c .. 8 c + 7: the byte permutes interleave
-  // rows 2 g + a and 2 g + 4 + a so that one conversion yields their f16 pair for a dimension.
-  const unsigned a = lane >> 5;
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const uint4 p0 = *reinterpret_cast<const uint4*>(&pbuf[a][g][0]);
-    const uint4 p1 = *reinterpret_cast<const uint4*>(&pbuf[a][g][4]);
-    const unsigned pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-    const unsigned r0w[2] = {vr[g].x, vr[g].y}, r1w[2] = {vr[g + 2].x, vr[g + 2].y};
-    unsigned pv[8];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const unsigned lo = __builtin_amdgcn_perm(r1w[j], r0w[j], 0x05010400u);
-      const unsigned hi = __builtin_amdgcn_perm(r1w[j], r0w[j], 0x07030602u);
-      pv[4 * j + 0] = fp8kv::pair_lo(lo);
-      pv[4 * j + 1] = fp8kv::pair_hi(lo);
-      pv[4 * j + 2] = fp8kv::pair_lo(hi);
-      pv[4 * j + 3] = fp8kv::pair_hi(hi);
-    }
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (kFirst && g == 0)
-          t[h][e] = dot2_first(cdna4::as_half2(pp[h]), pv[e]);
-        else
-          t[h][e] = __builtin_amdgcn_fdot2(cdna4::as_half2(pp[h]), cdna4::as_half2(pv[e]),
-                                           t[h][e], false);
-      }
-  }
+  for (unsigned b = 0; b < 16; ++b)
+    raw.v[b] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        reinterpret_cast<__attribute__((address_space(3))) fp8_i32x2*>(vaddr ^ (16u * b)));
 }
 
-// One 16-row e4m3 unit: every LDS read of both halves first, then the halves in order. The
-// unit's V reference is its largest V row scale among the rows of the span (wave-uniform): the
-// numerators carry each row's scale relative to it, the unit's P V sums stay in f32 and enter o
-// times the reference. A common power-of-two factor on every V scale therefore leaves the f16
-// numerators unchanged (no f16 overflow at the largest scales, no underflow at the smallest);
-// only the spread of V scales within 16 consecutive rows scales them down.
-__device__ __attribute__((always_inline)) inline void process_unit_fp8(
-    WaveState& st, const unsigned char* slot, const float* scl, const unsigned (&koff)[4],
-    const half2_t (&qh)[4][8], unsigned u0, unsigned span_end, uint32_t (*pbuf)[2][kGroup],
-    unsigned lane) {
-  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, a = lane >> 5, c = lane & 31u;
-  const unsigned srow = 4 * rq + (dc & 3u);  // the lane's score row within a half
-  uint4 kr[2][4];
-  uint2 vr[2][4];
-  float ksc[2], vsc[2];
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      kr[hf][rr] = *reinterpret_cast<const uint4*>(slot + 2048 * hf + koff[rr]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vr[hf][i] = *reinterpret_cast<const uint2*>(slot + 4096 + 2048 * hf + 512 * i + 256 * a +
-                                                  8 * c);
-    ksc[hf] = scl[8 * hf + srow];
-    vsc[hf] = scl[16 + 8 * hf + srow];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // Rows past the span are masked (p = 0) and stay out of the reference; row u0 is in the span.
-  const float v0 = u0 + srow < span_end ? vsc[0] : 0.0f;
-  const float v1 = u0 + 8 + srow < span_end ? vsc[1] : 0.0f;
-  const float uref = cdna4::wave_allmax(fmaxf(v0, v1));
-  const float inv = uref > 0.0f ? 1.0f / uref : 0.0f;
-  float t[kGroup][8];
-  process_half_fp8<true>(st, kr[0], vr[0], ksc[0], vsc[0] * inv, qh, u0, span_end, pbuf, t,
-                         lane);
-  process_half_fp8<false>(st, kr[1], vr[1], ksc[1], vsc[1] * inv, qh, u0 + 8, span_end, pbuf, t,
-                          lane);
-#pragma unroll
-  for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      st.o[h][e] = __builtin_fmaf(t[h][e], uref, st.o[h][e]);
-}
-
-// Partial (m, l, o) of keys [span.begin, span.end) for KV head kvh over e4m3 rows (K8 / V8 /
-// KS / VS: the KV head's bases), written at `base` in the reference's partial layout. The same
-// schedule as split_partial_rows with 16-row units: wave w streams units starting at rows
-// span.begin + 16 w, + 64, ... through its kRingUnits-unit LDS ring; rows past the span are
-// masked and rows past len - 1 are never read.
-template <class Shared>
-__device__ __attribute__((always_inline)) inline void split_partial_fp8(
+// Partial (m, l, o) of keys [span.begin, span.end) of KV head kvh over e4m3 rows (K8 / V8 / KS /
+// VS: the KV head's bases) at `base`, in the reference's partial layout (m: natural-log max of
+// the scaled scores). `more`: the workgroup runs another item afterwards.
+__device__ __attribute__((always_inline)) inline void split_partial_fp8_waves(
     const float* __restrict__ q, const uint8_t* K8, const uint8_t* V8, const float* KS,
-    const float* VS, unsigned len, AttnSpan span, unsigned kvh, float* part_m, float* part_l,
-    float* part_o, std::size_t base, Shared& sh, bool more) {
-  constexpr int kW = Shared::kWaveCount, kR = Shared::kRingUnits;
-  static_assert(kR >= 2 && kR <= 4 && kW == kWaves, "ring depth / wave count");
-  const unsigned t = threadIdx.x, lane = t & 63u;
+    const float* VS, AttnSpan span, unsigned kvh, float* part_m, float* part_l, float* part_o,
+    std::size_t base, Fp8WaveShared& sh, bool more) {
+  using cdna4::half8_t;
+  const unsigned t = threadIdx.x, lane = t & 63u, g = lane >> 4, c = lane & 15u;
   const unsigned wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const unsigned last_row = len - 1;
-  constexpr unsigned kStride = kW * kFp8UnitRows;
-  const unsigned first = span.begin + wave * kFp8UnitRows;
-  const unsigned n_units = first < span.end ? (span.end - first + kStride - 1) / kStride : 0;
-  const unsigned ring0 = cdna4::lds_offset(sh.base.ring[wave][0]);
-  const unsigned scale0 = cdna4::lds_offset(sh.scale[wave][0]);
-  // This lane's bytes of row quad 0 of unit 0 and its scale (K rows for lanes 0-15 of each
-  // half-wave, V rows for 16-31); unit k is kStride rows further.
-  const std::size_t lane_at = std::size_t{first + (lane >> 4)} * attn::kDim + (lane & 15u) * 16;
-  const float* lane_scale = ((lane & 16u) ? VS : KS) + first + (lane & 15u);
-  auto issue = [&](unsigned k) {
-    const unsigned u0 = first + k * kStride;
-    const unsigned slot = ring0 + (k % kR) * kUnitBytes;
-    const unsigned sslot = scale0 + (k % kR) * 256;
-    if (u0 + kFp8UnitRows <= len) {  // wave-uniform
-      const std::size_t step = std::size_t{k} * kStride * attn::kDim;
-      issue_unit_fp8(K8 + lane_at + step, V8 + lane_at + step, lane_scale + k * kStride, slot,
-                     sslot);
-    } else {
-      issue_unit_fp8_clamped(K8, V8, KS, VS, u0, last_row, slot, sslot, lane);
-    }
+  const unsigned n_tiles = (span.end - span.begin + kTileKeys - 1) / kTileKeys;
+  const unsigned last_row = span.end - 1;  // unused when n_tiles == 0
+  const unsigned nw = n_tiles > wave ? (n_tiles - wave + 3) / 4 : 0;
+  unsigned off[2][4];
+  fp8_copy_offsets(off, lane);
+  // Tile j of the wave (ti = w + 4 j) into stage j % 2: K codes, scales, V codes (17
+  // instructions).
+  auto issue = [&](unsigned j) __attribute__((always_inline)) {
+    const unsigned k0 = span.begin + (wave + 4 * j) * kTileKeys, st_ = j & 1u;
+    const unsigned lds = cdna4::lds_offset(sh.codes[wave][st_]);
+    issue_fp8_codes(K8, k0, last_row, lds, off, lane);
+    issue_fp8_scales(KS, VS, k0, last_row, cdna4::lds_offset(sh.scale[wave][st_]), lane);
+    issue_fp8_codes(V8, k0, last_row, lds + 8192u, off, lane);
   };
 
-  // This wave's query heads of the KV head (1 KiB each), then the first kR - 1 units.
-  constexpr int kHeadsPerWave = kGroup / kW;
 #pragma unroll
-  for (int i = 0; i < kHeadsPerWave; ++i) {
-    const unsigned h = kHeadsPerWave * wave + i;
+  for (unsigned i = 0; i < 2; ++i) {
+    const unsigned h = 2 * wave + i;
     cdna4::lds_load16(q + (std::size_t{kvh} * kGroup + h) * attn::kDim + 4 * lane,
-                      cdna4::lds_offset(sh.base.q[h]));
+                      cdna4::lds_offset(sh.q[h]));
   }
-#pragma unroll
-  for (unsigned k = 0; k + 1 < kR; ++k)
-    if (k < n_units)
-      issue(k);
-  wait_fp8_units_after(n_units < kR - 1 ? n_units : kR - 1);  // the query loads are older
-  __syncthreads();
+  if (nw > 0)
+    issue(0);
+  if (nw > 1)
+    issue(1);
+  // The queries landed (the tiles' copies may be in flight).
+  if (nw > 1)
+    cdna4::wait_vmcnt<34>();
+  else if (nw > 0)
+    cdna4::wait_vmcnt<17>();
+  else
+    cdna4::wait_vmcnt<0>();
+  tile_barrier();
+  const TileLane tln = tile_lane(lane);
+  WaveTileState st;
+  wave_start(st, sh.q, lane, tln);
+  const unsigned kl = 256 * c + 16 * (((g >> 1) ^ c) & 1u) + 8 * (g & 1u);
+  const unsigned kl0 = kl + 32 * (c >> 1), kl1 = 4096 + kl + 32 * ((c >> 1) ^ 4u);
+  unsigned vl;
+  {
+    const unsigned m = lane & 15u, k = m >> 1, h = m & 1u;
+    const unsigned key = k < 4 ? 4 * g + k : 16 + 4 * g + (k - 4);
+    vl = 8192 + 256 * key + 8 * h + 16 * fp8_swz(key);
+  }
+  float vref = 0.0f;  // R: the largest V row scale of the item's tiles so far (O is relative to it)
 
-  // Query slices as f16 pairs pre-scaled by log2(e)/16: slot hh = head 4 hq + (hh ^ dc / 4),
-  // pair j = dimensions 16 dc + 2 j, 16 dc + 2 j + 1.
-  const unsigned dc = lane & 15u, rq = (lane >> 4) & 1u, hq = lane >> 5;
-  half2_t qh[4][8];
-  constexpr float kScale = kLog2e / 16.0f;  // 1/sqrt(256) in log2 units
+  // Tile j: in flight after its copies, those of tile j + 1 (17, if it exists). Every operand of
+  // the tile is read into registers first; then tile j + 2 goes into its stage.
+  for (unsigned j = 0; j < nw; ++j) {
+    const unsigned ti = wave + 4 * j, st_ = j & 1u;
+    if (j + 1 < nw)
+      cdna4::wait_vmcnt<17>();
+    else
+      cdna4::wait_vmcnt<0>();
+    const unsigned lds = cdna4::lds_offset(sh.codes[wave][st_]);
+    Fp8Raw raw;
+    read_fp8_stage(raw, lds + kl0, lds + kl1, lds + vl);
+    const float* scl = sh.scale[wave][st_];
+    const float4 ka4 = *reinterpret_cast<const float4*>(scl + 4 * g);
+    const float4 kb4 = *reinterpret_cast<const float4*>(scl + 16 + 4 * g);
+    const float4 va4 = *reinterpret_cast<const float4*>(scl + 32 + 4 * g);
+    const float4 vb4 = *reinterpret_cast<const float4*>(scl + 48 + 4 * g);
+    __builtin_amdgcn_sched_barrier(0);  // every read of the stage in flight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (j + 2 < nw)
+      issue(j + 2);
+    // The lane's keys 4 g + i and 16 + 4 g + i (i < 4), in the order of its score values.
+    const float ksc[8] = {ka4.x, ka4.y, ka4.z, ka4.w, kb4.x, kb4.y, kb4.z, kb4.w};
+    const float vsc[8] = {va4.x, va4.y, va4.z, va4.w, vb4.x, vb4.y, vb4.z, vb4.w};
+    half8_t ka[2][8];
 #pragma unroll
-  for (int hh = 0; hh < 4; ++hh) {
-    const unsigned h = 4 * hq + (hh ^ (dc >> 2));
+    for (unsigned s = 0; s < 8; ++s)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 x = *reinterpret_cast<const float4*>(&sh.base.q[h][16 * dc + 4 * i]);
-      qh[hh][2 * i] = half2_t{static_cast<_Float16>(x.x * kScale),
-                              static_cast<_Float16>(x.y * kScale)};
-      qh[hh][2 * i + 1] = half2_t{static_cast<_Float16>(x.z * kScale),
-                                  static_cast<_Float16>(x.w * kScale)};
+      for (unsigned kb = 0; kb < 2; ++kb)
+        ka[kb][s] = widen8(raw.k[kb][s].x, raw.k[kb][s].y);
+    f32x4 s[2];
+    wave_scores(s, ka, st);
+    half8_t va[16];
+#pragma unroll
+    for (unsigned b = 0; b < 16; ++b)
+      va[b] = widen8(static_cast<unsigned>(raw.v[b].x), static_cast<unsigned>(raw.v[b].y));
+    // The tile's largest V row scale (rows past the span read the last row's): R moves up to it,
+    // O by the exact power-of-two ratio (0 on the first tile, whose O is 0).
+    const float vmax = cdna4::wave_allmax(
+        fmaxf(fmaxf(fmaxf(vsc[0], vsc[1]), fmaxf(vsc[2], vsc[3])),
+              fmaxf(fmaxf(vsc[4], vsc[5]), fmaxf(vsc[6], vsc[7]))));
+    if (vmax > vref) {  // wave-uniform
+      tile_scale_o(st.o, vref / vmax);
+      vref = vmax;
     }
-  }
-  // K read offsets in a half: row 4 rq + (rr ^ dc % 4), 16-byte chunk dc.
-  unsigned koff[4];
+    const float inv = 1.0f / vref;  // a power of two: exact
+    float vr[8];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr)
-    koff[rr] = (4 * rq + (rr ^ (dc & 3u))) * 256 + 16 * dc;
+    for (int i = 0; i < 8; ++i)
+      vr[i] = vsc[i] * inv;
+    const unsigned k0 = span.begin + ti * kTileKeys;
+    TileSoftmax sm;
+    if (k0 + kTileKeys > span.end)  // uniform
+      tile_scores_joined<true, true>(sm, s, st.m, k0, span.end, lane, tln, ksc);
+    else
+      tile_scores_joined<false, true>(sm, s, st.m, k0, span.end, lane, tln, ksc);
+    const bool first = j == 0;
+    if (tile_decide<true>(sm, st, first, tln, vr))
+      tile_rescale<true>(sm, st, first, tln, vr);
+    st.l += sm.lt;
+#pragma unroll
+    for (int b2 = 0; b2 < 16; ++b2)
+      st.o[b2] = mfma16(va[b2], sm.pb, st.o[b2]);
+  }
 
-  WaveState st;
-  st.m = -__builtin_inff();
-  st.mt = -__builtin_inff();
-  st.l = 0.0f;
-#pragma unroll
-  for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      st.o[h][e] = 0.0f;
-
-  unsigned k = 0;
-  for (; k + kR - 1 < n_units; ++k) {
-    issue(k + kR - 1);
-    cdna4::wait_vmcnt<9 * (kR - 1)>();
-    process_unit_fp8(st, sh.base.ring[wave][k % kR], sh.scale[wave][k % kR], koff, qh,
-                     first + k * kStride, span.end, sh.base.p[wave], lane);
+  // The merge through stage 0 of each wave: wave w's result in its own (O in the first 8 KiB, mt
+  // and l after it), which only it has used and which no copy still targets.
+  {
+    WaveResult r;
+    wave_result(r, st, nw > 0, vref);
+    float* mine = reinterpret_cast<float*>(sh.codes[wave][0]);
+    wave_merge_store(mine, mine + 8 * attn::kDim, r, lane, 0, 16);
   }
-  for (; k < n_units; ++k) {
-    wait_fp8_units_after(n_units - 1 - k);
-    process_unit_fp8(st, sh.base.ring[wave][k % kR], sh.scale[wave][k % kR], koff, qh,
-                     first + k * kStride, span.end, sh.base.p[wave], lane);
+  tile_barrier();
+  {
+    constexpr unsigned kStride = 2 * 16384 / 4;  // floats from one wave's stage 0 to the next
+    const float* area = reinterpret_cast<const float*>(sh.codes[0][0]);
+    const unsigned h = t % 8, d = t / 8;
+    const WaveMergeScale ms = wave_merge_load_scale(area + 8 * attn::kDim, kStride, h);
+    wave_merge_out(area, kStride, ms, d, d, h, part_o, base);
+    wave_merge_out(area, kStride, ms, d + 32, d + 32, h, part_o, base);
+    if (d == 0)
+      wave_merge_ml_out(ms, h, part_m, part_l, base);
   }
-  write_partial(st, sh.base, part_m, part_l, part_o, base, more);
+  if (more)
+    tile_barrier();  // LDS is reused by the next item
 }
 
 }  // namespace decode_detail
@@ -588,17 +578,16 @@ __device__ __attribute__((always_inline)) inline void split_partial_fp8(
 template <int kBlock>
 __global__ void __launch_bounds__(kBlock) attn_split_fp8_kernel(AttnSplitFp8Params p) {
   static_assert(kBlock == 256, "four waves per split workgroup");
-  __shared__ decode_detail::SplitFp8Shared sh;
+  __shared__ decode_detail::Fp8WaveShared sh;
   const unsigned count = attn::kKvHeads * p.n_splits;
   for (unsigned item = blockIdx.y * gridDim.x + blockIdx.x; item < count;
        item += gridDim.x * gridDim.y) {
     const unsigned kvh = item / p.n_splits, split = item % p.n_splits;
     const std::size_t rows = std::size_t{kvh} * p.max_ctx;
-    decode_detail::split_partial_fp8(
+    decode_detail::split_partial_fp8_waves(
         p.q, p.k8 + rows * attn::kDim, p.v8 + rows * attn::kDim, p.k_scale + rows,
-        p.v_scale + rows, p.len, attn_split_span(p.len, p.n_splits, split), kvh, p.part_m,
-        p.part_l, p.part_o, std::size_t{kvh} * p.n_splits + split, sh,
-        item + gridDim.x * gridDim.y < count);
+        p.v_scale + rows, attn_split_span(p.len, p.n_splits, split), kvh, p.part_m, p.part_l,
+        p.part_o, std::size_t{kvh} * p.n_splits + split, sh, item + gridDim.x * gridDim.y < count);
   }
 }
 
