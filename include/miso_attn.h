@@ -191,6 +191,11 @@ int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cach
  * max_len == 0. */
 uint32_t miso_attn_ragged_splits(uint32_t max_len);
 uint64_t miso_attn_ragged_partials(uint32_t batch, uint32_t max_len);
+/* Keys per span the ragged and paged decode use for this batch on the current device (no
+ * reference counterpart): 1024 when 2 x batch x ceil(max_len / 1024) reaches four spans per CU,
+ * else 512 (the scratch above is sized for 512, so it serves either). The same for both
+ * layouts, so their outputs stay bit-identical. */
+uint32_t miso_attn_ragged_chunk(uint32_t batch, uint32_t max_len);
 int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k_cache,
                             const uint16_t* v_cache, const uint64_t* kv_offsets,
                             const uint32_t* lens, uint32_t batch, uint32_t max_len, float* core,

@@ -36,6 +36,7 @@ SIGNATURES = {
                                      c_uint64, P]),
     "miso_attn_ragged_splits": (c_uint32, [c_uint32]),
     "miso_attn_ragged_partials": (c_uint64, [c_uint32, c_uint32]),
+    "miso_attn_ragged_chunk": (c_uint32, [c_uint32, c_uint32]),
     "miso_attn_decode_ragged": (c_int, [P, P, P, P, P, P, c_uint32, c_uint32, P, P, P, P, P]),
     "miso_attn_decode_paged": (c_int, [P, P, P, P, P, c_uint32, c_uint32, P, c_uint32, c_uint32,
                                        P, P, P, P, P]),

@@ -224,6 +224,11 @@ def ragged_partials(batch: int, max_len: int) -> int:
     return int(_lib.load().miso_attn_ragged_partials(batch, max_len))
 
 
+def ragged_chunk(batch: int, max_len: int) -> int:
+    """Keys per span the ragged / paged decode of such a batch uses on the current device."""
+    return int(_lib.load().miso_attn_ragged_chunk(batch, max_len))
+
+
 class RaggedScratch:
     def __init__(self, batch: int, max_len: int, device="cuda"):
         n = ragged_partials(batch, max_len)

@@ -405,6 +405,10 @@ int miso_attn_prefill_ws(const float* q, const float* qg, const uint16_t* k_cach
 
 uint32_t miso_attn_ragged_splits(uint32_t max_len) { return k::attn_ragged_splits(max_len); }
 
+uint32_t miso_attn_ragged_chunk(uint32_t batch, uint32_t max_len) {
+  return k::attn_ragged_chunk(batch, max_len, device_cus());
+}
+
 uint64_t miso_attn_ragged_partials(uint32_t batch, uint32_t max_len) {
   return uint64_t{batch} * k::attn::kKvHeads * k::attn_ragged_splits(max_len) *
          (k::attn::kQHeads / k::attn::kKvHeads);
@@ -423,15 +427,15 @@ int miso_attn_decode_ragged(const float* q, const float* gate, const uint16_t* k
   if (max_len == 0)
     return fail("miso_attn_decode_ragged", "max_len must be >= 1");
   const unsigned s_max = k::attn_ragged_splits(max_len);
+  const unsigned cus = device_cus();
   const k::AttnRaggedParams p{q,     gate,  as_half(k_cache), as_half(v_cache), kv_offsets,
                               lens,  core,  part_m,           part_l,           part_o,
-                              batch, s_max, 0xFFFFFFFFu};
+                              batch, s_max, 0xFFFFFFFFu, k::attn_ragged_chunk(batch, max_len, cus)};
   const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
   if (items > 0x7FFFFFFFull)
     return fail("miso_attn_decode_ragged", "batch x splits too large for one grid");
   // One streaming workgroup per CU where the batch fits its item list; else one workgroup per
   // (sequence, KV head, split) slot. Same partials either way.
-  const unsigned cus = device_cus();
   const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(cus, items));
   if (cus > 0 && k::attn_ragged_stream_fits(batch, s_max, grid))
     k::attn_ragged_stream_kernel<256><<<grid, 256, 0, as_stream(stream)>>>(p);
@@ -468,12 +472,13 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
   const uint64_t items = uint64_t{batch} * k::attn::kKvHeads * s_max;
   if (items > 0x7FFFFFFFull)
     return fail("miso_attn_decode_paged", "batch x splits too large for one grid");
+  const unsigned cus = device_cus();
+  const unsigned chunk = k::attn_ragged_chunk(batch, max_len, cus);
   const k::AttnPagedParams p{q,      as_half(k_pages), as_half(v_pages), page_table,
                              lens,   part_m,           part_l,           part_o,
                              batch,  s_max,            max_pages,
-                             static_cast<unsigned>(__builtin_ctz(page_size))};
+                             static_cast<unsigned>(__builtin_ctz(page_size)), chunk};
   // As the ragged decode: one streaming workgroup per CU where the batch fits its item list.
-  const unsigned cus = device_cus();
   const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(cus, items));
   if (cus > 0 && k::attn_ragged_stream_fits(batch, s_max, grid))
     k::attn_paged_stream_kernel<256><<<grid, 256, 0, as_stream(stream)>>>(p);
@@ -486,7 +491,7 @@ int miso_attn_decode_paged(const float* q, const float* gate, const uint16_t* k_
   // The merge reads only the partials, lens, gate and core of the ragged parameters.
   const k::AttnRaggedParams r{q,     gate,   nullptr, nullptr, nullptr,
                               lens,  core,   part_m,  part_l,  part_o,
-                              batch, s_max,  k::attn_paged_len_cap(max_pages, p.log2_page)};
+                              batch, s_max,  k::attn_paged_len_cap(max_pages, p.log2_page), chunk};
   const unsigned tiles = batch * k::attn::kQHeads * (k::attn::kDim / 64);
   k::attn_ragged_combine_kernel<<<tiles, 64, 0, as_stream(stream)>>>(r);
   return launched("miso_attn_decode_paged(combine)");

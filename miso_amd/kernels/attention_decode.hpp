@@ -2237,8 +2237,22 @@ attn_decode_fused_kernel(AttnDecodeFusedParams p) {
 // ------------------------------------------------------------------------------------------------
 
 // Keys per split for the batched path: large enough that the partials stay a few percent of the
-// KV bytes, small enough that a batch of long and short sequences balances across CUs.
+// KV bytes, small enough that a batch of long and short sequences balances across CUs. The partial
+// buffers are sized for this chunk; a launch may split at kAttnRaggedWideChunk instead
+// (attn_ragged_chunk), which needs fewer partials.
 constexpr unsigned kAttnRaggedChunk = 512;
+constexpr unsigned kAttnRaggedWideChunk = 1024;
+
+// The chunk a launch splits at: the wide one when even that gives at least four items per CU
+// for a batch of `batch` sequences of up to max_len keys (fewer per-item merges in the streaming
+// kernel; measured on C5, 64 sequences: 211 us against 230 us), else kAttnRaggedChunk so that
+// small batches still fill the CUs. cus = 0 (unknown) keeps kAttnRaggedChunk.
+__host__ __device__ constexpr unsigned attn_ragged_chunk(unsigned batch, unsigned max_len,
+                                                        unsigned cus) {
+  const unsigned long long items = 2ull * batch *
+                                   ((max_len + kAttnRaggedWideChunk - 1) / kAttnRaggedWideChunk);
+  return cus > 0 && items >= 4ull * cus ? kAttnRaggedWideChunk : kAttnRaggedChunk;
+}
 
 __host__ __device__ constexpr unsigned attn_ragged_splits(unsigned max_len) {
   const unsigned n = (max_len + kAttnRaggedChunk - 1) / kAttnRaggedChunk;
@@ -2259,11 +2273,13 @@ struct AttnRaggedParams {
   unsigned batch, s_max;
   unsigned len_cap;  // keys a sequence can hold (the paged layout's pages x page size); lens
                      // past it count as len_cap. ~0u for the contiguous ragged layout.
+  unsigned chunk;    // keys per split (attn_ragged_chunk), the same in the split and the merge
 };
 
-// Splits of a sequence of len keys: one per kAttnRaggedChunk keys, at most s_max.
-__host__ __device__ inline unsigned attn_ragged_seq_splits(unsigned len, unsigned s_max) {
-  const unsigned n = (len + kAttnRaggedChunk - 1) / kAttnRaggedChunk;
+// Splits of a sequence of len keys: one per `chunk` keys, at most s_max.
+__host__ __device__ inline unsigned attn_ragged_seq_splits(unsigned len, unsigned s_max,
+                                                           unsigned chunk) {
+  const unsigned n = (len + chunk - 1) / chunk;
   return n < s_max ? n : s_max;
 }
 
@@ -2278,7 +2294,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
   if (seq >= p.batch)
     return;
   const unsigned len = p.lens[seq];
-  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
+  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max, p.chunk);
   if (split >= n_splits)
     return;
   const std::size_t kv0 = p.kv_offsets[seq] + std::size_t{kvh} * len * attn::kDim;
@@ -2330,7 +2346,7 @@ struct StreamBatch {
   float* part_l;
   float* part_o;
   const uint32_t* lens;
-  unsigned batch, s_max, len_cap;
+  unsigned batch, s_max, len_cap, chunk;
 };
 
 __device__ __attribute__((always_inline)) inline unsigned lane_value(unsigned v, unsigned j) {
@@ -2444,7 +2460,7 @@ __device__ __attribute__((always_inline)) inline void stream_items(const StreamB
       unsigned cnt = 0;
       if (s_ < p.batch) {
         const unsigned len = p.lens[s_] < p.len_cap ? p.lens[s_] : p.len_cap;
-        cnt = attn::kKvHeads * attn_ragged_seq_splits(len, p.s_max);
+        cnt = attn::kKvHeads * attn_ragged_seq_splits(len, p.s_max, p.chunk);
       }
       unsigned incl = cnt;
 #pragma unroll
@@ -2648,7 +2664,7 @@ attn_ragged_stream_kernel(AttnRaggedParams p) {
   decode_detail::RaggedStreamSource src{p.k_cache, p.v_cache, p.kv_offsets};
   decode_detail::stream_items(
       decode_detail::StreamBatch{p.q, p.part_m, p.part_l, p.part_o, p.lens, p.batch, p.s_max,
-                                 p.len_cap},
+                                 p.len_cap, p.chunk},
       src, sh);
 }
 
@@ -2664,7 +2680,7 @@ __global__ void __launch_bounds__(64) attn_ragged_combine_kernel(AttnRaggedParam
     return;
   const std::size_t out = (std::size_t{seq} * attn::kQHeads + h) * attn::kDim + d;
   const unsigned len = p.lens[seq] < p.len_cap ? p.lens[seq] : p.len_cap;
-  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
+  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max, p.chunk);
   if (n_splits == 0) {
     p.core[out] = 0.0f;
     return;
@@ -2696,6 +2712,7 @@ struct AttnPagedParams {
   float* part_l;
   float* part_o;                 // [batch][2][s_max][8][256]
   unsigned batch, s_max, max_pages, log2_page;
+  unsigned chunk;                // keys per split (attn_ragged_chunk)
 };
 
 // Keys a paged sequence can hold: a longer lens[s] attends to its first max_pages pages only
@@ -2717,7 +2734,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 
     return;
   const unsigned cap = attn_paged_len_cap(p.max_pages, p.log2_page);
   const unsigned len = p.lens[seq] < cap ? p.lens[seq] : cap;
-  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max);
+  const unsigned n_splits = attn_ragged_seq_splits(len, p.s_max, p.chunk);
   if (split >= n_splits)
     return;
   const decode_detail::PagedRows rows{
@@ -2745,7 +2762,7 @@ attn_paged_stream_kernel(AttnPagedParams p) {
                                        p.log2_page};
   decode_detail::stream_items(
       decode_detail::StreamBatch{p.q, p.part_m, p.part_l, p.part_o, p.lens, p.batch, p.s_max,
-                                 attn_paged_len_cap(p.max_pages, p.log2_page)},
+                                 attn_paged_len_cap(p.max_pages, p.log2_page), p.chunk},
       src, sh);
 }
 

@@ -100,7 +100,8 @@ def test_ragged_wide_batch_fallback(O, attn, torch_mod):
 def test_ragged_stream_equals_split_kernel(O, attn, torch_mod):
     """The streaming kernel and the one-workgroup-per-split kernel compute each item the same
     way: a 600-sequence batch (above the streaming limit of 512) and its first 100 sequences as
-    a batch of their own (streamed) give bit-identical rows."""
+    a batch of their own (streamed) give bit-identical rows. Both run with max_len 6144, so both
+    launches split at the wide chunk."""
     torch = torch_mod
     rng = np.random.default_rng(602)
     lens = rng.integers(0, 1100, 600).astype(np.uint32)
@@ -110,10 +111,20 @@ def test_ragged_stream_equals_split_kernel(O, attn, torch_mod):
     offs, d_lens = to_dev(torch, r["offsets"]), to_dev(torch, r["lens"])
     out = {}
     for batch in (600, 100):
-        sc = attn.RaggedScratch(batch, int(lens[:batch].max()))
+        assert attn.ragged_chunk(batch, 6144) == 1024
+        sc = attn.RaggedScratch(batch, 6144)
         core = torch.full((batch * H * D,), -9123.5, device="cuda")
         attn.attn_decode_ragged(q[:batch * H * D], gate[:batch * H * D], k, v, offs[:batch],
                                 d_lens[:batch], core, sc)
         torch.cuda.synchronize()
         out[batch] = to_host(core).reshape(batch, H, D)
     assert np.array_equal(out[600][:100].view(np.uint32), out[100].view(np.uint32))
+
+
+def test_ragged_chunk_policy(attn, torch_mod):
+    """Spans of 1024 keys once they still give four per CU, else 512: C5 (64 sequences up to
+    16384 keys) takes the wide chunk, a single 64k-key sequence or a small batch the narrow one."""
+    cus = torch_mod.cuda.get_device_properties(0).multi_processor_count
+    assert attn.ragged_chunk(64, 16384) == (1024 if 2 * 64 * 16 >= 4 * cus else 512)
+    assert attn.ragged_chunk(1, 65536) == 512
+    assert attn.ragged_chunk(9, 2049) == 512
