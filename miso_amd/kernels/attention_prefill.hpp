@@ -462,12 +462,13 @@ __device__ __attribute__((always_inline)) inline void scores2(const Rows2& rw, u
 
 // One tile ti of a wave, software-pipelined over two groups of MFMAs (scheduling barriers keep
 // the interleave):
-//   A: S^T(ti + 1) of both blocks (32 MFMAs; each K operand read once for two) with O +=
-//      V^T(ti) P^T(ti) for key step 0 (16 MFMAs: 8 dimension blocks x 2 row blocks, each V^T
-//      operand read once for two), one P V MFMA after every second S MFMA, and the copy of tile
-//      ti + 2 (kCopy) spread one instruction per two k-steps;
-//   B: O += V^T(ti) P^T(ti) for key step 1 (16 MFMAs) with the decisions and numerators of tile
-//      ti + 1 for both blocks (kNext; masked when kMaskNext) into `cur`.
+//   A: S^T(ti + 1) of both blocks (16 kBlocks MFMAs; each K operand read once for all blocks)
+//      and the copy of tile ti + 2 (do_copy) spread one instruction per two k-steps;
+//   B: O += V^T(ti) P^T(ti) (16 kBlocks MFMAs: 8 dimension blocks x 2 key steps per block, each
+//      V^T operand read once for all blocks) with the decisions and numerators of tile ti + 1
+//      (kNext; masked when kMaskNext) into `cur`, their VALU work spread between the MFMAs.
+// The softmax VALU work needs all of S^T(ti + 1), so it can only overlap the P V MFMAs; with all
+// of them in group B it has 16 kBlocks MFMAs to hide behind instead of half of them.
 // A block whose m moved for tile ti + 1 has its O (holding every tile <= ti) rescaled at the end.
 // kb: K operand address in slot 0, k_off the byte offset of tile ti + 1's slot; vb[c] + v_off:
 // the V^T transpose-read address of 32-dim block c (rows 0-7 of key step 0) in tile ti's slot.
@@ -527,7 +528,6 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
     const unsigned b = i % 8, step = i / 8;
     pv_mfma(o[c][b], va[i % kAhead], cur.p[c][step]);
   };
-  half8_t next[2][2];
   auto copy = [&](unsigned st) __attribute__((always_inline)) {
     if (do_copy) {  // uniform
       switch (st) {
@@ -544,7 +544,7 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
     }
   };
 
-  // Group A.
+  // Group A: the score MFMAs, the first V^T operands read ahead for group B.
   kread(0);
   kread(1);
 #pragma unroll
@@ -554,34 +554,123 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
   for (unsigned st = 0; st < 16; ++st) {
     kread(st + 2);
     smma(st);
-    if (st % 2 == 1) {
-      const unsigned i = st / 2;  // dimension block i of key step 0
-#pragma unroll
-      for (int c = 0; c < kBlocks; ++c)
-        pv(i, c);
-      vread(i + kAhead);
-    }
     copy(st);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Group B.
+
+  // Group B: the decisions of tile ti + 1 (the arithmetic of decide_block, in the same order),
+  // spread over the slots so the VALU work issues between the MFMAs. Per block c: X (mask,
+  // first half of the row max) and Y (row max, wave-wide move decision, new reference max) in
+  // the first slots; then for each numerator pair k (pairs alternate between the blocks) SE
+  // (two differences and their 2^x) in one slot and CD (f16 pair and its share of the row sum)
+  // in the next, so no slot waits on a result of its own; F (operands, l) at the end. Each
+  // result is pinned by an empty volatile asm where it is made: the numerators are used only at
+  // the end of the step, and the compiler would otherwise sink their arithmetic below the last
+  // MFMA, where it runs with the matrix unit idle.
   bool moved[2] = {false, false};
   float corr[2] = {1.0f, 1.0f};
+  float x[kBlocks][16], run[kBlocks], lsum[kBlocks], ex[kBlocks][16];
+  cdna4::half2_t e2[kBlocks][8];
+  half8_t next[2][2];
+  const cdna4::half2_t ones{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  auto stage_x = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-  for (unsigned j = 0; j < 8; ++j) {
+    for (unsigned r = 0; r < 16; ++r) {
+      x[c][r] = s[c][r];
+      if (kMaskNext) {
+        const unsigned key = k0_next + 8 * (r / 4) + 4 * hi + (r % 4);
+        x[c][r] = key <= lim[c] ? x[c][r] : -__builtin_inff();
+      }
+    }
+    run[c] = max3(x[c][0], x[c][1], x[c][2]);
+    run[c] = max3(run[c], x[c][3], x[c][4]);
+    run[c] = max3(run[c], x[c][5], x[c][6]);
+    run[c] = max3(run[c], x[c][7], x[c][8]);
+    asm volatile("" : "+v"(run[c]));
+  };
+  auto stage_y = [&](int c) __attribute__((always_inline)) {
+    run[c] = max3(run[c], x[c][9], x[c][10]);
+    run[c] = max3(run[c], x[c][11], x[c][12]);
+    run[c] = max3(run[c], x[c][13], x[c][14]);
+    const float mx = cdna4::max_xor32(fmaxf(run[c], x[c][15]));
+    moved[c] = __builtin_amdgcn_ballot_w64(mx > rw.m[c] + kRescaleSlack) != 0;
+    if (moved[c]) {
+      const float mn = fmaxf(rw.m[c], mx);
+      corr[c] = __builtin_amdgcn_exp2f(rw.m[c] - mn);  // 0 on the first tile (m = -inf)
+      rw.m[c] = mn;
+    }
+    asm volatile("" : "+v"(rw.m[c]));
+  };
+  // Numerator pair k: block k % kBlocks, pair j = k / kBlocks (keys 2 j, 2 j + 1 of the lane).
+  auto stage_se = [&](unsigned k, unsigned half) __attribute__((always_inline)) {
+    const int c = static_cast<int>(k % kBlocks);
+    const unsigned r = 2 * (k / kBlocks) + half;
+    ex[c][r] = __builtin_amdgcn_exp2f(x[c][r] - rw.m[c]);
+    asm volatile("" : "+v"(ex[c][r]));
+  };
+  auto stage_cd = [&](unsigned k) __attribute__((always_inline)) {
+    const int c = static_cast<int>(k % kBlocks);
+    const unsigned j = k / kBlocks;
+    e2[c][j] = cdna4::half2_t{static_cast<_Float16>(ex[c][2 * j]),
+                              static_cast<_Float16>(ex[c][2 * j + 1])};
+    lsum[c] = __builtin_amdgcn_fdot2(e2[c][j], ones, j == 0 ? 0.0f : lsum[c], false);
+    asm volatile("" : "+v"(e2[c][j]), "+v"(lsum[c]));
+  };
+  auto stage_f = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < kBlocks; ++c)
-      pv(8 + j, c);
-    vread(8 + j + kAhead);
-    if (kNext && j == 1)
-      drain_pv();  // the last score MFMA is 6 MFMAs back; its result is read next
-    if (kNext && j == 1)
-      corr[0] = decide_block<kMaskNext>(s[0], rw.m[0], rw.l[0], next[0], k0_next, lim[0], hi,
-                                        moved[0]);
-    if constexpr (kBlocks == 2)
-      if (kNext && j == 5)
-        corr[1] = decide_block<kMaskNext>(s[1], rw.m[1], rw.l[1], next[1], k0_next, lim[1], hi,
-                                          moved[1]);
+    for (int h = 0; h < 2; ++h)
+      next[c][h] = half8_t{e2[c][4 * h][0],     e2[c][4 * h][1],     e2[c][4 * h + 1][0],
+                           e2[c][4 * h + 1][1], e2[c][4 * h + 2][0], e2[c][4 * h + 2][1],
+                           e2[c][4 * h + 3][0], e2[c][4 * h + 3][1]};
+    rw.l[c] = rw.l[c] * corr[c] + lsum[c];
+  };
+  // Work items in order: X of each block, Y of each block, then per numerator pair k its two
+  // halves of SE (one difference and its 2^x each) with the CD of pair k - 1 after them, then
+  // the last CD and F. Item n runs in slot n kSlots / kItems: an even spread, and a pair's CD
+  // lands about two slots after its SE, so no slot waits on a result it made itself.
+  constexpr unsigned kSlots = 16 * kBlocks;  // one P V MFMA each
+  constexpr unsigned kPairs = 8 * kBlocks;
+  constexpr unsigned kBase = 2 * kBlocks;
+  constexpr unsigned kItems = kBase + 3 * kPairs + 2;
+  auto item = [&](unsigned n) __attribute__((always_inline)) {
+    if (n < kBlocks) {
+      stage_x(static_cast<int>(n));
+    } else if (n < kBase) {
+      stage_y(static_cast<int>(n - kBlocks));
+    } else if (n < kBase + 3 * kPairs) {
+      const unsigned k = (n - kBase) / 3, part = (n - kBase) % 3;
+      if (part < 2)
+        stage_se(k, part);
+      else if (k > 0)
+        stage_cd(k - 1);
+    } else if (n == kBase + 3 * kPairs) {
+      stage_cd(kPairs - 1);
+    } else {
+#pragma unroll
+      for (int b = 0; b < kBlocks; ++b)
+        stage_f(b);
+    }
+  };
+#pragma unroll
+  for (unsigned q = 0; q < kSlots; ++q) {
+    // P V MFMAs in issue order: operand i (dimension block i % 8 of key step i / 8) for blocks
+    // 0 .. kBlocks - 1, each operand read once for all blocks.
+    const unsigned i = q / kBlocks;
+    const int c = static_cast<int>(q % kBlocks);
+    pv(i, c);
+    if (c == kBlocks - 1)
+      vread(i + kAhead);
+    if (kNext) {
+      if (q == 0) {
+        // The last score MFMA is at least one MFMA back; its results are read next.
+        drain_scores(s[0]);
+        if constexpr (kBlocks == 2)
+          asm volatile("" : "+v"(s[1]));
+      }
+#pragma unroll
+      for (unsigned n = (q * kItems + kSlots - 1) / kSlots; n < ((q + 1) * kItems + kSlots - 1) / kSlots; ++n)
+        item(n);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   drain_pv();
@@ -605,11 +694,12 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
 //
 // K/V tiles of 32 keys stream into a 3-stage LDS ring by direct global->LDS loads (each wave
 // copies 8 rows of each, one instruction at a time between its MFMAs); one barrier per tile. Per
-// tile i (tile_step2): O^T += V^T P^T(i) for every block (16 MFMAs per block, V^T from
-// ds_read_b64_tr_b16, each operand feeding every block) and S^T(i + 1) = K Q^T (16 MFMAs per
-// block; the first block's Q^T resident in VGPRs as f16 pre-scaled by log2(e)/16, the second's in
-// LDS), whose decisions and numerators close the step. Keys past a row's causal limit are masked
-// only in the diagonal tiles of a wave; the gate and 1/l are applied at the store.
+// tile i (tile_step2): S^T(i + 1) = K Q^T (16 MFMAs per block; the first block's Q^T resident in
+// VGPRs as f16 pre-scaled by log2(e)/16, the second's in LDS), then O^T += V^T P^T(i) for every
+// block (16 MFMAs per block, V^T from ds_read_b64_tr_b16, each operand feeding every block) with
+// the decisions and numerators of tile i + 1 issued between those MFMAs. Keys past a row's causal
+// limit are masked only in the diagonal tiles of a wave; the gate and 1/l are applied at the
+// store.
 namespace prefill_detail {
 
 // A workgroup's run over one token block: tiles [tb, te) of its keys; `part` says the tiles are
