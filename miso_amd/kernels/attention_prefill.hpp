@@ -559,14 +559,13 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
   }
 
   // Group B: the decisions of tile ti + 1 (the arithmetic of decide_block, in the same order),
-  // spread over the slots so the VALU work issues between the MFMAs. Per block c: X (mask,
-  // first half of the row max) and Y (row max, wave-wide move decision, new reference max) in
-  // the first slots; then for each numerator pair k (pairs alternate between the blocks) SE
-  // (two differences and their 2^x) in one slot and CD (f16 pair and its share of the row sum)
-  // in the next, so no slot waits on a result of its own; F (operands, l) at the end. Each
-  // result is pinned by an empty volatile asm where it is made: the numerators are used only at
-  // the end of the step, and the compiler would otherwise sink their arithmetic below the last
-  // MFMA, where it runs with the matrix unit idle.
+  // cut into items spread over the slots so the VALU work issues between the MFMAs. Per block c:
+  // X (mask, first half of the row max) and Y (row max, wave-wide move decision, new reference
+  // max); per numerator pair k (pairs alternate between the blocks) two SE halves (a difference
+  // and its 2^x each) and CD (the f16 pair and its share of the row sum); F (operands, l) at the
+  // end. Each result is pinned by an empty volatile asm where it is made: the numerators are
+  // used only at the end of the step, and the compiler would otherwise sink their arithmetic
+  // below the last MFMA, where it runs with the matrix unit idle.
   bool moved[2] = {false, false};
   float corr[2] = {1.0f, 1.0f};
   float x[kBlocks][16], run[kBlocks], lsum[kBlocks], ex[kBlocks][16];
@@ -667,8 +666,10 @@ __device__ __attribute__((always_inline)) inline void tile_step2(
         if constexpr (kBlocks == 2)
           asm volatile("" : "+v"(s[1]));
       }
+      const unsigned first = (q * kItems + kSlots - 1) / kSlots;
+      const unsigned end = ((q + 1) * kItems + kSlots - 1) / kSlots;
 #pragma unroll
-      for (unsigned n = (q * kItems + kSlots - 1) / kSlots; n < ((q + 1) * kItems + kSlots - 1) / kSlots; ++n)
+      for (unsigned n = first; n < end; ++n)
         item(n);
     }
     __builtin_amdgcn_sched_barrier(0);
